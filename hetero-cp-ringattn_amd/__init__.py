@@ -1,0 +1,408 @@
+"""Python bindings of ``libhcp_ring_amd.so`` (the C ABI in ``include/hcp_ring.h``).
+
+The operator names mirror the reference's ring-attention backend
+(``HcpRingAttentionBackend`` in rust/src/model/attention/ring.rs):
+
+* :func:`positioned_local_compact_partial`  ring.rs:538-571 -> ``hcp_ring_block_partial``
+* :func:`positioned_merge_compact_partial`  ring.rs:574-603 -> ``hcp_ring_block_partial``
+  (accumulate=1)
+* :func:`lse_merge`                         merge of ring-step partials -> ``hcp_ring_lse_merge``
+* :func:`decode_local_compact_partial`      ring.rs:515-523 over a paged pool ->
+  ``hcp_paged_decode_partial``
+* :func:`paged_kv_gather` / :func:`paged_kv_scatter`  the vLLM block extract / insert of
+  python/hcp_vllm_block_ring_plugin.py:143-174, 304-337 -> ``hcp_paged_kv_*``
+* :func:`ring_attention_replay`             ring.rs:861-1398 for every domain on one GPU ->
+  ``hcp_ring_prefill_replay`` (``_paged`` variant stages K/V from a block pool)
+
+Tensors are torch CUDA tensors (device memory and streams only; every computation
+runs in the HIP library).  A ``[heads, tokens, head_dim]`` argument may be any strided
+view whose last dimension is contiguous, e.g. ``x.permute(1, 0, 2)`` of a token-major
+``[tokens, heads, head_dim]`` tensor.  Errors raise :class:`HcpRingError` carrying the
+ABI status code and the library's message.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libhcp_ring_amd.so")
+HEADER = os.path.join(HERE, "..", "include", "hcp_ring.h")
+
+DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 1, 2, 3
+
+STATUS_NAMES = {
+    0: "OK", -1: "MISMATCH", -2: "EXCEPTION", -3: "UNKNOWN", -4: "DEVICE", -5: "BACKEND",
+    -6: "INVALID",
+}
+
+
+class HcpRingError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{STATUS_NAMES.get(code, code)}] {message}")
+        self.code = code
+        self.message = message
+
+
+class View(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("head_stride", ctypes.c_int64),
+                ("seq_stride", ctypes.c_int64)]
+
+
+class BlockDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int32), ("num_q_heads", ctypes.c_int32),
+                ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("q_len", ctypes.c_int64), ("kv_len", ctypes.c_int64),
+                ("q_offset", ctypes.c_int64), ("kv_offset", ctypes.c_int64),
+                ("causal", ctypes.c_int32), ("accumulate", ctypes.c_int32),
+                ("scale", ctypes.c_float)]
+
+
+class PagedPool(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("num_blocks", ctypes.c_int64),
+                ("block_size", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
+                ("head_dim", ctypes.c_int32), ("elem_bytes", ctypes.c_int32)]
+
+
+class DecodeDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int32), ("batch", ctypes.c_int32),
+                ("num_q_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
+                ("head_dim", ctypes.c_int32), ("reserved0", ctypes.c_int32),
+                ("t0", ctypes.c_int64), ("t1", ctypes.c_int64),
+                ("table_stride", ctypes.c_int64), ("table_len", ctypes.c_int64),
+                ("scale", ctypes.c_float)]
+
+
+class ReplayDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int32), ("num_q_heads", ctypes.c_int32),
+                ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("num_domains", ctypes.c_int32), ("causal", ctypes.c_int32),
+                ("chunk_lens", ctypes.POINTER(ctypes.c_int64)), ("scale", ctypes.c_float)]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library; raises if it was not built (there is no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HcpRingError(-5, f"{LIB_PATH} is missing; run hetero-cp-ringattn_amd/build.py")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+    sig = {
+        "hcp_ring_last_error": ([], ctypes.c_char_p),
+        "hcp_ring_abi_version": ([], ctypes.c_int),
+        "hcp_ring_device_count": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+        "hcp_ring_fetch_device_errors": ([vp, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+        "hcp_ring_block_partial": ([ctypes.POINTER(BlockDesc), View, View, View, vp, vp, vp],
+                                   ctypes.c_int),
+        "hcp_ring_lse_merge": ([i32, ctypes.POINTER(vp), ctypes.POINTER(vp), i32, i64, i32, i32,
+                                View, vp, vp], ctypes.c_int),
+        "hcp_paged_kv_gather": ([ctypes.POINTER(PagedPool), vp, i64, i64, i64, i64, View, View,
+                                 vp], ctypes.c_int),
+        "hcp_paged_kv_scatter": ([ctypes.POINTER(PagedPool), vp, i64, i64, i64, i64, View, View,
+                                  i32, vp], ctypes.c_int),
+        "hcp_paged_decode_workspace_size": ([ctypes.POINTER(DecodeDesc),
+                                             ctypes.POINTER(PagedPool)], ctypes.c_size_t),
+        "hcp_paged_decode_partial": ([ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedPool), View,
+                                      vp, vp, vp, vp, vp, ctypes.c_size_t, vp], ctypes.c_int),
+        "hcp_ring_replay_workspace_size": ([ctypes.POINTER(ReplayDesc), i32], ctypes.c_size_t),
+        "hcp_ring_prefill_replay": ([ctypes.POINTER(ReplayDesc), View, View, View, View, vp, vp,
+                                     ctypes.c_size_t, vp], ctypes.c_int),
+        "hcp_ring_prefill_replay_paged": ([ctypes.POINTER(ReplayDesc), View,
+                                           ctypes.POINTER(PagedPool), vp, i64, View, vp, vp,
+                                           ctypes.c_size_t, vp], ctypes.c_int),
+        "hcp_synth_normals": ([ctypes.c_uint64, i64, i64, i32, vp, vp], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def header_functions() -> list[str]:
+    """Names of the functions declared in include/hcp_ring.h."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\*?\s+\**(hcp_[a-z_0-9]+)\s*\(",
+                                 text, flags=re.M)))
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        msg = lib().hcp_ring_last_error()
+        raise HcpRingError(rc, msg.decode() if msg else "")
+
+
+def last_error() -> str:
+    m = lib().hcp_ring_last_error()
+    return m.decode() if m else ""
+
+
+# ---------------------------------------------------------------------------------
+# torch plumbing
+# ---------------------------------------------------------------------------------
+def _torch():
+    import torch
+    return torch
+
+
+def dtype_code(t) -> int:
+    torch = _torch()
+    return {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16, torch.float32: DTYPE_F32}[t]
+
+
+def _stream(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def view(t) -> View:
+    """[heads, tokens, head_dim] tensor (last dim contiguous) -> hcp_ring_view."""
+    if t.dim() != 3:
+        raise ValueError("expected a [heads, tokens, head_dim] tensor")
+    if t.stride(2) != 1 and t.shape[2] > 1:
+        raise ValueError("head_dim must be the contiguous dimension")
+    return View(t.data_ptr(), t.stride(0), t.stride(1))
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+# ---------------------------------------------------------------------------------
+# (1) block partial
+# ---------------------------------------------------------------------------------
+def block_partial(q, k, v, q_offset: int, kv_offset: int, causal: bool = True,
+                  scale: float | None = None, o=None, lse=None, accumulate: bool = False,
+                  stream=None):
+    """One ring step: q [Hq, Lq, D], k/v [Hkv, Lk, D] -> (o [Hq,Lq,D] fp32, lse [Hq,Lq] fp32)."""
+    torch = _torch()
+    hq, lq, d = q.shape
+    hkv, lk, _ = k.shape
+    if o is None:
+        o = torch.empty((hq, lq, d), dtype=torch.float32, device=q.device)
+    if lse is None:
+        lse = torch.empty((hq, lq), dtype=torch.float32, device=q.device)
+    desc = BlockDesc(dtype_code(q.dtype), hq, hkv, d, lq, lk, q_offset, kv_offset,
+                     1 if causal else 0, 1 if accumulate else 0,
+                     scale if scale is not None else 1.0 / math.sqrt(d))
+    _check(lib().hcp_ring_block_partial(ctypes.byref(desc), view(q), view(k), view(v), _ptr(o),
+                                        _ptr(lse), _stream(stream)))
+    return o, lse
+
+
+def positioned_local_compact_partial(q, q_offset, k, v, kv_offset, scale=None, stream=None):
+    """ring.rs:538-571 on the GPU: causal partial over one source -> (o fp32, lse fp32)."""
+    return block_partial(q, k, v, q_offset, kv_offset, True, scale, stream=stream)
+
+
+def positioned_merge_compact_partial(q, q_offset, o, lse, k, v, kv_offset, scale=None,
+                                     stream=None):
+    """ring.rs:574-603 on the GPU: merge (o, lse) with one more causal source (new tensors)."""
+    o2, l2 = o.clone(), lse.clone()
+    return block_partial(q, k, v, q_offset, kv_offset, True, scale, o=o2, lse=l2,
+                         accumulate=True, stream=stream)
+
+
+# ---------------------------------------------------------------------------------
+# (2) LSE merge
+# ---------------------------------------------------------------------------------
+def lse_merge(o_parts, lse_parts, out_dtype=None, out=None, lse_out=None, stream=None):
+    """Merge partials (each o [H,L,D] fp32 contiguous, lse [H,L] fp32)."""
+    torch = _torch()
+    h, l, d = o_parts[0].shape
+    if out is None:
+        out = torch.empty((h, l, d), dtype=out_dtype or torch.bfloat16, device=o_parts[0].device)
+    if lse_out is None:
+        lse_out = torch.empty((h, l), dtype=torch.float32, device=o_parts[0].device)
+    n = len(o_parts)
+    op = (ctypes.c_void_p * n)(*[p.data_ptr() for p in o_parts])
+    lp = (ctypes.c_void_p * n)(*[p.data_ptr() for p in lse_parts])
+    _check(lib().hcp_ring_lse_merge(n, op, lp, h, l, d, dtype_code(out.dtype), view(out),
+                                    _ptr(lse_out), _stream(stream)))
+    return out, lse_out
+
+
+# ---------------------------------------------------------------------------------
+# (3) paged KV staging
+# ---------------------------------------------------------------------------------
+def paged_pool(pool) -> PagedPool:
+    """pool tensor [2, num_blocks, block_size, Hkv, D] -> hcp_paged_pool."""
+    if pool.dim() != 5 or pool.shape[0] != 2 or not pool.is_contiguous():
+        raise ValueError("pool must be a contiguous [2, num_blocks, block_size, Hkv, D] tensor")
+    return PagedPool(pool.data_ptr(), pool.shape[1], pool.shape[2], pool.shape[3], pool.shape[4],
+                     pool.element_size())
+
+
+def paged_kv_gather(pool, block_table, table_seq_offset, t0, t1, k_out=None, v_out=None,
+                    stream=None):
+    torch = _torch()
+    _, nb, bs, hkv, d = pool.shape
+    if k_out is None:
+        k_out = torch.empty((hkv, t1 - t0, d), dtype=pool.dtype, device=pool.device)
+        v_out = torch.empty((hkv, t1 - t0, d), dtype=pool.dtype, device=pool.device)
+    pp = paged_pool(pool)
+    _check(lib().hcp_paged_kv_gather(ctypes.byref(pp), _ptr(block_table), block_table.numel(),
+                                     table_seq_offset, t0, t1, view(k_out), view(v_out),
+                                     _stream(stream)))
+    return k_out, v_out
+
+
+def paged_kv_scatter(pool, block_table, table_seq_offset, t0, t1, k_in, v_in, zero_tail=True,
+                     stream=None):
+    pp = paged_pool(pool)
+    _check(lib().hcp_paged_kv_scatter(ctypes.byref(pp), _ptr(block_table), block_table.numel(),
+                                      table_seq_offset, t0, t1, view(k_in), view(v_in),
+                                      1 if zero_tail else 0, _stream(stream)))
+
+
+def fetch_device_errors(stream=None) -> int:
+    flags = ctypes.c_int(0)
+    _check(lib().hcp_ring_fetch_device_errors(_stream(stream), ctypes.byref(flags)))
+    return flags.value
+
+
+# ---------------------------------------------------------------------------------
+# (4) paged decode
+# ---------------------------------------------------------------------------------
+def decode_desc(q, pool, block_tables, t0, t1, scale=None) -> DecodeDesc:
+    b, hq, d = q.shape
+    return DecodeDesc(dtype_code(q.dtype), b, hq, pool.shape[3], d, 0, t0, t1,
+                      block_tables.stride(0), block_tables.shape[1],
+                      scale if scale is not None else 1.0 / math.sqrt(d))
+
+
+def decode_workspace_size(q, pool, block_tables, t0, t1) -> int:
+    desc = decode_desc(q, pool, block_tables, t0, t1)
+    pp = paged_pool(pool)
+    return lib().hcp_paged_decode_workspace_size(ctypes.byref(desc), ctypes.byref(pp))
+
+
+def decode_local_compact_partial(q, pool, block_tables, t0, t1, seq_lens=None, scale=None,
+                                 workspace=None, o=None, lse=None, stream=None):
+    """ring.rs:515-523 / 625-639 for a batch: q [B, Hq, D] over tokens [t0, t1) of each
+    sequence's paged KV -> (o [B,Hq,D] fp32, lse [B,Hq] fp32)."""
+    torch = _torch()
+    b, hq, d = q.shape
+    desc = decode_desc(q, pool, block_tables, t0, t1, scale)
+    pp = paged_pool(pool)
+    need = lib().hcp_paged_decode_workspace_size(ctypes.byref(desc), ctypes.byref(pp))
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    if o is None:
+        o = torch.empty((b, hq, d), dtype=torch.float32, device=q.device)
+        lse = torch.empty((b, hq), dtype=torch.float32, device=q.device)
+    qv = View(q.data_ptr(), q.stride(1), q.stride(0))
+    _check(lib().hcp_paged_decode_partial(ctypes.byref(desc), ctypes.byref(pp), qv,
+                                          _ptr(block_tables), _ptr(seq_lens), _ptr(o), _ptr(lse),
+                                          _ptr(workspace), workspace.numel(), _stream(stream)))
+    return o, lse
+
+
+# ---------------------------------------------------------------------------------
+# (5) ring replay
+# ---------------------------------------------------------------------------------
+def replay_desc(dtype, hq, hkv, d, chunks, causal=True, scale=None):
+    arr = (ctypes.c_int64 * len(chunks))(*chunks)
+    desc = ReplayDesc(dtype_code(dtype), hq, hkv, d, len(chunks), 1 if causal else 0, arr,
+                      scale if scale is not None else 1.0 / math.sqrt(d))
+    return desc, arr
+
+
+def replay_workspace_size(dtype, hq, hkv, d, chunks, causal=True, paged=False) -> int:
+    desc, _arr = replay_desc(dtype, hq, hkv, d, chunks, causal)
+    return lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 1 if paged else 0)
+
+
+def ring_attention_replay(q, k, v, chunks, causal=True, scale=None, out=None, lse_out=None,
+                          workspace=None, stream=None):
+    """Every domain's ring on one GPU.  q [Hq, S, D], k/v [Hkv, S, D] (strided views ok)
+    -> (out [Hq, S, D] in q's dtype, lse [Hq, S] fp32)."""
+    torch = _torch()
+    hq, s, d = q.shape
+    hkv = k.shape[0]
+    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale)
+    need = lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 0)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    if out is None:
+        out = torch.empty((hq, s, d), dtype=q.dtype, device=q.device)
+    if lse_out is None:
+        lse_out = torch.empty((hq, s), dtype=torch.float32, device=q.device)
+    _check(lib().hcp_ring_prefill_replay(ctypes.byref(desc), view(q), view(k), view(v), view(out),
+                                         _ptr(lse_out), _ptr(workspace), workspace.numel(),
+                                         _stream(stream)))
+    del arr
+    return out, lse_out
+
+
+def ring_attention_replay_paged(q, pool, block_table, chunks, causal=True, scale=None, out=None,
+                                lse_out=None, workspace=None, stream=None):
+    """As :func:`ring_attention_replay`, K/V gathered per ring step from a paged pool."""
+    torch = _torch()
+    hq, s, d = q.shape
+    hkv = pool.shape[3]
+    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale)
+    need = lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 1)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    if out is None:
+        out = torch.empty((hq, s, d), dtype=q.dtype, device=q.device)
+    if lse_out is None:
+        lse_out = torch.empty((hq, s), dtype=torch.float32, device=q.device)
+    pp = paged_pool(pool)
+    _check(lib().hcp_ring_prefill_replay_paged(ctypes.byref(desc), view(q), ctypes.byref(pp),
+                                               _ptr(block_table), block_table.numel(), view(out),
+                                               _ptr(lse_out), _ptr(workspace), workspace.numel(),
+                                               _stream(stream)))
+    del arr
+    return out, lse_out
+
+
+# ---------------------------------------------------------------------------------
+# synthetic inputs and host helpers
+# ---------------------------------------------------------------------------------
+def synth_normals(seed: int, offset: int, count: int, out, stream=None):
+    """Fill ``out`` (contiguous, F32/BF16/F16) with normals offset..offset+count-1."""
+    _check(lib().hcp_synth_normals(ctypes.c_uint64(seed), offset, count, dtype_code(out.dtype),
+                                   _ptr(out), _stream(stream)))
+    return out
+
+
+def vanilla_offsets(chunks, seq_len: int | None = None) -> list[int]:
+    """Global start of each domain's contiguous chunk (strategy.rs:53-63).
+
+    Raises ValueError when the chunks do not sum to ``seq_len`` (the InvalidChunkSum of
+    rust/src/error.rs:15-16, rust/src/smoke/reference_algo.rs:92-116) or a chunk is empty.
+    """
+    if any(c <= 0 for c in chunks):
+        raise ValueError("every chunk must be non-empty")
+    if seq_len is not None and sum(chunks) != seq_len:
+        raise ValueError(f"invalid chunk sum: actual {sum(chunks)}, expected {seq_len}")
+    out, acc = [], 0
+    for c in chunks:
+        out.append(acc)
+        acc += c
+    return out
+
+
+def vanilla_assignment(chunks) -> list[int]:
+    """Owner domain of every global position for contiguous chunks (strategy.rs:53-63)."""
+    out = []
+    for d, c in enumerate(chunks):
+        out.extend([d] * c)
+    return out
+
+
+def ring_sources(target: int, num_domains: int) -> list[int]:
+    """Sources visited by ``target`` in ring order: local, then the predecessor chain
+    (ring.rs:1208-1311 with the mock ring of rust/src/model/transport/mock.rs:143-149)."""
+    return [(target - s) % num_domains for s in range(num_domains)]

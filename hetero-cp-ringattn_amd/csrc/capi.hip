@@ -1,0 +1,454 @@
+// extern "C" boundary of the ring-attention path (declared in include/hcp_ring.h).
+//
+// Conventions follow the reference's FFI bridge (src/rust_bridge.cc): int status,
+// caller-owned buffers, every exception caught at the boundary, and a message getter
+// -- here thread-local instead of the bridge's process-global std::string
+// (rust_bridge.cc:19-27,614-644).  The C++ ring-replay driver (the single-GPU
+// counterpart of HcpRingAttentionBackend::ring_attention, ring.rs:861-1398) lives here
+// too; it only enqueues kernels.
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "../../include/hcp_ring.h"
+
+namespace hcp {
+
+
+// Sticky device-side error flags, one copy per device (static device variable).
+__device__ int g_hcp_device_errors;
+
+int* device_error_flags() {
+  static std::mutex mu;
+  static int* ptrs[64] = {};
+  int dev = 0;
+  HCP_HIP(hipGetDevice(&dev));
+  require(dev >= 0 && dev < 64, "device index out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    HCP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_hcp_device_errors)));
+    ptrs[dev] = static_cast<int*>(p);
+  }
+  return ptrs[dev];
+}
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+template <typename F>
+int guarded(const char* fn, F&& body) {
+  try {
+    g_last_error.clear();
+    body();
+    return HCP_RING_OK;
+  } catch (const Error& e) {
+    return fail(e.code, std::string(fn) + ": " + e.what());
+  } catch (const std::exception& e) {
+    return fail(HCP_RING_E_EXCEPTION, std::string(fn) + ": " + e.what());
+  } catch (...) {
+    return fail(HCP_RING_E_UNKNOWN, std::string(fn) + ": unknown exception");
+  }
+}
+
+int elem_size(int dtype) {
+  switch (dtype) {
+    case kF16:
+    case kBF16: return 2;
+    case kF32: return 4;
+    default: throw Error(-6, "unsupported dtype " + std::to_string(dtype));
+  }
+}
+
+void check_view(const hcp_ring_view& v, const char* name, int64_t len) {
+  if (len == 0) return;
+  require(v.data != nullptr, std::string(name) + ": null data pointer");
+  require(v.head_stride >= 0 && v.seq_stride > 0, std::string(name) + ": strides must be positive");
+}
+
+void check_block_desc(const hcp_ring_block_desc* d) {
+  require(d != nullptr, "null descriptor");
+  elem_size(d->dtype);
+  require(d->num_q_heads > 0 && d->num_kv_heads > 0, "head counts must be positive");
+  require(d->num_q_heads % d->num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
+  require(d->head_dim > 0 && d->head_dim <= 256, "head_dim must be in [1, 256]");
+  require(d->q_len >= 0 && d->kv_len >= 0, "lengths must be >= 0");
+  require(d->q_len <= INT32_MAX && d->kv_len <= INT32_MAX, "lengths must fit in int32");
+  require(d->causal == 0 || d->causal == 1, "causal must be 0 or 1");
+  require(d->accumulate == 0 || d->accumulate == 1, "accumulate must be 0 or 1");
+  require(d->scale > 0.f, "scale must be positive");
+}
+
+bool mfma_layout_ok(const hcp_ring_view& v) {
+  return reinterpret_cast<uintptr_t>(v.data) % 16 == 0 && v.head_stride % 8 == 0 && v.seq_stride % 8 == 0;
+}
+
+// The merge writes 4 elements per lane: rows must start on 4-element boundaries.
+void check_out_view(const hcp_ring_view& out, int dtype) {
+  const int es = elem_size(dtype);
+  require(reinterpret_cast<uintptr_t>(out.data) % (4 * es) == 0 && out.head_stride % 4 == 0 &&
+              out.seq_stride % 4 == 0,
+          "out must be aligned to 4 elements with strides multiple of 4");
+}
+
+BlockLaunch make_launch(const hcp_ring_block_desc* d, hcp_ring_view q, hcp_ring_view k, hcp_ring_view v,
+                        float* o, float* lse) {
+  BlockLaunch L;
+  L.dtype = d->dtype;
+  L.q = q.data; L.k = k.data; L.v = v.data;
+  L.q_hs = q.head_stride; L.q_ss = q.seq_stride;
+  L.k_hs = k.head_stride; L.k_ss = k.seq_stride;
+  L.v_hs = v.head_stride; L.v_ss = v.seq_stride;
+  L.o = o; L.lse = lse;
+  L.hq = d->num_q_heads; L.hkv = d->num_kv_heads; L.d = d->head_dim;
+  L.lq = d->q_len; L.lk = d->kv_len;
+  L.q_off = d->q_offset; L.k_off = d->kv_offset;
+  L.causal = d->causal; L.accumulate = d->accumulate;
+  L.scale = d->scale;
+  // The matrix-core kernel reads 16-byte rows; other layouts take the general kernel.
+  L.force_general = !(mfma_layout_ok(q) && mfma_layout_ok(k) && mfma_layout_ok(v));
+  return L;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// ---- ring replay planning ----
+struct ReplayPlan {
+  int n;
+  std::vector<int64_t> len, off;
+  std::vector<std::vector<int>> sources;  // per target, in ring order, non-empty only
+  std::vector<std::vector<size_t>> part_off;  // byte offsets of each (target, source) partial
+  size_t partial_bytes = 0;
+  size_t staging_off = 0;
+  size_t staging_bytes_per_domain = 0;
+  size_t total = 0;
+  int64_t seq = 0;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
+  require(d != nullptr, "null descriptor");
+  require(d->num_domains >= 1 && d->num_domains <= 64, "num_domains must be in [1, 64]");
+  require(d->chunk_lens != nullptr, "null chunk_lens");
+  require(d->num_q_heads > 0 && d->num_kv_heads > 0 && d->num_q_heads % d->num_kv_heads == 0,
+          "bad head counts");
+  require(d->head_dim > 0 && d->head_dim <= 256, "head_dim must be in [1, 256]");
+  require(d->causal == 0 || d->causal == 1, "causal must be 0 or 1");
+  require(d->scale > 0.f, "scale must be positive");
+  const int es = elem_size(d->dtype);
+  ReplayPlan p;
+  p.n = d->num_domains;
+  int64_t acc = 0;
+  int64_t max_len = 0;
+  for (int i = 0; i < p.n; ++i) {
+    const int64_t l = d->chunk_lens[i];
+    require(l >= 1, "every chunk length must be >= 1");
+    p.len.push_back(l);
+    p.off.push_back(acc);
+    acc += l;
+    max_len = std::max(max_len, l);
+  }
+  require(acc <= INT32_MAX, "total sequence length must fit in int32");
+  p.seq = acc;
+  p.sources.resize(p.n);
+  p.part_off.resize(p.n);
+  size_t cur = 0;
+  for (int t = 0; t < p.n; ++t) {
+    for (int s = 0; s < p.n; ++s) {
+      const int src = ((t - s) % p.n + p.n) % p.n;
+      // A source wholly in the target's future contributes nothing (ring.rs:222-228).
+      if (d->causal && p.off[src] > p.off[t] + p.len[t] - 1) continue;
+      p.sources[t].push_back(src);
+      p.part_off[t].push_back(cur);
+      const size_t rows = static_cast<size_t>(d->num_q_heads) * p.len[t];
+      cur += align256(rows * d->head_dim * sizeof(float)) + align256(rows * sizeof(float));
+    }
+  }
+  p.partial_bytes = cur;
+  p.staging_off = cur;
+  if (paged) {
+    p.staging_bytes_per_domain =
+        align256(static_cast<size_t>(max_len) * d->num_kv_heads * d->head_dim * es) * 2;
+    cur += p.staging_bytes_per_domain * p.n;
+  }
+  p.total = cur;
+  return p;
+}
+
+void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k, hcp_ring_view v,
+                const hcp_paged_pool* pool, const int32_t* table, int64_t table_len,
+                hcp_ring_view out, float* lse_out, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const bool paged = pool != nullptr;
+  ReplayPlan p = plan_replay(d, paged);
+  require(ws != nullptr || p.total == 0, "null workspace");
+  require(ws_bytes >= p.total, "workspace too small: need " + std::to_string(p.total) + " bytes");
+  check_view(q, "q", p.seq);
+  check_view(out, "out", p.seq);
+  check_out_view(out, d->dtype);
+  require(d->head_dim % 4 == 0, "head_dim must be a multiple of 4");
+  const int es = elem_size(d->dtype);
+  char* base = static_cast<char*>(ws);
+  int* err = paged ? device_error_flags() : nullptr;
+  if (paged) {
+    require(pool->data != nullptr && table != nullptr, "null pool or block table");
+    require(pool->num_kv_heads == d->num_kv_heads && pool->head_dim == d->head_dim,
+            "pool shape does not match the descriptor");
+    require(pool->elem_bytes == es, "pool element size does not match dtype");
+    require(pool->block_size >= 1, "block_size must be >= 1");
+    require((p.seq - 1) / pool->block_size < table_len, "block table shorter than the sequence");
+  } else {
+    check_view(k, "k", p.seq);
+    check_view(v, "v", p.seq);
+  }
+  // Ring step s: domain t consumes source (t - s) mod N (local first, then the
+  // predecessor chain, as the mock ring delivers it: mock.rs:143-149).
+  for (int s = 0; s < p.n; ++s) {
+    for (int t = 0; t < p.n; ++t) {
+      const int src = ((t - s) % p.n + p.n) % p.n;
+      int idx = -1;
+      for (size_t i = 0; i < p.sources[t].size(); ++i)
+        if (p.sources[t][i] == src) idx = static_cast<int>(i);
+      if (idx < 0) continue;  // fully-future source
+      hcp_ring_view kv_k = k, kv_v = v;
+      if (paged) {
+        // Stage the source chunk into this domain's ring buffer (bit-exact gather).
+        char* stg = base + p.staging_off + static_cast<size_t>(t) * p.staging_bytes_per_domain;
+        const int64_t hs = p.len[src];  // [Hkv, L, D] packed per source length
+        kv_k.data = stg;
+        kv_k.head_stride = hs * d->head_dim;
+        kv_k.seq_stride = d->head_dim;
+        kv_v.data = stg + p.staging_bytes_per_domain / 2;
+        kv_v.head_stride = hs * d->head_dim;
+        kv_v.seq_stride = d->head_dim;
+        launch_paged_copy(true, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads,
+                          pool->head_dim, pool->elem_bytes, table, 0, p.off[src], p.off[src] + p.len[src],
+                          kv_k.data, kv_v.data, kv_k.head_stride, kv_k.seq_stride, 0, err, stream);
+      } else {
+        kv_k.data = static_cast<char*>(k.data) + p.off[src] * k.seq_stride * es;
+        kv_v.data = static_cast<char*>(v.data) + p.off[src] * v.seq_stride * es;
+      }
+      hcp_ring_view qv = q;
+      qv.data = static_cast<char*>(q.data) + p.off[t] * q.seq_stride * es;
+      hcp_ring_block_desc bd;
+      bd.dtype = d->dtype;
+      bd.num_q_heads = d->num_q_heads;
+      bd.num_kv_heads = d->num_kv_heads;
+      bd.head_dim = d->head_dim;
+      bd.q_len = p.len[t];
+      bd.kv_len = p.len[src];
+      bd.q_offset = p.off[t];
+      bd.kv_offset = p.off[src];
+      bd.causal = d->causal;
+      bd.accumulate = 0;
+      bd.scale = d->scale;
+      char* part = base + p.part_off[t][idx];
+      const size_t rows = static_cast<size_t>(d->num_q_heads) * p.len[t];
+      float* po = reinterpret_cast<float*>(part);
+      float* pl = reinterpret_cast<float*>(part + align256(rows * d->head_dim * sizeof(float)));
+      launch_block_partial(make_launch(&bd, qv, kv_k, kv_v, po, pl), stream);
+    }
+  }
+  // Final merge per target domain into the output rows [off_t, off_t + len_t).
+  for (int t = 0; t < p.n; ++t) {
+    std::vector<const float*> os, ls;
+    const size_t rows = static_cast<size_t>(d->num_q_heads) * p.len[t];
+    for (size_t i = 0; i < p.sources[t].size(); ++i) {
+      char* part = base + p.part_off[t][i];
+      os.push_back(reinterpret_cast<const float*>(part));
+      ls.push_back(reinterpret_cast<const float*>(part + align256(rows * d->head_dim * sizeof(float))));
+    }
+    char* o_ptr = static_cast<char*>(out.data) + p.off[t] * out.seq_stride * es;
+    launch_lse_merge(static_cast<int>(os.size()), os.data(), ls.data(), d->num_q_heads, p.len[t],
+                     d->head_dim, d->dtype, o_ptr, out.head_stride, out.seq_stride,
+                     lse_out ? lse_out + p.off[t] : nullptr, p.seq, stream);
+  }
+}
+
+}  // namespace
+}  // namespace hcp
+
+using namespace hcp;
+
+extern "C" {
+
+const char* hcp_ring_last_error(void) { return g_last_error.c_str(); }
+
+int hcp_ring_abi_version(void) { return HCP_RING_ABI_VERSION; }
+
+int hcp_ring_device_count(int* count) {
+  return guarded(__func__, [&] {
+    require(count != nullptr, "null count");
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+      *count = 0;
+      throw Error(HCP_RING_E_BACKEND, "no usable HIP device");
+    }
+    *count = n;
+  });
+}
+
+int hcp_ring_fetch_device_errors(void* stream, int* flags) {
+  return guarded(__func__, [&] {
+    require(flags != nullptr, "null flags");
+    int* dev = device_error_flags();
+    HCP_HIP(hipStreamSynchronize(as_stream(stream)));
+    int host = 0;
+    HCP_HIP(hipMemcpy(&host, dev, sizeof(int), hipMemcpyDeviceToHost));
+    const int zero = 0;
+    HCP_HIP(hipMemcpy(dev, &zero, sizeof(int), hipMemcpyHostToDevice));
+    *flags = host;
+  });
+}
+
+int hcp_ring_block_partial(const hcp_ring_block_desc* desc, hcp_ring_view q, hcp_ring_view k,
+                           hcp_ring_view v, float* o, float* lse, void* stream) {
+  return guarded(__func__, [&] {
+    check_block_desc(desc);
+    check_view(q, "q", desc->q_len);
+    check_view(k, "k", desc->kv_len);
+    check_view(v, "v", desc->kv_len);
+    if (desc->q_len > 0) require(o != nullptr && lse != nullptr, "null o or lse");
+    launch_block_partial(make_launch(desc, q, k, v, o, lse), as_stream(stream));
+  });
+}
+
+int hcp_ring_lse_merge(int32_t num_parts, const float* const* o_parts, const float* const* lse_parts,
+                       int32_t num_heads, int64_t q_len, int32_t head_dim, int32_t out_dtype,
+                       hcp_ring_view out, float* lse_out, void* stream) {
+  return guarded(__func__, [&] {
+    require(num_parts >= 1 && num_parts <= 64, "num_parts must be in [1, 64]");
+    require(o_parts != nullptr && lse_parts != nullptr, "null partial arrays");
+    for (int i = 0; i < num_parts; ++i)
+      require(o_parts[i] != nullptr && lse_parts[i] != nullptr, "null partial pointer");
+    require(num_heads > 0 && q_len >= 0, "bad shape");
+    require(head_dim > 0 && head_dim <= 256 && head_dim % 4 == 0, "head_dim must be a multiple of 4 in [4, 256]");
+    elem_size(out_dtype);
+    check_view(out, "out", q_len);
+    check_out_view(out, out_dtype);
+    launch_lse_merge(num_parts, o_parts, lse_parts, num_heads, q_len, head_dim, out_dtype, out.data,
+                     out.head_stride, out.seq_stride, lse_out, q_len, as_stream(stream));
+  });
+}
+
+static void check_pool(const hcp_paged_pool* pool) {
+  require(pool != nullptr && pool->data != nullptr, "null pool");
+  require(pool->num_blocks > 0 && pool->block_size > 0 && pool->num_kv_heads > 0 && pool->head_dim > 0,
+          "pool dimensions must be positive");
+  require(pool->elem_bytes == 2 || pool->elem_bytes == 4, "elem_bytes must be 2 or 4");
+}
+
+static void check_paged_range(const hcp_paged_pool* pool, const int32_t* table, int64_t table_len,
+                              int64_t off, int64_t t0, int64_t t1) {
+  require(table != nullptr, "null block table");
+  require(t0 >= off && t1 >= t0, "need table_seq_offset <= t0 <= t1");
+  if (t1 > t0) require((t1 - 1 - off) / pool->block_size < table_len, "block table too short for [t0, t1)");
+}
+
+int hcp_paged_kv_gather(const hcp_paged_pool* pool, const int32_t* block_table, int64_t table_len,
+                        int64_t table_seq_offset, int64_t t0, int64_t t1, hcp_ring_view k_out,
+                        hcp_ring_view v_out, void* stream) {
+  return guarded(__func__, [&] {
+    check_pool(pool);
+    check_paged_range(pool, block_table, table_len, table_seq_offset, t0, t1);
+    check_view(k_out, "k_out", t1 - t0);
+    check_view(v_out, "v_out", t1 - t0);
+    require(k_out.head_stride == v_out.head_stride && k_out.seq_stride == v_out.seq_stride,
+            "k_out and v_out must share strides");
+    launch_paged_copy(true, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads, pool->head_dim,
+                      pool->elem_bytes, block_table, table_seq_offset, t0, t1, k_out.data, v_out.data,
+                      k_out.head_stride, k_out.seq_stride, 0, device_error_flags(), as_stream(stream));
+  });
+}
+
+int hcp_paged_kv_scatter(const hcp_paged_pool* pool, const int32_t* block_table, int64_t table_len,
+                         int64_t table_seq_offset, int64_t t0, int64_t t1, hcp_ring_view k_in,
+                         hcp_ring_view v_in, int32_t zero_tail, void* stream) {
+  return guarded(__func__, [&] {
+    check_pool(pool);
+    check_paged_range(pool, block_table, table_len, table_seq_offset, t0, t1);
+    check_view(k_in, "k_in", t1 - t0);
+    check_view(v_in, "v_in", t1 - t0);
+    require(k_in.head_stride == v_in.head_stride && k_in.seq_stride == v_in.seq_stride,
+            "k_in and v_in must share strides");
+    launch_paged_copy(false, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads, pool->head_dim,
+                      pool->elem_bytes, block_table, table_seq_offset, t0, t1, k_in.data, v_in.data,
+                      k_in.head_stride, k_in.seq_stride, zero_tail ? 1 : 0, device_error_flags(),
+                      as_stream(stream));
+  });
+}
+
+size_t hcp_paged_decode_workspace_size(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool) {
+  if (desc == nullptr || pool == nullptr || desc->batch <= 0) return 0;
+  (void)pool;
+  return decode_workspace_bytes(desc->batch, desc->num_q_heads, desc->head_dim, desc->t0, desc->t1);
+}
+
+int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool, hcp_ring_view q,
+                             const int32_t* block_tables, const int32_t* seq_lens, float* o, float* lse,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded(__func__, [&] {
+    require(desc != nullptr, "null descriptor");
+    check_pool(pool);
+    require(desc->batch > 0, "batch must be positive");
+    require(desc->num_q_heads > 0 && desc->num_kv_heads == pool->num_kv_heads, "kv heads must match the pool");
+    require(desc->head_dim == pool->head_dim, "head_dim must match the pool");
+    require(pool->elem_bytes == 2, "paged decode needs a 16-bit pool");
+    require(desc->t0 >= 0 && desc->t1 >= desc->t0, "need 0 <= t0 <= t1");
+    require(block_tables != nullptr && o != nullptr && lse != nullptr, "null pointer");
+    require(desc->table_len >= 1 && desc->table_stride >= desc->table_len, "bad table shape");
+    if (desc->t1 > desc->t0) require((desc->t1 - 1) / pool->block_size < desc->table_len, "block table too short");
+    require(desc->scale > 0.f, "scale must be positive");
+    check_view(q, "q", 1);
+    require(mfma_layout_ok(q), "q must be 16-byte aligned with strides multiple of 8");
+    launch_paged_decode(desc->dtype, desc->batch, desc->num_q_heads, desc->num_kv_heads, desc->head_dim, q.data,
+                        q.seq_stride, q.head_stride, pool->data, pool->num_blocks, pool->block_size, block_tables,
+                        desc->table_stride, desc->table_len, seq_lens, desc->t0, desc->t1, desc->scale, o, lse,
+                        workspace, workspace_bytes, device_error_flags(), as_stream(stream));
+  });
+}
+
+size_t hcp_ring_replay_workspace_size(const hcp_ring_replay_desc* desc, int32_t paged) {
+  try {
+    return plan_replay(desc, paged != 0).total;
+  } catch (...) {
+    return 0;
+  }
+}
+
+int hcp_ring_prefill_replay(const hcp_ring_replay_desc* desc, hcp_ring_view q, hcp_ring_view k, hcp_ring_view v,
+                            hcp_ring_view out, float* lse_out, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return guarded(__func__, [&] {
+    run_replay(desc, q, k, v, nullptr, nullptr, 0, out, lse_out, workspace, workspace_bytes, as_stream(stream));
+  });
+}
+
+int hcp_ring_prefill_replay_paged(const hcp_ring_replay_desc* desc, hcp_ring_view q, const hcp_paged_pool* pool,
+                                  const int32_t* block_table, int64_t table_len, hcp_ring_view out, float* lse_out,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded(__func__, [&] {
+    check_pool(pool);
+    hcp_ring_view none{nullptr, 0, 1};
+    run_replay(desc, q, none, none, pool, block_table, table_len, out, lse_out, workspace, workspace_bytes,
+               as_stream(stream));
+  });
+}
+
+int hcp_synth_normals(uint64_t seed, int64_t offset, int64_t count, int32_t dtype, void* out, void* stream) {
+  return guarded(__func__, [&] {
+    require(offset >= 0 && count >= 0, "offset and count must be >= 0");
+    if (count > 0) require(out != nullptr, "null out");
+    launch_synth_normals(seed, offset, count, dtype, out, as_stream(stream));
+  });
+}
+
+}  // extern "C"

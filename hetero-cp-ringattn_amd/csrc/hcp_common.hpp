@@ -1,0 +1,103 @@
+// Shared definitions for the gfx950 kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace hcp {
+
+// bf16 / fp16 vectors as the gfx950 MFMA builtins take them.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+enum DType : int32_t { kF16 = 1, kBF16 = 2, kF32 = 3, kI32 = 4, kI64 = 5 };
+
+// Error raised inside the library; the C-ABI layer turns it into a status code.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+inline void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    throw Error(-5, std::string(what) + ": " + hipGetErrorString(e));
+  }
+}
+
+#define HCP_HIP(expr) ::hcp::hip_check((expr), #expr)
+
+inline void require(bool ok, const std::string& msg) {
+  if (!ok) throw Error(-6, msg);
+}
+
+// Sticky device-side error flags (bit 0: paged block id out of range).
+// Defined in capi.hip; kernels set bits with atomicOr through this pointer
+// argument resolved once per device by the host (hipGetSymbolAddress).
+int* device_error_flags();
+
+// ---- scalar conversions (device) ----
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (finite and inf inputs; NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+// Element load/store by dtype (used by the general kernels).
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_elem<kF32>(const void* p, int64_t i) {
+  return static_cast<const float*>(p)[i];
+}
+template <>
+__device__ __forceinline__ float load_elem<kBF16>(const void* p, int64_t i) {
+  return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <>
+__device__ __forceinline__ float load_elem<kF16>(const void* p, int64_t i) {
+  return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void store_elem(void* p, int64_t i, float v);
+template <>
+__device__ __forceinline__ void store_elem<kF32>(void* p, int64_t i, float v) {
+  static_cast<float*>(p)[i] = v;
+}
+template <>
+__device__ __forceinline__ void store_elem<kBF16>(void* p, int64_t i, float v) {
+  static_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+}
+template <>
+__device__ __forceinline__ void store_elem<kF16>(void* p, int64_t i, float v) {
+  static_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v);
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+}  // namespace hcp

@@ -1,0 +1,44 @@
+// Host-side launchers of the gfx950 kernels (internal to the library).
+#pragma once
+
+#include "hcp_common.hpp"
+
+namespace hcp {
+
+// One (query chunk, KV chunk) block partial; see block_attn.hip.
+struct BlockLaunch {
+  int dtype;
+  const void *q, *k, *v;
+  int64_t q_hs, q_ss, k_hs, k_ss, v_hs, v_ss;  // element strides
+  float* o;
+  float* lse;
+  int hq, hkv, d;
+  int64_t lq, lk, q_off, k_off;
+  int causal, accumulate;
+  float scale;
+  bool force_general;  // take the general kernel even where the matrix-core one applies
+};
+
+bool block_uses_mfma(int dtype, int d);
+void launch_block_partial(const BlockLaunch& L, hipStream_t stream);
+
+void launch_lse_merge(int n, const float* const* o_parts, const float* const* lse_parts, int heads,
+                      int64_t q_len, int d, int out_dtype, void* out, int64_t out_hs, int64_t out_ss,
+                      float* lse_out, int64_t lse_out_hs, hipStream_t stream);
+
+void launch_paged_copy(bool gather, void* pool, int64_t num_blocks, int bs, int hkv, int d,
+                       int elem_bytes, const int32_t* table, int64_t table_seq_offset, int64_t t0,
+                       int64_t t1, void* k_buf, void* v_buf, int64_t head_stride, int64_t seq_stride,
+                       int zero_tail, int* err, hipStream_t stream);
+
+size_t decode_workspace_bytes(int batch, int hq, int d, int64_t t0, int64_t t1);
+void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const void* q, int64_t q_bs,
+                         int64_t q_hs, const void* pool, int64_t num_blocks, int bs,
+                         const int32_t* tables, int64_t table_stride, int64_t table_len,
+                         const int32_t* seq_lens, int64_t t0, int64_t t1, float scale, float* o,
+                         float* lse, void* ws, size_t ws_bytes, int* err, hipStream_t stream);
+
+void launch_synth_normals(uint64_t seed, int64_t offset, int64_t count, int dtype, void* out,
+                          hipStream_t stream);
+
+}  // namespace hcp

@@ -1,0 +1,357 @@
+// Single-query paged decode partial over one domain chunk.
+//
+// Replaces decode_local_partial / decode_local_compact_partial (ring.rs:625-639,
+// :515-523): one query token per sequence, no causal mask (ring.rs:631-637), output
+// normalised o and natural-log lse in fp32.  KV is read in place from the vLLM pool
+// [2, num_blocks, bs, Hkv, D] (python/hcp_vllm_block_ring_plugin.py:8-14) through the
+// sequence's block table -- no gather, no GQA expand copy.
+//
+// Work split (HBM-bound: every K/V byte is read exactly once):
+//   * grid = (splits, batch).  A workgroup (4 waves) owns one sequence and a
+//     contiguous run of 16-token groups of the chunk, for ALL kv heads, so per 16
+//     tokens it reads the whole K and V rows of those slots (one contiguous span per
+//     plane when bs >= 16).  Wave w handles kv heads w, w+4, ...
+//   * Scores: S^T = K Q^T on MFMA 16x16x32 (A = 16 key rows loaded straight from the
+//     pool, 16 bytes per lane; B = the rep <= 16 query heads of the kv head, zero-padded
+//     to 16 columns, held in registers for the whole kernel).
+//   * Online softmax per query head in the log2 domain; P goes through a small LDS
+//     slot (broadcast reads) and PV runs on VALU with each lane owning 8 head-dim
+//     values of 4 of the 16 keys (fp32 accumulators), reduced across lanes once at the
+//     end.
+//   * Each split writes (o, lse) to the workspace; the LSE merge kernel combines the
+//     splits of a sequence (heads = batch*Hq, q_len = 1).
+#include "kernels.hpp"
+
+namespace hcp {
+
+struct DecodeArgs {
+  const uint16_t* q;
+  int64_t q_bs, q_hs;  // element strides: batch, head
+  const uint16_t* pool;
+  int64_t plane_elems;
+  int64_t num_blocks;
+  int32_t bs, hkv, hq, rep;
+  const int32_t* tables;
+  int64_t table_stride, table_len;
+  const int32_t* seq_lens;
+  int64_t t0, t1;
+  int64_t g_begin;      // first 16-token group index (t0 / 16)
+  int32_t groups_per_split;
+  int32_t n_groups;     // total groups in [g_begin*16, t1)
+  float scale_log2;
+  float* ws_o;          // [splits][batch*hq][D]
+  float* ws_lse;        // [splits][batch*hq]
+  int32_t batch;
+  int* err;
+};
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+template <int DT>
+__device__ __forceinline__ f32x4 mma16(u32x4 a, u32x4 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mma16<kBF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mma16<kF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ float lo_half(uint32_t w) {
+  return DT == kBF16 ? __uint_as_float(w << 16) : f16_bits_to_f32(static_cast<uint16_t>(w & 0xffffu));
+}
+template <int DT>
+__device__ __forceinline__ float hi_half(uint32_t w) {
+  return DT == kBF16 ? __uint_as_float(w & 0xffff0000u) : f16_bits_to_f32(static_cast<uint16_t>(w >> 16));
+}
+
+constexpr int kDecWaves = 4;
+constexpr int kMaxHeadsPerWave = 4;  // supports Hkv <= 16
+
+// HPW = kv heads per wave; wave w owns kv heads w*HPW .. w*HPW+HPW-1 (< Hkv).
+template <int D, int DT, int HPW>
+__global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
+  constexpr int KS = D / 32;        // k-steps of 32 for the QK^T product
+  constexpr int DCH = D / 8;        // 8-wide d chunks per row (16 for D=128)
+  constexpr int TOKS_PER_LANE = 16 * DCH / 64;  // keys per lane in PV (4 for D=128)
+
+  __shared__ float p_lds[kDecWaves][16][16];  // [wave][key][query col]
+  __shared__ float alpha_lds[kDecWaves][16];
+
+  const int b = blockIdx.y;
+  const int split = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;   // MFMA column = query head within the kv group
+  const int grp = lane >> 4;   // MFMA k-group / key group
+  // PV role: lane owns d chunk pv_dc (8 values) of keys pv_tg*TOKS_PER_LANE .. +TOKS_PER_LANE.
+  const int pv_dc = lane % DCH;
+  const int pv_tg = lane / DCH;  // key subgroup: keys pv_tg*TOKS_PER_LANE .. +TOKS_PER_LANE
+
+  int64_t t_end = a.t1;
+  if (a.seq_lens != nullptr) t_end = min(t_end, static_cast<int64_t>(a.seq_lens[b]));
+  const int g0 = split * a.groups_per_split;
+  const int g1 = min(a.n_groups, g0 + a.groups_per_split);
+  const int32_t* table = a.tables + static_cast<int64_t>(b) * a.table_stride;
+
+  // Q^T fragments: lane (col, grp) holds Q[head kvh*rep + col][grp*8 + 32*s .. +8].
+  u32x4 qf[HPW][KS];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    const int kvh = wave * HPW + hh;
+    const bool hv = kvh < a.hkv;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 v = {0, 0, 0, 0};
+      if (hv && col < a.rep) {
+        const uint16_t* qp = a.q + b * a.q_bs + (kvh * a.rep + col) * a.q_hs + grp * 8 + 32 * s;
+        v = *reinterpret_cast<const u32x4*>(qp);
+      }
+      qf[hh][s] = v;
+    }
+  }
+
+  // PV accumulators cover rep <= 4 query heads per kv head (checked by the launcher).
+  float acc[HPW][4][8];  // [head][query col][d]
+  float m_run[HPW], l_run[HPW];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    m_run[hh] = -1.0e30f;
+    l_run[hh] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[hh][c][e] = 0.f;
+  }
+
+  const int64_t row_elems = static_cast<int64_t>(a.hkv) * D;  // one slot, all heads
+  for (int g = g0; g < g1; ++g) {
+    const int64_t tok0 = (a.g_begin + g) * 16;
+    // Keys tok0 .. tok0+15 come from table entries (tok0 / bs) (bs multiple of 16).
+    const int64_t entry = tok0 / a.bs;
+    const int32_t blk = entry < a.table_len ? table[entry] : -1;
+    const bool blk_ok = blk >= 0 && blk < a.num_blocks;
+    if (!blk_ok) {
+      if (threadIdx.x == 0 && entry < a.table_len) atomicOr(a.err, 1);
+      continue;
+    }
+    const int slot0 = static_cast<int>(tok0 - entry * a.bs);
+    const uint16_t* kslot = a.pool + (static_cast<int64_t>(blk) * a.bs + slot0) * row_elems;
+    const uint16_t* vslot = kslot + a.plane_elems;
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int kvh = wave * HPW + hh;
+      if (kvh >= a.hkv) break;
+      // ---- S^T = K Q^T ----
+      f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+      const uint16_t* krow = kslot + col * row_elems + kvh * D + grp * 8;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + 32 * s);
+        s4 = mma16<DT>(kf, qf[hh][s], s4);
+      }
+      // lane (col = query, grp) holds keys grp*4 + i.
+      float tmax = -INFINITY;
+      float sv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t t = tok0 + grp * 4 + i;
+        const bool ok = t >= a.t0 && t < t_end;
+        sv[i] = ok ? s4[i] * a.scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, sv[i]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float m_new = fmaxf(m_run[hh], tmax);
+      const float alpha = exp2f(m_run[hh] - m_new);
+      m_run[hh] = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(sv[i] - m_new);
+        psum += p;
+        if (col < 4) p_lds[wave][grp * 4 + i][col] = p;
+      }
+      l_run[hh] = l_run[hh] * alpha + psum;  // per-lane partial over its keys (rescaled)
+      if (lane < 4) alpha_lds[wave][lane] = alpha;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // ---- O += P V (VALU) ----
+      float al[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) al[c] = alpha_lds[wave][c];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[hh][c][e] *= al[c];
+      const uint16_t* vbase = vslot + kvh * D + pv_dc * 8;
+#pragma unroll
+      for (int j = 0; j < TOKS_PER_LANE; ++j) {
+        const int key = pv_tg * TOKS_PER_LANE + j;
+        const int64_t t = tok0 + key;
+        const bool ok = t >= a.t0 && t < t_end;
+        u32x4 vv = ok ? *reinterpret_cast<const u32x4*>(vbase + key * row_elems) : u32x4{0, 0, 0, 0};
+        const float4 p4 = *reinterpret_cast<const float4*>(&p_lds[wave][key][0]);
+        float vf[8];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          vf[2 * w] = lo_half<DT>(vv[w]);
+          vf[2 * w + 1] = hi_half<DT>(vv[w]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc[hh][0][e] += p4.x * vf[e];
+          acc[hh][1][e] += p4.y * vf[e];
+          acc[hh][2][e] += p4.z * vf[e];
+          acc[hh][3][e] += p4.w * vf[e];
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+
+  // ---- epilogue: reduce over key subgroups, normalise, write split partial ----
+  const int64_t ws_row_base = static_cast<int64_t>(split) * a.batch * a.hq + static_cast<int64_t>(b) * a.hq;
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    const int kvh = wave * HPW + hh;
+    if (kvh >= a.hkv) break;
+    float l = l_run[hh];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);  // lanes with the same col now hold the total over keys
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = acc[hh][c][e];
+        // Lanes with equal pv_dc hold the same d for different key subgroups.
+        for (int off = DCH; off < 64; off *= 2) v += __shfl_xor(v, off);
+        acc[hh][c][e] = v;
+      }
+    // l for query c lives in lanes with col == c; broadcast.
+    float lc[4], mc;
+    mc = m_run[hh];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) lc[c] = __shfl(l, c);
+    if (pv_tg == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (c >= a.rep) break;
+        const float inv = lc[c] > 0.f ? 1.f / lc[c] : 0.f;
+        float* orow = a.ws_o + (ws_row_base + kvh * a.rep + c) * D + pv_dc * 8;
+        float4 o0 = make_float4(acc[hh][c][0] * inv, acc[hh][c][1] * inv, acc[hh][c][2] * inv, acc[hh][c][3] * inv);
+        float4 o1 = make_float4(acc[hh][c][4] * inv, acc[hh][c][5] * inv, acc[hh][c][6] * inv, acc[hh][c][7] * inv);
+        reinterpret_cast<float4*>(orow)[0] = o0;
+        reinterpret_cast<float4*>(orow)[1] = o1;
+      }
+    }
+    if (lane < a.rep && lane < 4) {
+      const float lt = lc[lane];
+      a.ws_lse[ws_row_base + kvh * a.rep + lane] = lt > 0.f ? (mc + __log2f(lt)) * kLn2 : -INFINITY;
+    }
+  }
+}
+
+struct DecodePlan {
+  int splits;
+  int groups_per_split;
+  int n_groups;
+  int64_t g_begin;
+};
+
+DecodePlan plan_decode(int batch, int64_t t0, int64_t t1) {
+  DecodePlan p;
+  p.g_begin = t0 / 16;
+  const int64_t g_end = t1 > t0 ? (t1 + 15) / 16 : p.g_begin;
+  p.n_groups = static_cast<int>(g_end - p.g_begin);
+  // Aim for ~8 workgroups per CU on 256 CUs, at least 4 groups (64 keys) per split.
+  const int target = 2048;
+  int splits = static_cast<int>(ceil_div(target, std::max(batch, 1)));
+  splits = std::max(1, std::min(splits, 64));
+  int gps = static_cast<int>(ceil_div(std::max(p.n_groups, 1), splits));
+  gps = std::max(gps, 4);
+  p.groups_per_split = gps;
+  p.splits = static_cast<int>(ceil_div(std::max(p.n_groups, 1), gps));
+  return p;
+}
+
+size_t decode_workspace_bytes(int batch, int hq, int d, int64_t t0, int64_t t1) {
+  const DecodePlan p = plan_decode(batch, t0, t1);
+  const size_t rows = static_cast<size_t>(p.splits) * batch * hq;
+  auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+  return al(rows * d * sizeof(float)) + al(rows * sizeof(float));
+}
+
+void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const void* q, int64_t q_bs,
+                         int64_t q_hs, const void* pool, int64_t num_blocks, int bs,
+                         const int32_t* tables, int64_t table_stride, int64_t table_len,
+                         const int32_t* seq_lens, int64_t t0, int64_t t1, float scale, float* o,
+                         float* lse, void* ws, size_t ws_bytes, int* err, hipStream_t stream) {
+  require(hq % hkv == 0 && hq / hkv <= 4, "paged_decode: num_q_heads/num_kv_heads must be <= 4");
+  require(hkv <= kDecWaves * kMaxHeadsPerWave, "paged_decode: num_kv_heads must be <= 16");
+  require(bs % 16 == 0, "paged_decode: block_size must be a multiple of 16");
+  require(d == 64 || d == 128, "paged_decode: head_dim must be 64 or 128");
+  require(dtype == kBF16 || dtype == kF16, "paged_decode: dtype must be BF16 or F16");
+  const DecodePlan p = plan_decode(batch, t0, t1);
+  require(ws_bytes >= decode_workspace_bytes(batch, hq, d, t0, t1), "paged_decode: workspace too small");
+  auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+  const size_t rows = static_cast<size_t>(p.splits) * batch * hq;
+  float* ws_o = static_cast<float*>(ws);
+  float* ws_lse = reinterpret_cast<float*>(static_cast<char*>(ws) + al(rows * d * sizeof(float)));
+
+  DecodeArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_bs = q_bs;
+  a.q_hs = q_hs;
+  a.pool = static_cast<const uint16_t*>(pool);
+  a.plane_elems = num_blocks * bs * hkv * static_cast<int64_t>(d);
+  a.num_blocks = num_blocks;
+  a.bs = bs;
+  a.hkv = hkv;
+  a.hq = hq;
+  a.rep = hq / hkv;
+  a.tables = tables;
+  a.table_stride = table_stride;
+  a.table_len = table_len;
+  a.seq_lens = seq_lens;
+  a.t0 = t0;
+  a.t1 = t1;
+  a.g_begin = p.g_begin;
+  a.groups_per_split = p.groups_per_split;
+  a.n_groups = p.n_groups;
+  a.scale_log2 = scale * kLog2e;
+  a.ws_o = ws_o;
+  a.ws_lse = ws_lse;
+  a.batch = batch;
+  a.err = err;
+  const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(batch));
+  const int hpw = (hkv + kDecWaves - 1) / kDecWaves;
+#define HCP_DEC(D_, DT_)                                                               \
+  switch (hpw) {                                                                       \
+    case 1: paged_decode_kernel<D_, DT_, 1><<<grid, 256, 0, stream>>>(a); break;        \
+    case 2: paged_decode_kernel<D_, DT_, 2><<<grid, 256, 0, stream>>>(a); break;        \
+    case 3: paged_decode_kernel<D_, DT_, 3><<<grid, 256, 0, stream>>>(a); break;        \
+    default: paged_decode_kernel<D_, DT_, 4><<<grid, 256, 0, stream>>>(a); break;       \
+  }
+  if (dtype == kBF16) {
+    if (d == 128) { HCP_DEC(128, kBF16) } else { HCP_DEC(64, kBF16) }
+  } else {
+    if (d == 128) { HCP_DEC(128, kF16) } else { HCP_DEC(64, kF16) }
+  }
+#undef HCP_DEC
+  HCP_HIP(hipGetLastError());
+  // Merge the splits of every (sequence, head): rows = batch*hq, one token each.
+  const float* o_parts[64];
+  const float* l_parts[64];
+  for (int s = 0; s < p.splits; ++s) {
+    o_parts[s] = ws_o + static_cast<size_t>(s) * batch * hq * d;
+    l_parts[s] = ws_lse + static_cast<size_t>(s) * batch * hq;
+  }
+  launch_lse_merge(p.splits, o_parts, l_parts, batch * hq, 1, d, kF32, o, d, d, lse, 1, stream);
+}
+
+}  // namespace hcp

@@ -1,0 +1,267 @@
+/*
+ * hcp_ring.h -- C ABI of the MI355X-native ring-attention compute path.
+ *
+ * Drop-in boundary for the blockwise ring-attention operator of hetero-cp-ringattn
+ * (HcpRingAttentionBackend in rust/src/model/attention/ring.rs).  Every entry point is
+ * `extern "C"`, takes plain pointers and sizes, and returns an int status in the style
+ * of the reference's FFI bridge (src/rust_bridge.cc:109-128,180-199,715-721):
+ *
+ *     0  success
+ *    -1  numeric mismatch            (reserved; rust_bridge.cc -1)
+ *    -2  C++ exception caught at the boundary (rust_bridge.cc -2)
+ *    -3  unknown exception           (rust_bridge.cc -3)
+ *    -4  bad device index            (rust_bridge.cc -4, bad device name)
+ *    -5  GPU backend unavailable or a HIP call failed (rust_bridge.cc -5)
+ *    -6  invalid arguments, null pointer or size mismatch (rust_bridge.cc -6)
+ *
+ * The human-readable message of the last failing call on the calling thread is
+ * returned by hcp_ring_last_error() (thread-local; the reference keeps one
+ * process-global std::string per smoke, rust_bridge.cc:19-27,614-644).
+ *
+ * Memory: every tensor pointer is a DEVICE pointer owned by the caller.  Entry points
+ * never allocate device memory; scratch comes in through a caller-provided workspace
+ * whose size the matching *_workspace_size() query reports.  Work is enqueued on the
+ * given stream (hipStream_t passed as void*; NULL = the default stream) and returns
+ * without synchronising.
+ *
+ * Layout convention (hcp_ring_view): a [heads, tokens, head_dim] tensor whose last
+ * dimension is contiguous; element (h, t, d) lives at data + h*head_stride +
+ * t*seq_stride + d (strides in ELEMENTS).  Both the reference's head-major [B,H,S,D]
+ * tensors and the projection's token-major [S,H,D] view (ring.rs:1884-1903,
+ * view+transpose) are expressible without a copy.
+ */
+#ifndef HCP_RING_H_
+#define HCP_RING_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HCP_RING_ABI_VERSION 1
+
+enum hcp_ring_status {
+  HCP_RING_OK = 0,
+  HCP_RING_E_MISMATCH = -1,
+  HCP_RING_E_EXCEPTION = -2,
+  HCP_RING_E_UNKNOWN = -3,
+  HCP_RING_E_DEVICE = -4,
+  HCP_RING_E_BACKEND = -5,
+  HCP_RING_E_INVALID = -6
+};
+
+/* Element types; numbering of TensorDType (include/hcp_ringattn/core/tensor_types.h:9-16). */
+enum hcp_ring_dtype {
+  HCP_DTYPE_F16 = 1,
+  HCP_DTYPE_BF16 = 2,
+  HCP_DTYPE_F32 = 3,
+  HCP_DTYPE_I32 = 4,
+  HCP_DTYPE_I64 = 5
+};
+
+typedef struct hcp_ring_view {
+  void* data;          /* device pointer of element (0, 0, 0)            */
+  int64_t head_stride; /* elements between consecutive heads              */
+  int64_t seq_stride;  /* elements between consecutive tokens             */
+} hcp_ring_view;
+
+/* ---------------------------------------------------------------------------------
+ * Library state
+ * ------------------------------------------------------------------------------- */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* hcp_ring_last_error(void);
+
+/* HCP_RING_ABI_VERSION of the loaded library. */
+int hcp_ring_abi_version(void);
+
+/* Number of visible GPUs in *count; -5 when no HIP device is usable. */
+int hcp_ring_device_count(int* count);
+
+/*
+ * Reads and clears the sticky device-side error flags of the current device
+ * (bit 0: a paged block id outside [0, num_blocks) was met and that row skipped).
+ * Synchronises `stream`.
+ */
+int hcp_ring_fetch_device_errors(void* stream, int* flags);
+
+/* ---------------------------------------------------------------------------------
+ * (1) Block partial: one ring step = one (query chunk, KV chunk) pair.
+ *
+ * Replaces process_kv_block + positioned_local_compact_partial
+ * (ring.rs:201-370, :538-571) and, with accumulate=1,
+ * positioned_merge_compact_partial (ring.rs:574-603).
+ *
+ * Query token i has global position q_offset+i, key token j has kv_offset+j;
+ * with causal=1 a key is visible iff q_pos >= k_pos (ring.rs:249-273).  Query head h
+ * reads KV head h / (num_q_heads/num_kv_heads) (the GQA expand of ring.rs:496-512,
+ * done by index, no copy).  Outputs, fp32:
+ *     o   [num_q_heads, q_len, head_dim] contiguous, normalised (softmax-weighted V);
+ *     lse [num_q_heads, q_len]           contiguous, natural-log log-sum-exp of the
+ *                                        scaled scores; -inf (and o = 0) for a row
+ *                                        that sees no key.
+ * With accumulate=1, o/lse hold a running partial on entry and are replaced by the
+ * merge of it with this block (the rm=lse, rs=1, obh=o re-entry of ring.rs:585-587).
+ * dtype: BF16 or F16 (matrix-core path, head_dim 64 or 128) or F32 (any head_dim
+ * <= 256; F16/BF16 with other head dims take the same general kernel).
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_ring_block_desc {
+  int32_t dtype;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int64_t q_len;
+  int64_t kv_len;
+  int64_t q_offset;
+  int64_t kv_offset;
+  int32_t causal;
+  int32_t accumulate;
+  float scale; /* softmax scale, 1/sqrt(head_dim) in the reference (ring.rs:152) */
+} hcp_ring_block_desc;
+
+int hcp_ring_block_partial(const hcp_ring_block_desc* desc, hcp_ring_view q, hcp_ring_view k,
+                           hcp_ring_view v, float* o, float* lse, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * (2) LSE merge of ring-step partials.
+ *
+ * Replaces the re-entry merge of positioned_merge_compact_partial / decode_merge_packet
+ * (ring.rs:574-603, :647-663) applied across all steps, in closed form:
+ *   m = max_i lse_i;  o = sum_i e^(lse_i-m) o_i / sum_i e^(lse_i-m);
+ *   lse = m + ln sum_i e^(lse_i-m);  all -inf -> (o = 0, lse = -inf).
+ * o_parts / lse_parts are HOST arrays of num_parts DEVICE pointers, each partial laid
+ * out as hcp_ring_block_partial writes it ([H, q_len, D] and [H, q_len] fp32).
+ * The merged output goes to `out` (out_dtype BF16, F16 or F32, strided view) and, if
+ * lse_out is not NULL, to lse_out [H, q_len] fp32.  1 <= num_parts <= 64.
+ * ------------------------------------------------------------------------------- */
+int hcp_ring_lse_merge(int32_t num_parts, const float* const* o_parts,
+                       const float* const* lse_parts, int32_t num_heads, int64_t q_len,
+                       int32_t head_dim, int32_t out_dtype, hcp_ring_view out, float* lse_out,
+                       void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * (3) Paged-KV staging: vLLM block layout <-> contiguous ring buffer.
+ *
+ * Pool layout [2, num_blocks, block_size, num_kv_heads, head_dim] (plane 0 = K,
+ * plane 1 = V), python/hcp_vllm_block_ring_plugin.py:8-14.  Token t of the sequence
+ * lives in physical block block_table[(t - table_seq_offset) / block_size], slot
+ * (t - table_seq_offset) % block_size (:304-337).  Gather copies tokens [t0, t1) to
+ * k_out/v_out (row t - t0); scatter is its inverse and, with zero_tail=1, zero-fills
+ * the slots after t1 in t1's block (the partial-last-block rule of :520-530).
+ * Copies are bit-exact.  block_table is a DEVICE int32 array of table_len entries.
+ * Block ids outside [0, num_blocks) are skipped and raise device error flag bit 0.
+ * elem_bytes: 2 (bf16/fp16) or 4 (fp32).
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_paged_pool {
+  void* data;
+  int64_t num_blocks;
+  int32_t block_size;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t elem_bytes;
+} hcp_paged_pool;
+
+int hcp_paged_kv_gather(const hcp_paged_pool* pool, const int32_t* block_table, int64_t table_len,
+                        int64_t table_seq_offset, int64_t t0, int64_t t1, hcp_ring_view k_out,
+                        hcp_ring_view v_out, void* stream);
+
+int hcp_paged_kv_scatter(const hcp_paged_pool* pool, const int32_t* block_table,
+                         int64_t table_len, int64_t table_seq_offset, int64_t t0, int64_t t1,
+                         hcp_ring_view k_in, hcp_ring_view v_in, int32_t zero_tail,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * (4) Paged single-query decode partial over one domain chunk.
+ *
+ * Replaces decode_local_partial / decode_local_compact_partial (ring.rs:625-639,
+ * :515-523) for a batch of independent sequences: each sequence b has one query
+ * token q[b] ([num_q_heads, head_dim] at q.data + b*q.seq_stride + h*q.head_stride)
+ * and attends, without a causal mask (ring.rs:631-637), to its tokens
+ * [t0, min(t1, seq_lens[b])) read straight from the paged pool through row b of
+ * block_tables (token t in block block_tables[b*table_stride + t/block_size]).
+ * seq_lens may be NULL (every sequence covers [t0, t1)).  Outputs fp32:
+ *     o [batch, num_q_heads, head_dim], lse [batch, num_q_heads] (-inf, o = 0 when the
+ *     range is empty).
+ * The chunk is split across workgroups; workspace holds the split partials
+ * (hcp_paged_decode_workspace_size bytes, 256-byte aligned).
+ * dtype BF16 or F16, head_dim 64 or 128, block_size a multiple of 16.
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_paged_decode_desc {
+  int32_t dtype;
+  int32_t batch;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t reserved0;
+  int64_t t0;
+  int64_t t1;
+  int64_t table_stride;
+  int64_t table_len;
+  float scale;
+} hcp_paged_decode_desc;
+
+size_t hcp_paged_decode_workspace_size(const hcp_paged_decode_desc* desc,
+                                       const hcp_paged_pool* pool);
+
+int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool,
+                             hcp_ring_view q, const int32_t* block_tables,
+                             const int32_t* seq_lens, float* o, float* lse, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * (5) Single-GPU ring replay of a whole prefill (the ring_attention driver).
+ *
+ * Replays ring_attention (ring.rs:861-1398) for every domain of a contiguous uneven
+ * split: domain d owns global positions [off_d, off_d + chunk_lens[d]) (vanilla
+ * assignment, rust/src/model/attention/strategy.rs:53-63), visits sources
+ * (d - s) mod N for s = 0..N-1 (local first, then the predecessor chain), skips
+ * sources entirely in its future (ring.rs:222-228), computes one partial per
+ * (domain, source) with (1) and merges them with (2).  q/k/v/out cover the whole
+ * sequence (global token index = view token index).  out receives the merged
+ * attention (dtype = desc->dtype), lse_out (may be NULL) the merged LSE [Hq, S] fp32.
+ * Workspace: hcp_ring_replay_workspace_size bytes.
+ *
+ * With a paged pool (hcp_ring_prefill_replay_paged), K/V are not given as views: each
+ * source domain's chunk is first gathered with (3) from the pool through block_table
+ * (table_seq_offset 0) into a staging area inside the workspace, then consumed.
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_ring_replay_desc {
+  int32_t dtype;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t num_domains;
+  int32_t causal;
+  const int64_t* chunk_lens; /* HOST array of num_domains lengths (each >= 1) */
+  float scale;
+} hcp_ring_replay_desc;
+
+size_t hcp_ring_replay_workspace_size(const hcp_ring_replay_desc* desc, int32_t paged);
+
+int hcp_ring_prefill_replay(const hcp_ring_replay_desc* desc, hcp_ring_view q, hcp_ring_view k,
+                            hcp_ring_view v, hcp_ring_view out, float* lse_out, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+int hcp_ring_prefill_replay_paged(const hcp_ring_replay_desc* desc, hcp_ring_view q,
+                                  const hcp_paged_pool* pool, const int32_t* block_table,
+                                  int64_t table_len, hcp_ring_view out, float* lse_out,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Synthetic inputs (no reference counterpart; used by the benchmark).
+ *
+ * Writes normals n = offset .. offset+count-1 of the LCG + Box-Muller stream of
+ * rust/src/smoke/reference_algo.rs:56-90 started at `seed` (normal 2j is r*cos,
+ * 2j+1 is r*sin of pair j), rounded f64 -> fp32 (-> bf16/fp16), to out (dtype F32,
+ * BF16 or F16), computed on the device with LCG jump-ahead.
+ * ------------------------------------------------------------------------------- */
+int hcp_synth_normals(uint64_t seed, int64_t offset, int64_t count, int32_t dtype, void* out,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HCP_RING_H_ */

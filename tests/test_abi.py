@@ -1,0 +1,75 @@
+"""C-ABI checks that need no GPU: the library loads, exports what the header declares,
+and validates arguments before touching a device."""
+import ctypes
+import math
+
+import pytest
+import torch
+
+import hcp_ring_amd as H
+
+
+def test_library_exports_every_header_function(hcp):
+    names = hcp.header_functions()
+    assert len(names) >= 14
+    lib = ctypes.CDLL(hcp.LIB_PATH)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version(hcp):
+    assert hcp.lib().hcp_ring_abi_version() == 1
+
+
+def test_null_descriptor_is_invalid(hcp):
+    v = hcp.View(0, 0, 1)
+    rc = hcp.lib().hcp_ring_block_partial(None, v, v, v, None, None, None)
+    assert rc == -6
+    assert "null descriptor" in hcp.last_error()
+
+
+def test_bad_head_ratio_is_invalid(hcp):
+    d = hcp.BlockDesc(2, 6, 4, 128, 8, 8, 0, 0, 1, 0, 0.1)
+    v = hcp.View(16, 0, 128)
+    rc = hcp.lib().hcp_ring_block_partial(ctypes.byref(d), v, v, v, ctypes.c_void_p(16),
+                                          ctypes.c_void_p(16), None)
+    assert rc == -6 and "multiple of num_kv_heads" in hcp.last_error()
+
+
+def test_merge_rejects_too_many_parts(hcp):
+    v = hcp.View(16, 0, 128)
+    rc = hcp.lib().hcp_ring_lse_merge(65, None, None, 1, 1, 128, 2, v, None, None)
+    assert rc == -6
+
+
+def test_paged_rejects_short_table(hcp):
+    pool = hcp.PagedPool(16, 8, 16, 8, 128, 2)
+    v = hcp.View(16, 128, 128 * 8)
+    rc = hcp.lib().hcp_paged_kv_gather(ctypes.byref(pool), ctypes.c_void_p(16), 2, 0, 0, 40, v, v, None)
+    assert rc == -6 and "too short" in hcp.last_error()
+
+
+def test_replay_workspace_size_matches_plan(hcp):
+    chunks = [12288, 8192, 8192, 4096]
+    n = hcp.replay_workspace_size(torch.bfloat16, 32, 8, 128, chunks)
+    # 10 non-empty (target, source) pairs; per pair o [32, L, 128] + lse [32, L] fp32.
+    rows = 32 * (12288 + 2 * 8192 + 3 * 8192 + 4 * 4096)
+    assert n == rows * 128 * 4 + rows * 4
+    assert hcp.replay_workspace_size(torch.bfloat16, 32, 8, 128, [5, 0]) == 0
+
+
+def test_vanilla_helpers_known_answers(hcp):
+    # strategy.rs:157-163 (vanilla [3,1] -> [0,0,0,1]); reference_algo.rs:92-116 chunk sum.
+    assert hcp.vanilla_assignment([3, 1]) == [0, 0, 0, 1]
+    assert hcp.vanilla_offsets([640, 384], 1024) == [0, 640]
+    with pytest.raises(ValueError):
+        hcp.vanilla_offsets([640, 383], 1024)
+    assert hcp.ring_sources(1, 4) == [1, 0, 3, 2]
+
+
+def test_device_count_without_gpu(hcp):
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    c = ctypes.c_int(-1)
+    assert hcp.lib().hcp_ring_device_count(ctypes.byref(c)) == -5
+    assert c.value == 0

@@ -1,0 +1,298 @@
+"""GPU parity tests: every kernel through the C ABI against the oracle on identical
+seeded inputs.
+
+Tolerances: attention outputs max-abs <= 2e-2, LSE (fp32)
+max-abs <= 1e-3 against the same algorithm on exact fp32 upcasts of the bf16 inputs;
+paged gather/scatter bit-exact.  The fp32 path is held to the reference's Relaxed tier
+(1e-4, rust/src/error.rs:56-76).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import hcp_ring_amd as H
+from oracle import clib, closed_form as C, inputs as I, tch_ring as T
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 2e-2
+LSE_TOL = 1e-3
+
+
+def dev_bits(bits: np.ndarray, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(dtype).cuda()
+
+
+def draw(seed, shapes, dtype):
+    """Seeded inputs: (device tensors, fp32 upcasts as numpy)."""
+    if dtype == torch.float32:
+        arrs = clib.draw_normals(seed, shapes, "fp32")
+        return [torch.from_numpy(a).cuda() for a in arrs], arrs
+    if dtype == torch.float16:
+        arrs = clib.draw_normals(seed, shapes, "fp32")
+        t = [torch.from_numpy(a).to(torch.float16) for a in arrs]
+        return [x.cuda() for x in t], [x.float().numpy() for x in t]
+    bits = clib.draw_normals(seed, shapes, "bf16")
+    return [dev_bits(b) for b in bits], [I.bf16_bits_to_f32(b) for b in bits]
+
+
+def bhsd(x32):
+    return torch.from_numpy(np.ascontiguousarray(x32)).permute(1, 0, 2).unsqueeze(0)
+
+
+BLOCK_CASES = [
+    # name, Lq, Lk, Hq, Hkv, D, q_off, k_off, causal, dtype
+    ("diag_gqa4", 200, 200, 8, 2, 128, 0, 0, True, torch.bfloat16),
+    ("full_past", 130, 250, 8, 2, 128, 300, 0, True, torch.bfloat16),
+    ("partly_future", 200, 100, 8, 2, 128, 0, 50, True, torch.bfloat16),
+    ("wholly_future", 64, 64, 4, 1, 128, 0, 1000, True, torch.bfloat16),
+    ("noncausal", 100, 333, 4, 4, 128, 0, 0, False, torch.bfloat16),
+    ("gqa8_qwen", 96, 517, 16, 2, 128, 600, 100, True, torch.bfloat16),
+    ("mha_d64_f16", 300, 300, 4, 4, 64, 77, 77, True, torch.float16),
+    ("diag_unaligned_offsets", 257, 260, 8, 8, 128, 1003, 1000, True, torch.bfloat16),
+    ("fp32_general_d64", 150, 150, 8, 8, 64, 0, 0, True, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_CASES, ids=[c[0] for c in BLOCK_CASES])
+def test_block_partial_matches_oracle(gpu, case):
+    name, lq, lk, hq, hkv, d, qo, ko, causal, dt = case
+    (q, k, v), (q32, k32, v32) = draw(len(name) * 7 + lq, [(lq, hq, d), (lk, hkv, d), (lk, hkv, d)], dt)
+    scale = 1 / math.sqrt(d)
+    o, lse = H.block_partial(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), qo, ko,
+                             causal=causal, scale=scale)
+    torch.cuda.synchronize()
+    o, lse = o.cpu().numpy(), lse.cpu().numpy()
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, np.arange(qo, qo + lq), np.arange(ko, ko + lk), scale,
+                                   causal=causal)
+    ref_o, ref_l = ref_o.transpose(1, 0, 2), ref_l.T
+    assert np.array_equal(np.isneginf(lse), np.isneginf(ref_l))
+    fin = np.isfinite(ref_l)
+    tol = 1e-4 if dt == torch.float32 else OUT_TOL
+    assert np.abs(o - ref_o).max() <= tol
+    assert np.abs(lse[fin] - ref_l[fin]).max() <= (1e-4 if dt == torch.float32 else LSE_TOL)
+    assert np.all(o[~fin] == 0)
+    # the op-for-op restatement on fp32 upcasts agrees as well
+    if causal:
+        to, tl = T.positioned_local_compact_partial(scale, bhsd(q32), torch.arange(qo, qo + lq),
+                                                    bhsd(k32), bhsd(v32), torch.arange(ko, ko + lk))
+        tl = tl[0].numpy()
+        assert np.abs(o - to[0].numpy()).max() <= tol
+        assert np.abs(lse[fin] - tl[fin]).max() <= LSE_TOL
+
+
+def test_block_partial_head_major_and_unaligned_views(gpu):
+    (q, k, v), (q32, k32, v32) = draw(5, [(96, 4, 130), (96, 4, 130), (96, 4, 130)], torch.bfloat16)
+    # [L, H, 130] sliced to D=128: seq stride 520 is not a multiple of 8 -> general kernel.
+    qs, ks, vs = (x[:, :, :128].permute(1, 0, 2) for x in (q, k, v))
+    o1, l1 = H.block_partial(qs, ks, vs, 0, 0)
+    # the same data head-major contiguous -> matrix-core kernel
+    o2, l2 = H.block_partial(qs.contiguous(), ks.contiguous(), vs.contiguous(), 0, 0)
+    torch.cuda.synchronize()
+    ref_o, ref_l = C.attention_f64(q32[:, :, :128], k32[:, :, :128], v32[:, :, :128], np.arange(96),
+                                   np.arange(96), 1 / math.sqrt(128))
+    for o, l in ((o1, l1), (o2, l2)):
+        assert np.abs(o.cpu().numpy() - ref_o.transpose(1, 0, 2)).max() <= OUT_TOL
+        assert np.abs(l.cpu().numpy() - ref_l.T).max() <= LSE_TOL
+
+
+def test_block_partial_accumulate_is_positioned_merge(gpu):
+    # ring.rs:574-603: (o, lse) of source A merged in place with source B.
+    (q, k, v), (q32, k32, v32) = draw(11, [(150, 8, 128), (400, 2, 128), (400, 2, 128)], torch.bfloat16)
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    o, l = H.positioned_local_compact_partial(qh, 300, kh[:, 250:], vh[:, 250:], 250)
+    o2, l2 = H.positioned_merge_compact_partial(qh, 300, o, l, kh[:, :250], vh[:, :250], 0)
+    torch.cuda.synchronize()
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, np.arange(300, 450), np.arange(400), 1 / math.sqrt(128))
+    assert np.abs(o2.cpu().numpy() - ref_o.transpose(1, 0, 2)).max() <= OUT_TOL
+    assert np.abs(l2.cpu().numpy() - ref_l.T).max() <= LSE_TOL
+
+
+def test_lse_merge_matches_closed_form(gpu):
+    rng = np.random.default_rng(4)
+    h, l, d, n = 8, 333, 128, 5
+    os_ = [rng.standard_normal((h, l, d)).astype(np.float32) for _ in range(n)]
+    ls = [rng.normal(3.0, 2.0, (h, l)).astype(np.float32) for _ in range(n)]
+    ls[1][:, :40] = -np.inf       # an empty partial on some rows
+    for x in ls:
+        x[0, 100] = -np.inf       # a row with no keys at all
+    os_[1][:, :40] = 0
+    for x in os_:
+        x[0, 100] = 0
+    out, lse = H.lse_merge([torch.from_numpy(x).cuda() for x in os_], [torch.from_numpy(x).cuda() for x in ls],
+                           out_dtype=torch.bfloat16)
+    out32, lse32 = H.lse_merge([torch.from_numpy(x).cuda() for x in os_], [torch.from_numpy(x).cuda() for x in ls],
+                               out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref_o, ref_l = C.merge_partials_f64(os_, ls)
+    assert np.abs(out32.cpu().numpy() - ref_o).max() < 1e-5
+    assert np.abs(out.float().cpu().numpy() - ref_o).max() <= 1e-2
+    lse = lse.cpu().numpy()
+    assert lse[0, 100] == -np.inf and np.all(out.float().cpu().numpy()[0, 100] == 0)
+    fin = np.isfinite(ref_l)
+    assert np.abs(lse[fin] - ref_l[fin]).max() < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_paged_gather_scatter_bit_exact(gpu, dtype):
+    nb, bs, hkv, d = 96, 16, 8, 128
+    rng = np.random.default_rng(6)
+    if dtype == torch.bfloat16:
+        pool_np = rng.integers(0, 2**16, size=(2, nb, bs, hkv, d), dtype=np.uint16)
+        pool = torch.from_numpy(pool_np.view(np.int16)).view(torch.bfloat16).cuda()
+    else:
+        pool_np = rng.standard_normal((2, nb, bs, hkv, d)).astype(np.float32)
+        pool = torch.from_numpy(pool_np).cuda()
+    table_np = I.permuted_block_table(7, nb)[:40]
+    table = torch.from_numpy(table_np).cuda()
+    off, t0, t1 = 32, 45, 590  # unaligned range, table starting at global position 32
+    k, v = H.paged_kv_gather(pool, table, off, t0, t1)
+    torch.cuda.synchronize()
+    rk, rv = clib.paged_gather(pool_np, table_np, off, t0, t1)
+    view_np = lambda x: x.cpu().view(torch.int16 if dtype == torch.bfloat16 else torch.int32).numpy()
+    assert np.array_equal(view_np(k), rk.view(np.int16 if dtype == torch.bfloat16 else np.int32))
+    assert np.array_equal(view_np(v), rv.view(np.int16 if dtype == torch.bfloat16 else np.int32))
+    # scatter new data back (zero tail) and compare the whole pool with the oracle's scatter
+    k2 = torch.flip(k, dims=[1]).contiguous()
+    v2 = torch.flip(v, dims=[1]).contiguous()
+    H.paged_kv_scatter(pool, table, off, t0, t1, k2, v2, zero_tail=True)
+    torch.cuda.synchronize()
+    clib.paged_scatter(pool_np, table_np, off, t0, t1, _np_bits(k2), _np_bits(v2), zero_tail=True)
+    assert np.array_equal(_np_bits(pool), pool_np)
+    # gather(scatter(x)) == x
+    k3, v3 = H.paged_kv_gather(pool, table, off, t0, t1)
+    assert torch.equal(k3, k2) and torch.equal(v3, v2)
+    assert H.fetch_device_errors() == 0
+
+
+def _np_bits(t):
+    if t.dtype == torch.bfloat16:
+        return t.cpu().view(torch.int16).numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def test_paged_gather_strided_ring_buffer(gpu):
+    # gather straight into a token-major [L, Hkv, D] buffer (a strided [Hkv, L, D] view)
+    nb, bs, hkv, d = 16, 16, 4, 64
+    rng = np.random.default_rng(9)
+    pool_np = rng.integers(0, 2**16, size=(2, nb, bs, hkv, d), dtype=np.uint16)
+    pool = torch.from_numpy(pool_np.view(np.int16)).view(torch.bfloat16).cuda()
+    table_np = I.permuted_block_table(3, nb)
+    table = torch.from_numpy(table_np).cuda()
+    buf_k = torch.zeros(200, hkv, d, dtype=torch.bfloat16, device="cuda")
+    buf_v = torch.zeros(200, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.paged_kv_gather(pool, table, 0, 10, 210, buf_k.permute(1, 0, 2), buf_v.permute(1, 0, 2))
+    torch.cuda.synchronize()
+    rk, rv = clib.paged_gather(pool_np, table_np, 0, 10, 210)
+    assert np.array_equal(_np_bits(buf_k.permute(1, 0, 2).contiguous()), rk)
+    assert np.array_equal(_np_bits(buf_v.permute(1, 0, 2).contiguous()), rv)
+
+
+def test_paged_bad_block_id_sets_device_flag(gpu):
+    pool = torch.zeros(2, 8, 16, 2, 64, dtype=torch.bfloat16, device="cuda")
+    table = torch.tensor([0, 99, 1], dtype=torch.int32, device="cuda")
+    H.fetch_device_errors()
+    k, v = H.paged_kv_gather(pool, table, 0, 0, 48)
+    assert H.fetch_device_errors() & 1
+    assert H.fetch_device_errors() == 0
+
+
+DECODE_CASES = [
+    # name, B, Hq, Hkv, D, bs, ctx, t0, t1, ragged
+    ("c4_shape_small", 4, 32, 8, 128, 16, 1024, 0, 1024, False),
+    ("middle_chunk", 3, 32, 8, 128, 16, 900, 320, 700, False),
+    ("ragged_lens", 5, 16, 4, 128, 32, 600, 100, 600, True),
+    ("d64_bs16", 2, 8, 2, 64, 16, 300, 7, 290, False),
+]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
+def test_paged_decode_matches_oracle(gpu, case):
+    name, b, hq, hkv, d, bs, ctx, t0, t1, ragged = case
+    nblk_seq = (ctx + bs - 1) // bs
+    nb = b * nblk_seq + 3
+    (q, kv), (q32, kv32) = draw(31 + b, [(b, hq, d), (2, nb, bs, hkv, d)], torch.bfloat16)
+    perm = I.permuted_block_table(40 + b, nb)
+    tables_np = perm[: b * nblk_seq].reshape(b, nblk_seq)
+    tables = torch.from_numpy(np.ascontiguousarray(tables_np)).cuda()
+    lens_np = np.array([ctx - 37 * i for i in range(b)], dtype=np.int32) if ragged else None
+    lens = torch.from_numpy(lens_np).cuda() if ragged else None
+    o, lse = H.decode_local_compact_partial(q, kv, tables, t0, t1, seq_lens=lens)
+    torch.cuda.synchronize()
+    o, lse = o.cpu().numpy(), lse.cpu().numpy()
+    scale = 1 / math.sqrt(d)
+    for i in range(b):
+        end = min(t1, int(lens_np[i])) if ragged else t1
+        kk, vv = clib.paged_gather(kv32, tables_np[i], 0, t0, end)
+        ref_o, ref_l = C.attention_f64(q32[i:i + 1], kk.transpose(1, 0, 2), vv.transpose(1, 0, 2),
+                                       np.zeros(1), np.zeros(end - t0), scale, causal=False)
+        assert np.abs(o[i] - ref_o[0]).max() <= OUT_TOL, name
+        assert np.abs(lse[i] - ref_l[0]).max() <= LSE_TOL, name
+        # op-for-op decode restatement (ring.rs:625-639) on fp32 upcasts
+        to, tl = T.decode_local_compact_partial(scale, bhsd(q32[i:i + 1]), bhsd(kk.transpose(1, 0, 2)),
+                                                bhsd(vv.transpose(1, 0, 2)))
+        assert np.abs(lse[i] - tl[0, :, 0].numpy()).max() <= LSE_TOL
+
+
+def test_synth_normals_match_oracle_generator(gpu):
+    for dtype, kind in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        n = 100_003
+        out = torch.empty(n, dtype=dtype, device="cuda")
+        H.synth_normals(44, 0, n, out)
+        part = torch.empty(1001, dtype=dtype, device="cuda")
+        H.synth_normals(44, 5001, 1001, part)  # odd offset: starts on a spare
+        torch.cuda.synchronize()
+        ref, = clib.draw_normals(44, [(n,)], kind)
+        got = _np_bits(out) if dtype == torch.bfloat16 else out.cpu().numpy()
+        mism = np.count_nonzero(got != ref)
+        assert mism <= n * 1e-4, mism  # device libm may differ from glibc in the last f64 ulp
+        assert torch.equal(part, out[5001:6002])
+
+
+RING_CASES = [
+    ("c1_fp32", [640, 384], 8, 8, 64, torch.float32, 42),
+    ("c2_small", [512, 320, 192], 16, 2, 128, torch.bfloat16, 43),
+    ("uneven4", [300, 77, 500, 123], 8, 2, 128, torch.bfloat16, 50),
+]
+
+
+@pytest.mark.parametrize("case", RING_CASES, ids=[c[0] for c in RING_CASES])
+def test_ring_replay_matches_tch_blockwise(gpu, case):
+    name, chunks, hq, hkv, d, dt, seed = case
+    s = sum(chunks)
+    (q, k, v), (q32, k32, v32) = draw(seed, [(s, hq, d), (s, hkv, d), (s, hkv, d)], dt)
+    scale = 1 / math.sqrt(d)
+    out, lse = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    lse = lse.cpu().numpy()
+    # the reference driver on fp32 upcasts (ring.rs:861-1398 restated op for op)
+    ro, rl = T.ring_attention_replay(scale, bhsd(q32), bhsd(k32), bhsd(v32), chunks, return_lse=True)
+    ro, rl = ro[0].numpy(), rl[0].numpy()
+    if dt == torch.float32:
+        assert np.abs(out - ro).max() <= 1e-4 and np.abs(out - ro).mean() <= 1e-5
+        assert np.abs(lse - rl).max() <= 1e-4
+    else:
+        assert np.abs(out - ro).max() <= OUT_TOL
+        assert np.abs(lse - rl).max() <= LSE_TOL
+        # and the reference's own dtype (bf16 state) within the bf16 output tolerance
+        rb = T.ring_attention_replay(scale, bhsd(q32).to(torch.bfloat16), bhsd(k32).to(torch.bfloat16),
+                                     bhsd(v32).to(torch.bfloat16), chunks)
+        assert np.abs(out - rb[0].float().numpy()).max() <= OUT_TOL
+
+
+def test_ring_replay_paged_matches_unpaged(gpu):
+    chunks = [256, 96, 160]
+    s, hq, hkv, d, bs = sum(chunks), 8, 2, 128, 16
+    (q, k, v), _ = draw(77, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
+    nb = s // bs + 5
+    table_np = I.permuted_block_table(78, nb)[: s // bs]
+    table = torch.from_numpy(table_np).cuda()
+    pool = torch.zeros(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.paged_kv_scatter(pool, table, 0, 0, s, k.permute(1, 0, 2), v.permute(1, 0, 2))
+    o1, l1 = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+    o2, l2 = H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, chunks)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
