@@ -1,0 +1,359 @@
+"""Benchmark of the MI355X ring-attention path (one GPU).
+
+Headline (BASELINE.json ``metric``): ring-prefill TFLOP/s at 32k on the Llama-3-8B
+shape (config c3: S=32768 in 4 uneven domains [12288, 8192, 8192, 4096], 32 query /
+8 KV heads, head_dim 128, bf16, causal).  One step = one full single-GPU ring replay
+(every domain's ring steps, one partial per (domain, source) pair, then the LSE
+merge) through ``hcp_ring_prefill_replay``, inputs resident in HBM.  ``value`` counts
+algorithmic FLOPs of causal pairs only: 2 GEMMs x 2 x D x Hq x S(S+1)/2.
+
+Also reported on the same line: paged decode GB/s (config c4), KV staging gather GB/s
+and the staged 128k prefill (config c5), the LSE merge GB/s, a roofline object for the
+dominant kernel (the flash block kernel, from HIP events recorded by the replay
+driver on its launch stream over the timed region) and the CPU baseline (the oracle's
+op-for-op libtorch restatement of ring.rs timed on this host on a bounded sample).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "hetero-cp-ringattn_amd")
+
+METRIC = "ring-prefill TFLOP/s (% MFMA peak) at 32k; paged-decode GB/s (% HBM peak)"
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU (dense)
+PEAK_HBM_GBS = 8000.0
+
+C3 = dict(chunks=[12288, 8192, 8192, 4096], hq=32, hkv=8, d=128, seed=44)
+C4 = dict(batch=64, hq=32, hkv=8, d=128, bs=16, ctx=16384, chunks=[8192, 5120, 3072],
+          pool_blocks=65536, seed=45)
+C5 = dict(chunks=[21504, 13312, 18432, 23552, 24576, 9216, 8192, 12288], hq=32, hkv=8, d=128,
+          bs=16, seed=46)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def load_pkg():
+    spec = importlib.util.spec_from_file_location(
+        "hcp_ring_amd", os.path.join(PKG_DIR, "__init__.py"), submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["hcp_ring_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def causal_flops(seq: int, hq: int, d: int) -> float:
+    return 2.0 * d * hq * seq * (seq + 1)
+
+
+def synth_qkv(H, torch, seq, hq, hkv, d, seed):
+    """Q [S,Hq,D], K/V [S,Hkv,D] bf16 drawn Q, K, V from one LCG stream on the device."""
+    q = torch.empty(seq, hq, d, dtype=torch.bfloat16, device="cuda")
+    k = torch.empty(seq, hkv, d, dtype=torch.bfloat16, device="cuda")
+    v = torch.empty(seq, hkv, d, dtype=torch.bfloat16, device="cuda")
+    off = 0
+    for t in (q, k, v):
+        H.synth_normals(seed, off, t.numel(), t)
+        off += t.numel()
+    return q, k, v
+
+
+def lcg_permutation(seed: int, n: int):
+    """Fisher-Yates over range(n) driven by the 64-bit LCG's open-interval uniforms."""
+    a, c, mask = 6364136223846793005, 1442695040888963407, (1 << 64) - 1
+    s = seed
+    p = list(range(n))
+    for i in range(n - 1, 0, -1):
+        s = (s * a + c) & mask
+        u = ((s >> 11) + 0.5) / float(1 << 53)
+        j = int(u * (i + 1))
+        p[i], p[j] = p[j], p[i]
+    return p
+
+
+def time_cuda(torch, fn, reps: int) -> float:
+    """Mean ms per call between torch events on the current stream."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+# ------------------------------------------------------------------ c3 prefill ----
+def bench_prefill(H, torch, steps: int, warmup: int):
+    c = C3
+    seq = sum(c["chunks"])
+    q, k, v = synth_qkv(H, torch, seq, c["hq"], c["hkv"], c["d"], c["seed"])
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    ws = torch.empty(H.replay_workspace_size(torch.bfloat16, c["hq"], c["hkv"], c["d"], c["chunks"]),
+                     dtype=torch.uint8, device="cuda")
+    out = torch.empty(c["hq"], seq, c["d"], dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(c["hq"], seq, dtype=torch.float32, device="cuda")
+    step = lambda: H.ring_attention_replay(qh, kh, vh, c["chunks"], out=out, lse_out=lse, workspace=ws)
+    log(f"c3 prefill warmup x{warmup}")
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    H.replay_timing(True)
+    H.replay_timing_read()
+    log(f"c3 prefill timed x{steps}")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    tm = H.replay_timing_read()
+    H.replay_timing(False)
+    flops = causal_flops(seq, c["hq"], c["d"])
+    ms_step = elapsed * 1e3 / steps
+    tflops = flops / (ms_step * 1e-3) / 1e12
+    blk_ms, blk_n = tm["block"]
+    mrg_ms, mrg_n = tm["merge"]
+    per_launch_flops = flops * steps / blk_n
+    avg_blk_ms = blk_ms / blk_n
+    achieved = per_launch_flops / (avg_blk_ms * 1e-3) / 1e12
+    # merge: algorithmic bytes = partial o+lse reads + bf16 out + fp32 lse writes
+    n = len(c["chunks"])
+    offs = [sum(c["chunks"][:i]) for i in range(n)]
+    mbytes = 0
+    for t in range(n):
+        parts = sum(1 for s_ in range(n) if offs[s_] <= offs[t] + c["chunks"][t] - 1)
+        rows = c["hq"] * c["chunks"][t]
+        mbytes += rows * (parts * (4 * c["d"] + 4) + 2 * c["d"] + 4)
+    merge_gbs = mbytes * steps / (mrg_ms * 1e-3) / 1e9
+    finite = bool(torch.isfinite(lse).all().item()) and bool(torch.isfinite(out.float()).all().item())
+    del ws
+    return dict(ms_step=ms_step, tflops=tflops, flops=flops, blk_launches=blk_n // steps,
+                avg_blk_ms=avg_blk_ms, per_launch_flops=per_launch_flops, achieved=achieved,
+                merge_ms=mrg_ms / steps, merge_gbs=merge_gbs, merge_bytes=mbytes, finite=finite,
+                tensors=(q, k, v))
+
+
+# ------------------------------------------------------------------ c4 decode ----
+def bench_decode(H, torch, steps: int, warmup: int):
+    c = C4
+    nb, bs, hkv, d = c["pool_blocks"], c["bs"], c["hkv"], c["d"]
+    q = torch.empty(c["batch"], c["hq"], d, dtype=torch.bfloat16, device="cuda")
+    pool = torch.empty(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.synth_normals(c["seed"], 0, q.numel(), q)
+    H.synth_normals(c["seed"], q.numel(), pool.numel(), pool)
+    perm = lcg_permutation(c["seed"], nb)
+    per_seq = c["ctx"] // bs
+    tables = torch.tensor(perm[: c["batch"] * per_seq], dtype=torch.int32, device="cuda").view(c["batch"], per_seq)
+    bounds, acc = [], 0
+    for L in c["chunks"]:
+        bounds.append((acc, acc + L))
+        acc += L
+    outs = [(torch.empty(c["batch"], c["hq"], d, dtype=torch.float32, device="cuda"),
+             torch.empty(c["batch"], c["hq"], dtype=torch.float32, device="cuda")) for _ in bounds]
+    wss = [torch.empty(max(H.decode_workspace_size(q, pool, tables, t0, t1), 1), dtype=torch.uint8, device="cuda")
+           for t0, t1 in bounds]
+    final = torch.empty(c["batch"], c["hq"], d, dtype=torch.bfloat16, device="cuda")
+    final_lse = torch.empty(c["batch"], c["hq"], dtype=torch.float32, device="cuda")
+
+    def chunk(i):
+        t0, t1 = bounds[i]
+        H.decode_local_compact_partial(q, pool, tables, t0, t1, workspace=wss[i], o=outs[i][0], lse=outs[i][1])
+
+    def step():
+        for i in range(len(bounds)):
+            chunk(i)
+        # per-chunk partials merged across domains: rows = batch*Hq, one token each
+        H.lse_merge([o.view(-1, 1, d) for o, _ in outs],
+                    [l.view(-1, 1) for _, l in outs], out=final.view(-1, 1, d), lse_out=final_lse.view(-1, 1))
+
+    log(f"c4 decode warmup x{warmup}")
+    for _ in range(warmup):
+        step()
+    log(f"c4 decode timed x{steps}")
+    ms_step = time_cuda(torch, step, steps)
+    kv_bytes = 2 * c["batch"] * c["ctx"] * hkv * d * 2
+    alg_bytes = kv_bytes + q.numel() * 2 + c["batch"] * c["hq"] * (d + 1) * 4 * len(bounds) \
+        + tables.numel() * 4 + final.numel() * 2
+    # dominant kernel: the chunk-0 decode call (8192 keys of each sequence)
+    ms_c0 = time_cuda(torch, lambda: chunk(0), steps)
+    c0_bytes = 2 * c["batch"] * c["chunks"][0] * hkv * d * 2
+    res = dict(ms_step=ms_step, gbs=alg_bytes / (ms_step * 1e-3) / 1e9, bytes=alg_bytes,
+               chunk0_ms=ms_c0, chunk0_gbs=c0_bytes / (ms_c0 * 1e-3) / 1e9,
+               finite=bool(torch.isfinite(final.float()).all().item()))
+    del pool
+    return res
+
+
+# ------------------------------------------------------------------ c5 staging ----
+def bench_staged(H, torch, steps: int, warmup: int, full_prefill: bool = True):
+    c = C5
+    seq, hkv, d, bs = sum(c["chunks"]), c["hkv"], c["d"], c["bs"]
+    q, k, v = synth_qkv(H, torch, seq, c["hq"], hkv, d, c["seed"])
+    nb = seq // bs
+    perm = lcg_permutation(42, nb)
+    table = torch.tensor(perm, dtype=torch.int32, device="cuda")
+    pool = torch.zeros(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.paged_kv_scatter(pool, table, 0, 0, seq, k.permute(1, 0, 2), v.permute(1, 0, 2))
+    offs = [sum(c["chunks"][:i]) for i in range(len(c["chunks"]))]
+    stage_k = torch.empty(hkv, seq, d, dtype=torch.bfloat16, device="cuda")
+    stage_v = torch.empty(hkv, seq, d, dtype=torch.bfloat16, device="cuda")
+
+    def gather_all():
+        for o, L in zip(offs, c["chunks"]):
+            H.paged_kv_gather(pool, table, 0, o, o + L, stage_k[:, o:o + L], stage_v[:, o:o + L])
+
+    for _ in range(warmup):
+        gather_all()
+    ms = time_cuda(torch, gather_all, steps)
+    gbytes = 2 * seq * hkv * d * 2 * 2
+    exact = bool(torch.equal(stage_k.view(torch.int16), k.permute(1, 0, 2).contiguous().view(torch.int16))) and \
+        bool(torch.equal(stage_v.view(torch.int16), v.permute(1, 0, 2).contiguous().view(torch.int16)))
+    res = dict(gather_ms=ms, gather_gbs=gbytes / (ms * 1e-3) / 1e9, gather_bytes=gbytes, bit_exact=exact)
+    del stage_k, stage_v
+    if full_prefill:
+        ws = torch.empty(H.replay_workspace_size(torch.bfloat16, c["hq"], hkv, d, c["chunks"], paged=True),
+                         dtype=torch.uint8, device="cuda")
+        out = torch.empty(c["hq"], seq, d, dtype=torch.bfloat16, device="cuda")
+        lse = torch.empty(c["hq"], seq, dtype=torch.float32, device="cuda")
+        run = lambda: H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, c["chunks"], out=out,
+                                                    lse_out=lse, workspace=ws)
+        run()
+        reps = 2
+        ms_p = time_cuda(torch, run, reps)
+        res.update(prefill_ms=ms_p, prefill_tflops=causal_flops(seq, c["hq"], d) / (ms_p * 1e-3) / 1e12)
+        del ws
+    return res
+
+
+# ------------------------------------------------------------------ CPU baseline ----
+def cpu_baseline(torch, tensors, budget_s: float = 10.0):
+    """The oracle's op-for-op libtorch restatement of ring.rs (ring_attention driver,
+    process_kv_block folds, bf16 state, 2048 tiling, GQA-expand copies) on this host:
+    whole target domains of c3, in order 0, 1, 2, 3, until the budget is spent (at
+    least one).  value = algorithmic causal FLOPs of the completed domains / time."""
+    sys.path.insert(0, ROOT)
+    from oracle import tch_ring
+
+    c = C3
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    q, k, v = tensors
+    n = len(c["chunks"])
+    offs = [sum(c["chunks"][:i]) for i in range(n)]
+    rep = c["hq"] // c["hkv"]
+    scale = 1 / math.sqrt(c["d"])
+    qh = q.permute(1, 0, 2).unsqueeze(0).cpu()
+    kx = tch_ring.repeat_kv_heads(k.permute(1, 0, 2).unsqueeze(0).cpu(), rep)
+    vx = tch_ring.repeat_kv_heads(v.permute(1, 0, 2).unsqueeze(0).cpu(), rep)
+    sent = [tch_ring.local_micro_blocks(kx[:, :, o:o + L], vx[:, :, o:o + L], o, n)
+            for o, L in zip(offs, c["chunks"])]
+    flops, t_total, done = 0.0, 0.0, []
+    for d in range(n):
+        o, L = offs[d], c["chunks"][d]
+        rounds = [sent[(d - 1 - r) % n] for r in range(n - 1)]
+        t0 = time.perf_counter()
+        tch_ring.ring_attention(scale, qh[:, :, o:o + L], kx[:, :, o:o + L], vx[:, :, o:o + L],
+                                torch.arange(o, o + L), o, n, rounds)
+        t_total += time.perf_counter() - t0
+        # causal pairs of rows o..o+L-1: sum (p+1)
+        flops += 4.0 * c["d"] * c["hq"] * (L * o + L * (L + 1) / 2)
+        done.append(d)
+        log(f"cpu baseline domain {d}: {t_total:.1f}s")
+        if t_total >= budget_s:
+            break
+    return dict(value=flops / t_total / 1e12, unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"c3 ring_attention of target domains {done} (of 4), op-for-op libtorch restatement of "
+                       f"ring.rs:861-1398 (bf16 state, 2048 q/kv tiles, GQA-expanded K/V), {t_total:.1f} s; "
+                       f"algorithmic causal FLOPs of those domains / time")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
+    ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
+    args = ap.parse_args()
+    if args.only_prefill:
+        args.no_extra = args.no_cpu = True
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the ring is replayed on a single MI355X "
+              "(multi-GPU rings are a design note, not part of this build); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    H = load_pkg()
+    torch.cuda.set_device(0)
+    log(f"device {torch.cuda.get_device_name(0)}")
+    pre = bench_prefill(H, torch, args.steps, args.warmup)
+    log(f"c3 prefill {pre['tflops']:.1f} TFLOP/s ({pre['ms_step']:.3f} ms/step)")
+    extra = {}
+    if not args.no_extra:
+        dec = bench_decode(H, torch, args.steps, args.warmup)
+        log(f"c4 decode {dec['gbs']:.1f} GB/s")
+        stg = bench_staged(H, torch, args.steps, args.warmup)
+        log(f"c5 gather {stg['gather_gbs']:.1f} GB/s, prefill {stg.get('prefill_tflops', 0):.1f} TFLOP/s")
+        extra = dict(
+            paged_decode={"workload": "c4: B=64, ctx 16384 in [8192,5120,3072], 32q/8kv, D=128, bf16, bs=16",
+                          "value": round(dec["gbs"], 1), "unit": "GB/s", "ms_per_step": round(dec["ms_step"], 4),
+                          "frac_hbm": round(dec["gbs"] / PEAK_HBM_GBS, 4), "bytes": dec["bytes"],
+                          "chunk0_kernel_gbs": round(dec["chunk0_gbs"], 1), "finite": dec["finite"]},
+            kv_staging={"workload": "c5: gather of all 8 chunks (131072 tokens, 8 kv heads, D=128, bf16) from a "
+                                    "permuted bs=16 block pool",
+                        "value": round(stg["gather_gbs"], 1), "unit": "GB/s", "ms": round(stg["gather_ms"], 4),
+                        "frac_hbm": round(stg["gather_gbs"] / PEAK_HBM_GBS, 4), "bytes": stg["gather_bytes"],
+                        "bit_exact": stg["bit_exact"]},
+            staged_prefill_128k={"value": round(stg.get("prefill_tflops", 0.0), 1), "unit": "TFLOP/s",
+                                 "ms": round(stg.get("prefill_ms", 0.0), 3),
+                                 "frac_mfma": round(stg.get("prefill_tflops", 0.0) / PEAK_BF16_TFLOPS, 4)},
+            lse_merge={"value": round(pre["merge_gbs"], 1), "unit": "GB/s", "ms_per_step": round(pre["merge_ms"], 4),
+                       "frac_hbm": round(pre["merge_gbs"] / PEAK_HBM_GBS, 4), "bytes": pre["merge_bytes"]},
+        )
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, pre["tensors"])
+        log(f"cpu baseline {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": round(pre["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["ms_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (LCG + Box-Muller normals, seed 44, generated on the device)",
+        "config": {"workload": "c3_llama3_8b_ring_prefill_32k", "chunks": C3["chunks"], "num_q_heads": C3["hq"],
+                   "num_kv_heads": C3["hkv"], "head_dim": C3["d"], "causal": True,
+                   "flops_per_step": pre["flops"], "frac_mfma_peak": round(pre["tflops"] / PEAK_BF16_TFLOPS, 4)},
+        "roofline": {"bound": "mfma", "kernel": "flash_block_kernel",
+                     "achieved": round(pre["achieved"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(pre["achieved"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "launches_per_step": pre["blk_launches"], "avg_launch_ms": round(pre["avg_blk_ms"], 4),
+                     "flops_per_launch": pre["per_launch_flops"]},
+        "cpu_baseline": cpu,
+        "finite": pre["finite"],
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

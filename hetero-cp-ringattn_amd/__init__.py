@@ -118,6 +118,9 @@ def lib() -> ctypes.CDLL:
                                            ctypes.POINTER(PagedPool), vp, i64, View, vp, vp,
                                            ctypes.c_size_t, vp], ctypes.c_int),
         "hcp_synth_normals": ([ctypes.c_uint64, i64, i64, i32, vp, vp], ctypes.c_int),
+        "hcp_ring_replay_timing": ([i32], ctypes.c_int),
+        "hcp_ring_replay_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)],
+                                        ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -375,6 +378,19 @@ def synth_normals(seed: int, offset: int, count: int, out, stream=None):
     _check(lib().hcp_synth_normals(ctypes.c_uint64(seed), offset, count, dtype_code(out.dtype),
                                    _ptr(out), _stream(stream)))
     return out
+
+
+def replay_timing(enable: bool) -> None:
+    """Turn per-launch HIP-event timing of the replay driver on or off."""
+    _check(lib().hcp_ring_replay_timing(1 if enable else 0))
+
+
+def replay_timing_read() -> dict:
+    """Summed kernel ms and launch counts since the last read: block, merge, gather."""
+    ms = (ctypes.c_double * 3)()
+    n = (ctypes.c_int64 * 3)()
+    _check(lib().hcp_ring_replay_timing_read(ms, n))
+    return {k: (ms[i], n[i]) for i, k in enumerate(("block", "merge", "gather"))}
 
 
 def vanilla_offsets(chunks, seq_len: int | None = None) -> list[int]:

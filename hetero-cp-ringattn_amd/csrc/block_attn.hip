@@ -114,6 +114,26 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 
 }  // namespace
 
+// Raw buffer resource over [base, base + bytes): loads past the end return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int32_t n = bytes <= 0 ? 0 : (bytes > 0x7ffffff0LL ? 0x7ffffff0 : static_cast<int32_t>(bytes));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// {x[lane], x[lane ^ 32]} in some order, on the VALU (no LDS round trip).
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int D, int DT, int G>
 __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
   using Ops = MfmaOps<DT>;
@@ -137,7 +157,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
   const int hg = logical % a.n_groups;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  // Wave index as a scalar: everything derived from it stays in SGPRs.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int lcol = lane & 31;   // query column owned by this lane
   const int lhalf = lane >> 5;  // 0/1: which 8-wide k slice this lane feeds
@@ -157,16 +178,14 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
   }
   const int n_tiles = (n_kv + kBK - 1) / kBK;
 
-  // Q^T fragments (B operand): Q[my_q][lhalf*8 + 16*s .. +8].
+  // Q^T fragments (B operand): Q[my_q][lhalf*8 + 16*s .. +8]; rows past lq read zeros.
   frag qf[KS];
   {
-    const bool ok = my_q < a.lq;
-    const uint16_t* qp = a.q + head * a.q_hs + static_cast<int64_t>(ok ? my_q : 0) * a.q_ss + lhalf * 8;
+    const uint16_t* qbase = a.q + head * a.q_hs + static_cast<int64_t>(wq0) * a.q_ss;
+    const auto qr = make_rsrc(qbase, static_cast<int64_t>(a.lq - wq0) * a.q_ss * 2);
+    const int32_t qoff = (lcol * static_cast<int32_t>(a.q_ss) + lhalf * 8) * 2;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      u32x4 raw = ok ? *reinterpret_cast<const u32x4*>(qp + 16 * s) : u32x4{0, 0, 0, 0};
-      qf[s] = as_frag<frag>(raw);
-    }
+    for (int s = 0; s < KS; ++s) qf[s] = as_frag<frag>(buf_load16(qr, qoff + 32 * s));
   }
 
   f32x16 oacc[DB];
@@ -174,11 +193,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
   for (int b = 0; b < DB; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
-  float m_run = kInitMax;
-  float l_run = 0.f;
+  float m_run = kInitMax;  // reference max, log2 domain (scaled)
+  float l_run = 0.f;       // this lane's partial row sum
 
-  // ---- loader roles: threads [0,256) stage K, [256,512) stage V (transposed) ----
-  const bool k_loader = tid < 256;
+  // ---- loader roles: waves 0-3 stage K, waves 4-7 stage V (transposed) ----
+  const bool k_loader = wave < 4;
   const int lt = tid & 255;
   const uint16_t* kbase = a.k + kvh * a.k_hs;
   const uint16_t* vbase = a.v + kvh * a.v_hs;
@@ -186,26 +205,30 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
   const int v_rg = lt % (kBK / 4);
   const int v_dc = lt / (kBK / 4);
   const bool v_active = !k_loader && lt < V_ITEMS;
+  // Byte offsets within a tile (tile base = row kv0).
+  int32_t ld_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (k_loader) {
+      const int c = lt + 256 * (i < K_LOADS ? i : 0);
+      ld_off[i] = ((c / KCH) * static_cast<int32_t>(a.k_ss) + (c % KCH) * 8) * 2;
+    } else {
+      ld_off[i] = ((v_rg * 4 + i) * static_cast<int32_t>(a.v_ss) + v_dc * 8) * 2;
+    }
+  }
+  const uint16_t* ld_base = k_loader ? kbase : vbase;
+  const int64_t ld_ss = k_loader ? a.k_ss : a.v_ss;
 
   u32x4 stage[4];
   auto load_tile = [&](int t) {
     const int kv0 = t * kBK;
+    const auto r = make_rsrc(ld_base + kv0 * ld_ss, static_cast<int64_t>(a.lk - kv0) * ld_ss * 2);
     if (k_loader) {
 #pragma unroll
-      for (int i = 0; i < K_LOADS; ++i) {
-        const int c = lt + 256 * i;
-        const int row = c / KCH, ch = c % KCH;
-        const int kv = kv0 + row;
-        stage[i] = kv < a.lk ? *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(kv) * a.k_ss + ch * 8)
-                             : u32x4{0, 0, 0, 0};
-      }
+      for (int i = 0; i < K_LOADS; ++i) stage[i] = buf_load16(r, ld_off[i]);
     } else if (v_active) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kv = kv0 + v_rg * 4 + i;
-        stage[i] = kv < a.lk ? *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(kv) * a.v_ss + v_dc * 8)
-                             : u32x4{0, 0, 0, 0};
-      }
+      for (int i = 0; i < 4; ++i) stage[i] = buf_load16(r, ld_off[i]);
     }
   };
   auto store_tile = [&](int buf) {
@@ -221,14 +244,14 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 #pragma unroll
       for (int dd = 0; dd < 8; ++dd) {
         const int w = dd >> 1;
-        const int sh = (dd & 1) * 16;
-        const uint32_t e0 = (stage[0][w] >> sh) & 0xffffu;
-        const uint32_t e1 = (stage[1][w] >> sh) & 0xffffu;
-        const uint32_t e2 = (stage[2][w] >> sh) & 0xffffu;
-        const uint32_t e3 = (stage[3][w] >> sh) & 0xffffu;
         u32x2 pk;
-        pk[0] = e0 | (e1 << 16);
-        pk[1] = e2 | (e3 << 16);
+        if (dd & 1) {
+          pk[0] = __builtin_amdgcn_perm(stage[1][w], stage[0][w], 0x07060302u);
+          pk[1] = __builtin_amdgcn_perm(stage[3][w], stage[2][w], 0x07060302u);
+        } else {
+          pk[0] = __builtin_amdgcn_perm(stage[1][w], stage[0][w], 0x05040100u);
+          pk[1] = __builtin_amdgcn_perm(stage[3][w], stage[2][w], 0x05040100u);
+        }
         *reinterpret_cast<u32x2*>(&vt_lds[buf][(v_dc * 8 + dd) * kVtStride + v_rg * 4]) = pk;
       }
     }
@@ -238,23 +261,27 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
     load_tile(0);
     store_tile(0);
   }
+  // Q fragments and tile 0 are resident before the loop: the prefetch issued inside
+  // the loop is then the only outstanding memory traffic during the MFMA section.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   const int krow0 = kperm(lcol);  // permuted K row fed by this lane (within a 32-block)
-  const int64_t qpos = a.q_off + my_q;
-  const int64_t wave_qpos0 = a.q_off + wq0;
-  const int64_t wave_qpos_last = a.q_off + min(wq0 + 31, a.lq - 1);
+  const float c = a.scale_log2;
+  // Causal limit of this lane relative to key 0 of the chunk: key j visible iff j <= qlim.
+  const int64_t qlim64 = a.q_off + my_q - a.k_off;
+  const int64_t wave_lim_first = a.q_off + wq0 - a.k_off;                  // first row of the wave
+  const int64_t wave_lim_last = a.q_off + min(wq0 + 31, a.lq - 1) - a.k_off;  // last row
 
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < n_tiles) load_tile(t + 1);
 
     const int kv0 = t * kBK;
-    const int64_t kpos0 = a.k_off + kv0;
     // Skip tiles wholly in this wave's future (causal) -- other waves may need them.
-    const bool wave_live = !a.causal || kpos0 <= wave_qpos_last;
+    const bool wave_live = !a.causal || kv0 <= wave_lim_last;
     if (wave_live && wq0 < a.lq) {
-      const bool need_mask = (kv0 + kBK > a.lk) || (a.causal && kpos0 + kBK - 1 > wave_qpos0);
+      const bool need_mask = (kv0 + kBK > a.lk) || (a.causal && kv0 + kBK - 1 > wave_lim_first);
 
       // ---- S^T = K Q^T for two 32-key blocks ----
       f32x16 sacc[2];
@@ -272,24 +299,27 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
         }
       }
 
-      // ---- scale (log2 domain), mask, tile row max ----
+      // ---- mask (boundary tiles only), tile row max on raw scores ----
+      if (need_mask) {
+        // key kv0 + kl visible iff kl <= lim (kl = tile-local key index).
+        int64_t lim64 = a.lk - 1 - kv0;
+        if (a.causal) lim64 = min(lim64, qlim64 - kv0);
+        const int lim = static_cast<int>(max(min(lim64, static_cast<int64_t>(kBK)), static_cast<int64_t>(-1))) - 8 * lhalf;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int j = r >> 2, i = r & 3;
+            const int kl0 = 32 * b + 16 * (j >> 1) + 4 * (j & 1) + i;  // kl minus 8*lhalf
+            sacc[b][r] = kl0 <= lim ? sacc[b][r] : -INFINITY;
+          }
+      }
       float tmax = -INFINITY;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = sacc[b][r] * a.scale_log2;
-          if (need_mask) {
-            const int j = r >> 2, i = r & 3;
-            const int key = kv0 + 32 * b + kperm(j * 8 + lhalf * 4 + i);
-            const bool vis = key < a.lk && (!a.causal || qpos >= a.k_off + key);
-            x = vis ? x : -INFINITY;
-          }
-          sacc[b][r] = x;
-          tmax = fmaxf(tmax, x);
-        }
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[b][r]);
+      tmax = max_xor32(tmax) * c;
 
       // ---- lazy rescale: move the reference max only when it grows by > 8 ----
       const bool grow = tmax > m_run + kRescaleThreshold;
@@ -304,14 +334,14 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
         m_run = m_new;
       }
 
-      // ---- P = 2^(s - m), row-sum partial, P^T as bf16 B operands ----
+      // ---- P = 2^(s*c - m) as 16-bit B operands, row-sum partial ----
       frag pf[4];
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         float p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          p[r] = __builtin_amdgcn_exp2f(sacc[b][r] - m_run);
+          p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][r], c, -m_run));
           l_run += p[r];
         }
         pf[2 * b] = Ops::pack(p);
@@ -336,7 +366,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 
   // ---- epilogue: normalise, LSE (natural log), optional merge with running partial ----
   if (my_q >= a.lq) return;
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = sum_xor32(l_run);
   const bool any = l_tot > 0.f;
   const float inv = any ? 1.f / l_tot : 0.f;
   const float lse_new = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;

@@ -134,6 +134,46 @@ struct ReplayPlan {
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+// Optional per-launch timing of the replay driver: HIP events recorded on the launch
+// stream around every block-kernel, merge and gather launch (benchmark instrumentation).
+enum TimedKind { kTimedBlock = 0, kTimedMerge = 1, kTimedGather = 2, kTimedKinds = 3 };
+struct ReplayTiming {
+  std::mutex mu;
+  bool enabled = false;
+  std::vector<hipEvent_t> pool;
+  std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
+};
+ReplayTiming& timing() {
+  static ReplayTiming t;
+  return t;
+}
+hipEvent_t take_event(ReplayTiming& t) {
+  if (!t.pool.empty()) {
+    hipEvent_t e = t.pool.back();
+    t.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  HCP_HIP(hipEventCreate(&e));
+  return e;
+}
+// Runs `launch` bracketed by events when timing is on.
+template <typename F>
+void timed(int kind, hipStream_t stream, F&& launch) {
+  ReplayTiming& t = timing();
+  std::unique_lock<std::mutex> lock(t.mu);
+  if (!t.enabled) {
+    lock.unlock();
+    launch();
+    return;
+  }
+  hipEvent_t a = take_event(t), b = take_event(t);
+  HCP_HIP(hipEventRecord(a, stream));
+  launch();
+  HCP_HIP(hipEventRecord(b, stream));
+  t.pending.push_back({kind, {a, b}});
+}
+
 ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
   require(d != nullptr, "null descriptor");
   require(d->num_domains >= 1 && d->num_domains <= 64, "num_domains must be in [1, 64]");
@@ -228,9 +268,11 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
         kv_v.data = stg + p.staging_bytes_per_domain / 2;
         kv_v.head_stride = hs * d->head_dim;
         kv_v.seq_stride = d->head_dim;
-        launch_paged_copy(true, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads,
-                          pool->head_dim, pool->elem_bytes, table, 0, p.off[src], p.off[src] + p.len[src],
-                          kv_k.data, kv_v.data, kv_k.head_stride, kv_k.seq_stride, 0, err, stream);
+        timed(kTimedGather, stream, [&] {
+          launch_paged_copy(true, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads,
+                            pool->head_dim, pool->elem_bytes, table, 0, p.off[src], p.off[src] + p.len[src],
+                            kv_k.data, kv_v.data, kv_k.head_stride, kv_k.seq_stride, 0, err, stream);
+        });
       } else {
         kv_k.data = static_cast<char*>(k.data) + p.off[src] * k.seq_stride * es;
         kv_v.data = static_cast<char*>(v.data) + p.off[src] * v.seq_stride * es;
@@ -253,7 +295,8 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
       const size_t rows = static_cast<size_t>(d->num_q_heads) * p.len[t];
       float* po = reinterpret_cast<float*>(part);
       float* pl = reinterpret_cast<float*>(part + align256(rows * d->head_dim * sizeof(float)));
-      launch_block_partial(make_launch(&bd, qv, kv_k, kv_v, po, pl), stream);
+      const BlockLaunch L = make_launch(&bd, qv, kv_k, kv_v, po, pl);
+      timed(kTimedBlock, stream, [&] { launch_block_partial(L, stream); });
     }
   }
   // Final merge per target domain into the output rows [off_t, off_t + len_t).
@@ -266,9 +309,11 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
       ls.push_back(reinterpret_cast<const float*>(part + align256(rows * d->head_dim * sizeof(float))));
     }
     char* o_ptr = static_cast<char*>(out.data) + p.off[t] * out.seq_stride * es;
-    launch_lse_merge(static_cast<int>(os.size()), os.data(), ls.data(), d->num_q_heads, p.len[t],
-                     d->head_dim, d->dtype, o_ptr, out.head_stride, out.seq_stride,
-                     lse_out ? lse_out + p.off[t] : nullptr, p.seq, stream);
+    timed(kTimedMerge, stream, [&] {
+      launch_lse_merge(static_cast<int>(os.size()), os.data(), ls.data(), d->num_q_heads, p.len[t],
+                       d->head_dim, d->dtype, o_ptr, out.head_stride, out.seq_stride,
+                       lse_out ? lse_out + p.off[t] : nullptr, p.seq, stream);
+    });
   }
 }
 
@@ -440,6 +485,36 @@ int hcp_ring_prefill_replay_paged(const hcp_ring_replay_desc* desc, hcp_ring_vie
     hcp_ring_view none{nullptr, 0, 1};
     run_replay(desc, q, none, none, pool, block_table, table_len, out, lse_out, workspace, workspace_bytes,
                as_stream(stream));
+  });
+}
+
+int hcp_ring_replay_timing(int32_t enable) {
+  return guarded(__func__, [&] {
+    ReplayTiming& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    t.enabled = enable != 0;
+  });
+}
+
+int hcp_ring_replay_timing_read(double* ms, int64_t* launches) {
+  return guarded(__func__, [&] {
+    require(ms != nullptr && launches != nullptr, "null output arrays");
+    ReplayTiming& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    for (int k = 0; k < kTimedKinds; ++k) {
+      ms[k] = 0.0;
+      launches[k] = 0;
+    }
+    for (auto& e : t.pending) {
+      HCP_HIP(hipEventSynchronize(e.second.second));
+      float el = 0.f;
+      HCP_HIP(hipEventElapsedTime(&el, e.second.first, e.second.second));
+      ms[e.first] += el;
+      launches[e.first] += 1;
+      t.pool.push_back(e.second.first);
+      t.pool.push_back(e.second.second);
+    }
+    t.pending.clear();
   });
 }
 

@@ -250,6 +250,19 @@ int hcp_ring_prefill_replay_paged(const hcp_ring_replay_desc* desc, hcp_ring_vie
                                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * Replay kernel timing (no reference counterpart; benchmark instrumentation; the
+ * reference logs wall-clock compute per phase to HCP_PERF_LOG, ring.rs:820-844).
+ *
+ * With timing enabled, the replay driver brackets every block-kernel (kind 0), merge
+ * (kind 1) and paged-gather (kind 2) launch with HIP events on the launch stream.
+ * hcp_ring_replay_timing_read waits for the recorded events, writes the summed kernel
+ * milliseconds and launch counts per kind into ms[3] / launches[3], and clears them.
+ * ------------------------------------------------------------------------------- */
+int hcp_ring_replay_timing(int32_t enable);
+
+int hcp_ring_replay_timing_read(double* ms, int64_t* launches);
+
+/* ---------------------------------------------------------------------------------
  * Synthetic inputs (no reference counterpart; used by the benchmark).
  *
  * Writes normals n = offset .. offset+count-1 of the LCG + Box-Muller stream of

@@ -72,7 +72,8 @@ def test_block_partial_matches_oracle(gpu, case):
     fin = np.isfinite(ref_l)
     tol = 1e-4 if dt == torch.float32 else OUT_TOL
     assert np.abs(o - ref_o).max() <= tol
-    assert np.abs(lse[fin] - ref_l[fin]).max() <= (1e-4 if dt == torch.float32 else LSE_TOL)
+    if fin.any():
+        assert np.abs(lse[fin] - ref_l[fin]).max() <= (1e-4 if dt == torch.float32 else LSE_TOL)
     assert np.all(o[~fin] == 0)
     # the op-for-op restatement on fp32 upcasts agrees as well
     if causal:
@@ -80,7 +81,8 @@ def test_block_partial_matches_oracle(gpu, case):
                                                     bhsd(k32), bhsd(v32), torch.arange(ko, ko + lk))
         tl = tl[0].numpy()
         assert np.abs(o - to[0].numpy()).max() <= tol
-        assert np.abs(lse[fin] - tl[fin]).max() <= LSE_TOL
+        if fin.any():
+            assert np.abs(lse[fin] - tl[fin]).max() <= LSE_TOL
 
 
 def test_block_partial_head_major_and_unaligned_views(gpu):
@@ -128,7 +130,8 @@ def test_lse_merge_matches_closed_form(gpu):
     torch.cuda.synchronize()
     ref_o, ref_l = C.merge_partials_f64(os_, ls)
     assert np.abs(out32.cpu().numpy() - ref_o).max() < 1e-5
-    assert np.abs(out.float().cpu().numpy() - ref_o).max() <= 1e-2
+    # bf16 output: within one bf16 rounding (relative 2^-8) of the f64 merge
+    assert np.all(np.abs(out.float().cpu().numpy() - ref_o) <= np.abs(ref_o) * 2.0**-8 + 1e-6)
     lse = lse.cpu().numpy()
     assert lse[0, 100] == -np.inf and np.all(out.float().cpu().numpy()[0, 100] == 0)
     fin = np.isfinite(ref_l)
@@ -163,7 +166,7 @@ def test_paged_gather_scatter_bit_exact(gpu, dtype):
     assert np.array_equal(_np_bits(pool), pool_np)
     # gather(scatter(x)) == x
     k3, v3 = H.paged_kv_gather(pool, table, off, t0, t1)
-    assert torch.equal(k3, k2) and torch.equal(v3, v2)
+    assert np.array_equal(_np_bits(k3), _np_bits(k2)) and np.array_equal(_np_bits(v3), _np_bits(v2))
     assert H.fetch_device_errors() == 0
 
 
