@@ -152,9 +152,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 
   const int nblk = gridDim.x;
   const int logical = xcd_remap(blockIdx.x, nblk);
-  // Heavier (later) query tiles first; all head groups of one tile are adjacent.
-  const int qt = a.n_qtiles - 1 - logical / a.n_groups;
-  const int hg = logical % a.n_groups;
+  // Head-group-major: each XCD's contiguous share of logical tiles covers the query
+  // tiles of as few KV heads as possible, so its CUs stream the same K/V through that
+  // XCD's L2.  Within a head group, heavier (later, causal) query tiles come first.
+  const int hg = logical / a.n_qtiles;
+  const int qt = a.n_qtiles - 1 - logical % a.n_qtiles;
 
   const int tid = threadIdx.x;
   // Wave index as a scalar: everything derived from it stays in SGPRs.
