@@ -209,9 +209,11 @@ def bench_staged(H, torch, steps: int, warmup: int, full_prefill: bool = True):
     stage_k = torch.empty(hkv, seq, d, dtype=torch.bfloat16, device="cuda")
     stage_v = torch.empty(hkv, seq, d, dtype=torch.bfloat16, device="cuda")
 
+    ranges = [(table, 0, o, o + L, stage_k[:, o:o + L], stage_v[:, o:o + L]) for o, L in zip(offs, c["chunks"])]
+
     def gather_all():
-        for o, L in zip(offs, c["chunks"]):
-            H.paged_kv_gather(pool, table, 0, o, o + L, stage_k[:, o:o + L], stage_v[:, o:o + L])
+        # every domain's chunk staged by one batched launch (8 ranges)
+        H.paged_kv_gather_batch(pool, ranges)
 
     for _ in range(warmup):
         gather_all()

@@ -66,6 +66,12 @@ class PagedPool(ctypes.Structure):
                 ("head_dim", ctypes.c_int32), ("elem_bytes", ctypes.c_int32)]
 
 
+class PagedRange(ctypes.Structure):
+    _fields_ = [("block_table", ctypes.c_void_p), ("table_len", ctypes.c_int64),
+                ("table_seq_offset", ctypes.c_int64), ("t0", ctypes.c_int64), ("t1", ctypes.c_int64),
+                ("k_out", View), ("v_out", View)]
+
+
 class DecodeDesc(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int32), ("batch", ctypes.c_int32),
                 ("num_q_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
@@ -107,6 +113,8 @@ def lib() -> ctypes.CDLL:
                                  vp], ctypes.c_int),
         "hcp_paged_kv_scatter": ([ctypes.POINTER(PagedPool), vp, i64, i64, i64, i64, View, View,
                                   i32, vp], ctypes.c_int),
+        "hcp_paged_kv_gather_batch": ([ctypes.POINTER(PagedPool), i32, ctypes.POINTER(PagedRange),
+                                       vp], ctypes.c_int),
         "hcp_paged_decode_workspace_size": ([ctypes.POINTER(DecodeDesc),
                                              ctypes.POINTER(PagedPool)], ctypes.c_size_t),
         "hcp_paged_decode_partial": ([ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedPool), View,
@@ -265,6 +273,16 @@ def paged_kv_scatter(pool, block_table, table_seq_offset, t0, t1, k_in, v_in, ze
     _check(lib().hcp_paged_kv_scatter(ctypes.byref(pp), _ptr(block_table), block_table.numel(),
                                       table_seq_offset, t0, t1, view(k_in), view(v_in),
                                       1 if zero_tail else 0, _stream(stream)))
+
+
+def paged_kv_gather_batch(pool, ranges, stream=None):
+    """ranges: list of (block_table, table_seq_offset, t0, t1, k_out, v_out); one launch."""
+    n = len(ranges)
+    arr = (PagedRange * max(n, 1))()
+    for i, (tab, off, t0, t1, ko, vo) in enumerate(ranges):
+        arr[i] = PagedRange(tab.data_ptr(), tab.numel(), off, t0, t1, view(ko), view(vo))
+    pp = paged_pool(pool)
+    _check(lib().hcp_paged_kv_gather_batch(ctypes.byref(pp), n, arr, _stream(stream)))
 
 
 def fetch_device_errors(stream=None) -> int:

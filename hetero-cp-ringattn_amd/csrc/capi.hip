@@ -251,29 +251,37 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
   // Ring step s: domain t consumes source (t - s) mod N (local first, then the
   // predecessor chain, as the mock ring delivers it: mock.rs:143-149).
   for (int s = 0; s < p.n; ++s) {
+    std::vector<hcp_ring_view> ks(p.n, k), vs(p.n, v);
+    if (paged) {
+      // Stage every domain's source chunk of this step into its ring buffer: one
+      // batched, bit-exact gather for the whole step.
+      std::vector<PagedRangeDesc> rs;
+      for (int t = 0; t < p.n; ++t) {
+        const int src = ((t - s) % p.n + p.n) % p.n;
+        bool used = false;
+        for (int x : p.sources[t]) used = used || x == src;
+        if (!used) continue;
+        char* stg = base + p.staging_off + static_cast<size_t>(t) * p.staging_bytes_per_domain;
+        const int64_t hs = p.len[src] * d->head_dim;  // [Hkv, L, D] packed per source length
+        ks[t] = hcp_ring_view{stg, hs, d->head_dim};
+        vs[t] = hcp_ring_view{stg + p.staging_bytes_per_domain / 2, hs, d->head_dim};
+        rs.push_back(PagedRangeDesc{table, 0, p.off[src], p.off[src] + p.len[src], ks[t].data, vs[t].data, hs,
+                                    d->head_dim});
+      }
+      timed(kTimedGather, stream, [&] {
+        launch_paged_copy_batch(true, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads,
+                                pool->head_dim, pool->elem_bytes, static_cast<int>(rs.size()), rs.data(), 0, err,
+                                stream);
+      });
+    }
     for (int t = 0; t < p.n; ++t) {
       const int src = ((t - s) % p.n + p.n) % p.n;
       int idx = -1;
       for (size_t i = 0; i < p.sources[t].size(); ++i)
         if (p.sources[t][i] == src) idx = static_cast<int>(i);
       if (idx < 0) continue;  // fully-future source
-      hcp_ring_view kv_k = k, kv_v = v;
-      if (paged) {
-        // Stage the source chunk into this domain's ring buffer (bit-exact gather).
-        char* stg = base + p.staging_off + static_cast<size_t>(t) * p.staging_bytes_per_domain;
-        const int64_t hs = p.len[src];  // [Hkv, L, D] packed per source length
-        kv_k.data = stg;
-        kv_k.head_stride = hs * d->head_dim;
-        kv_k.seq_stride = d->head_dim;
-        kv_v.data = stg + p.staging_bytes_per_domain / 2;
-        kv_v.head_stride = hs * d->head_dim;
-        kv_v.seq_stride = d->head_dim;
-        timed(kTimedGather, stream, [&] {
-          launch_paged_copy(true, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads,
-                            pool->head_dim, pool->elem_bytes, table, 0, p.off[src], p.off[src] + p.len[src],
-                            kv_k.data, kv_v.data, kv_k.head_stride, kv_k.seq_stride, 0, err, stream);
-        });
-      } else {
+      hcp_ring_view kv_k = ks[t], kv_v = vs[t];
+      if (!paged) {
         kv_k.data = static_cast<char*>(k.data) + p.off[src] * k.seq_stride * es;
         kv_v.data = static_cast<char*>(v.data) + p.off[src] * v.seq_stride * es;
       }
@@ -431,10 +439,33 @@ int hcp_paged_kv_scatter(const hcp_paged_pool* pool, const int32_t* block_table,
   });
 }
 
+int hcp_paged_kv_gather_batch(const hcp_paged_pool* pool, int32_t num_ranges, const hcp_paged_range* ranges,
+                              void* stream) {
+  return guarded(__func__, [&] {
+    check_pool(pool);
+    require(num_ranges >= 0 && (num_ranges == 0 || ranges != nullptr), "bad range array");
+    std::vector<PagedRangeDesc> rs;
+    rs.reserve(num_ranges);
+    for (int i = 0; i < num_ranges; ++i) {
+      const hcp_paged_range& r = ranges[i];
+      check_paged_range(pool, r.block_table, r.table_len, r.table_seq_offset, r.t0, r.t1);
+      check_view(r.k_out, "k_out", r.t1 - r.t0);
+      check_view(r.v_out, "v_out", r.t1 - r.t0);
+      require(r.k_out.head_stride == r.v_out.head_stride && r.k_out.seq_stride == r.v_out.seq_stride,
+              "k_out and v_out must share strides");
+      rs.push_back(PagedRangeDesc{r.block_table, r.table_seq_offset, r.t0, r.t1, r.k_out.data, r.v_out.data,
+                                  r.k_out.head_stride, r.k_out.seq_stride});
+    }
+    launch_paged_copy_batch(true, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads,
+                            pool->head_dim, pool->elem_bytes, num_ranges, rs.data(), 0, device_error_flags(),
+                            as_stream(stream));
+  });
+}
+
 size_t hcp_paged_decode_workspace_size(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool) {
   if (desc == nullptr || pool == nullptr || desc->batch <= 0) return 0;
   (void)pool;
-  return decode_workspace_bytes(desc->batch, desc->num_q_heads, desc->head_dim, desc->t0, desc->t1);
+  return decode_workspace_bytes(desc->batch, desc->num_q_heads, desc->num_kv_heads, desc->head_dim, desc->t0, desc->t1);
 }
 
 int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool, hcp_ring_view q,

@@ -26,12 +26,25 @@ void launch_lse_merge(int n, const float* const* o_parts, const float* const* ls
                       int64_t q_len, int d, int out_dtype, void* out, int64_t out_hs, int64_t out_ss,
                       float* lse_out, int64_t lse_out_hs, hipStream_t stream);
 
+// One token range of one sequence for the batched paged copy.
+struct PagedRangeDesc {
+  const int32_t* table;
+  int64_t table_seq_offset;
+  int64_t t0, t1;
+  void* k_buf;
+  void* v_buf;
+  int64_t head_stride, seq_stride;  // elements
+};
+void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs, int hkv, int d,
+                             int elem_bytes, int n, const PagedRangeDesc* ranges, int zero_tail,
+                             int* err, hipStream_t stream);
+
 void launch_paged_copy(bool gather, void* pool, int64_t num_blocks, int bs, int hkv, int d,
                        int elem_bytes, const int32_t* table, int64_t table_seq_offset, int64_t t0,
                        int64_t t1, void* k_buf, void* v_buf, int64_t head_stride, int64_t seq_stride,
                        int zero_tail, int* err, hipStream_t stream);
 
-size_t decode_workspace_bytes(int batch, int hq, int d, int64_t t0, int64_t t1);
+size_t decode_workspace_bytes(int batch, int hq, int hkv, int d, int64_t t0, int64_t t1);
 void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const void* q, int64_t q_bs,
                          int64_t q_hs, const void* pool, int64_t num_blocks, int bs,
                          const int32_t* tables, int64_t table_stride, int64_t table_len,

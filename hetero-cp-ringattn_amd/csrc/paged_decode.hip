@@ -68,28 +68,30 @@ __device__ __forceinline__ float hi_half(uint32_t w) {
   return DT == kBF16 ? __uint_as_float(w & 0xffff0000u) : f16_bits_to_f32(static_cast<uint16_t>(w >> 16));
 }
 
-constexpr int kDecWaves = 4;
-constexpr int kMaxHeadsPerWave = 4;  // supports Hkv <= 16
+constexpr int kDecWaves = 4;  // kv heads per workgroup (one per wave)
 
-// HPW = kv heads per wave; wave w owns kv heads w*HPW .. w*HPW+HPW-1 (< Hkv).
-template <int D, int DT, int HPW>
+// One wave per kv head.  Per 16-key group the wave needs the head's 16 K rows and 16 V
+// rows (4 KiB each for D=128); the loads of two groups are issued before either is
+// computed, so each wave keeps ~16 KiB of HBM reads in flight.
+template <int D, int DT>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;        // k-steps of 32 for the QK^T product
   constexpr int DCH = D / 8;        // 8-wide d chunks per row (16 for D=128)
-  constexpr int TOKS_PER_LANE = 16 * DCH / 64;  // keys per lane in PV (4 for D=128)
+  constexpr int TPL = 16 * DCH / 64;  // keys per lane in PV (4 for D=128)
 
-  __shared__ float p_lds[kDecWaves][16][16];  // [wave][key][query col]
-  __shared__ float alpha_lds[kDecWaves][16];
+  __shared__ float p_lds[kDecWaves][16][4];  // [wave][key][query col]
 
   const int b = blockIdx.y;
   const int split = blockIdx.x;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kvh = blockIdx.z * kDecWaves + wave;
+  if (kvh >= a.hkv) return;  // no workgroup barriers below
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;   // MFMA column = query head within the kv group
   const int grp = lane >> 4;   // MFMA k-group / key group
-  // PV role: lane owns d chunk pv_dc (8 values) of keys pv_tg*TOKS_PER_LANE .. +TOKS_PER_LANE.
+  // PV role: lane owns d chunk pv_dc (8 values) of keys pv_tg*TPL .. +TPL.
   const int pv_dc = lane % DCH;
-  const int pv_tg = lane / DCH;  // key subgroup: keys pv_tg*TOKS_PER_LANE .. +TOKS_PER_LANE
+  const int pv_tg = lane / DCH;
 
   int64_t t_end = a.t1;
   if (a.seq_lens != nullptr) t_end = min(t_end, static_cast<int64_t>(a.seq_lens[b]));
@@ -98,161 +100,161 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   const int32_t* table = a.tables + static_cast<int64_t>(b) * a.table_stride;
 
   // Q^T fragments: lane (col, grp) holds Q[head kvh*rep + col][grp*8 + 32*s .. +8].
-  u32x4 qf[HPW][KS];
+  u32x4 qf[KS];
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
-    const int kvh = wave * HPW + hh;
-    const bool hv = kvh < a.hkv;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      u32x4 v = {0, 0, 0, 0};
-      if (hv && col < a.rep) {
-        const uint16_t* qp = a.q + b * a.q_bs + (kvh * a.rep + col) * a.q_hs + grp * 8 + 32 * s;
-        v = *reinterpret_cast<const u32x4*>(qp);
-      }
-      qf[hh][s] = v;
-    }
+  for (int s = 0; s < KS; ++s) {
+    u32x4 v = {0, 0, 0, 0};
+    if (col < a.rep) v = *reinterpret_cast<const u32x4*>(a.q + b * a.q_bs + (kvh * a.rep + col) * a.q_hs + grp * 8 + 32 * s);
+    qf[s] = v;
   }
 
   // PV accumulators cover rep <= 4 query heads per kv head (checked by the launcher).
-  float acc[HPW][4][8];  // [head][query col][d]
-  float m_run[HPW], l_run[HPW];
+  float acc[4][8];
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
-    m_run[hh] = -1.0e30f;
-    l_run[hh] = 0.f;
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
+  float m_run = -1.0e30f, l_run = 0.f;
+
+  const int64_t row_elems = static_cast<int64_t>(a.hkv) * D;  // one slot, all heads
+
+  struct Group {
+    u32x4 k[KS];
+    u32x4 v[TPL];
+    int64_t tok0;
+    bool ok;
+  };
+  auto load_group = [&](int g, Group& G) {
+    G.tok0 = (a.g_begin + g) * 16;
+    // Keys tok0 .. tok0+15 lie in table entry tok0 / bs (bs is a multiple of 16).
+    const int64_t entry = G.tok0 / a.bs;
+    const int32_t blk = entry < a.table_len ? table[entry] : -1;
+    G.ok = blk >= 0 && blk < a.num_blocks;
+    if (!G.ok) {
+      if (lane == 0 && entry < a.table_len) atomicOr(a.err, 1);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) G.k[s] = u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < TPL; ++j) G.v[j] = u32x4{0, 0, 0, 0};
+      return;
+    }
+    const int slot0 = static_cast<int>(G.tok0 - entry * a.bs);
+    const uint16_t* kslot = a.pool + (static_cast<int64_t>(blk) * a.bs + slot0) * row_elems + kvh * D;
+    const uint16_t* krow = kslot + col * row_elems + grp * 8;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) G.k[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow + 32 * s));
+    const uint16_t* vrow = kslot + a.plane_elems + pv_dc * 8;
+#pragma unroll
+    for (int j = 0; j < TPL; ++j)
+      G.v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow + (pv_tg * TPL + j) * row_elems));
+  };
+  auto compute_group = [&](const Group& G) {
+    if (!G.ok) return;
+    // ---- S^T = K Q^T: lane (col = query, grp) holds keys grp*4 + i ----
+    f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) s4 = mma16<DT>(G.k[s], qf[s], s4);
+    float tmax = -INFINITY;
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t t = G.tok0 + grp * 4 + i;
+      const bool ok = t >= a.t0 && t < t_end;
+      sv[i] = ok ? s4[i] * a.scale_log2 : -INFINITY;
+      tmax = fmaxf(tmax, sv[i]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = __builtin_amdgcn_exp2f(sv[i] - m_new);
+      psum += p;
+      if (col < 4) p_lds[wave][grp * 4 + i][col] = p;
+    }
+    l_run = l_run * alpha + psum;  // per-lane partial over its keys (rescaled)
+    // alpha of query column c lives in lane c.
+    float al[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) al[c] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), c));
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[hh][c][e] = 0.f;
-  }
+      for (int e = 0; e < 8; ++e) acc[c][e] *= al[c];
+    __builtin_amdgcn_wave_barrier();
+    // ---- O += P V (VALU): lane owns 8 head-dim values of keys pv_tg*TPL .. +TPL ----
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) {
+      const int key = pv_tg * TPL + j;
+      const int64_t t = G.tok0 + key;
+      const bool ok = t >= a.t0 && t < t_end;
+      const u32x4 vv = ok ? G.v[j] : u32x4{0, 0, 0, 0};
+      const float4 p4 = *reinterpret_cast<const float4*>(&p_lds[wave][key][0]);
+      float vf[8];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        vf[2 * w] = lo_half<DT>(vv[w]);
+        vf[2 * w + 1] = hi_half<DT>(vv[w]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        acc[0][e] += p4.x * vf[e];
+        acc[1][e] += p4.y * vf[e];
+        acc[2][e] += p4.z * vf[e];
+        acc[3][e] += p4.w * vf[e];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
 
-  const int64_t row_elems = static_cast<int64_t>(a.hkv) * D;  // one slot, all heads
-  for (int g = g0; g < g1; ++g) {
-    const int64_t tok0 = (a.g_begin + g) * 16;
-    // Keys tok0 .. tok0+15 come from table entries (tok0 / bs) (bs multiple of 16).
-    const int64_t entry = tok0 / a.bs;
-    const int32_t blk = entry < a.table_len ? table[entry] : -1;
-    const bool blk_ok = blk >= 0 && blk < a.num_blocks;
-    if (!blk_ok) {
-      if (threadIdx.x == 0 && entry < a.table_len) atomicOr(a.err, 1);
-      continue;
-    }
-    const int slot0 = static_cast<int>(tok0 - entry * a.bs);
-    const uint16_t* kslot = a.pool + (static_cast<int64_t>(blk) * a.bs + slot0) * row_elems;
-    const uint16_t* vslot = kslot + a.plane_elems;
-#pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-      const int kvh = wave * HPW + hh;
-      if (kvh >= a.hkv) break;
-      // ---- S^T = K Q^T ----
-      f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = kslot + col * row_elems + kvh * D + grp * 8;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + 32 * s);
-        s4 = mma16<DT>(kf, qf[hh][s], s4);
-      }
-      // lane (col = query, grp) holds keys grp*4 + i.
-      float tmax = -INFINITY;
-      float sv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t t = tok0 + grp * 4 + i;
-        const bool ok = t >= a.t0 && t < t_end;
-        sv[i] = ok ? s4[i] * a.scale_log2 : -INFINITY;
-        tmax = fmaxf(tmax, sv[i]);
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float m_new = fmaxf(m_run[hh], tmax);
-      const float alpha = exp2f(m_run[hh] - m_new);
-      m_run[hh] = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(sv[i] - m_new);
-        psum += p;
-        if (col < 4) p_lds[wave][grp * 4 + i][col] = p;
-      }
-      l_run[hh] = l_run[hh] * alpha + psum;  // per-lane partial over its keys (rescaled)
-      if (lane < 4) alpha_lds[wave][lane] = alpha;
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // ---- O += P V (VALU) ----
-      float al[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) al[c] = alpha_lds[wave][c];
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[hh][c][e] *= al[c];
-      const uint16_t* vbase = vslot + kvh * D + pv_dc * 8;
-#pragma unroll
-      for (int j = 0; j < TOKS_PER_LANE; ++j) {
-        const int key = pv_tg * TOKS_PER_LANE + j;
-        const int64_t t = tok0 + key;
-        const bool ok = t >= a.t0 && t < t_end;
-        u32x4 vv = ok ? *reinterpret_cast<const u32x4*>(vbase + key * row_elems) : u32x4{0, 0, 0, 0};
-        const float4 p4 = *reinterpret_cast<const float4*>(&p_lds[wave][key][0]);
-        float vf[8];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          vf[2 * w] = lo_half<DT>(vv[w]);
-          vf[2 * w + 1] = hi_half<DT>(vv[w]);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          acc[hh][0][e] += p4.x * vf[e];
-          acc[hh][1][e] += p4.y * vf[e];
-          acc[hh][2][e] += p4.z * vf[e];
-          acc[hh][3][e] += p4.w * vf[e];
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
+  Group ga, gb;
+  int g = g0;
+  for (; g + 1 < g1; g += 2) {
+    load_group(g, ga);
+    load_group(g + 1, gb);
+    compute_group(ga);
+    compute_group(gb);
+  }
+  if (g < g1) {
+    load_group(g, ga);
+    compute_group(ga);
   }
 
   // ---- epilogue: reduce over key subgroups, normalise, write split partial ----
   const int64_t ws_row_base = static_cast<int64_t>(split) * a.batch * a.hq + static_cast<int64_t>(b) * a.hq;
+  float l = l_run;
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);  // lanes with the same col now hold the total over keys
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
-    const int kvh = wave * HPW + hh;
-    if (kvh >= a.hkv) break;
-    float l = l_run[hh];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);  // lanes with the same col now hold the total over keys
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float v = acc[hh][c][e];
-        // Lanes with equal pv_dc hold the same d for different key subgroups.
-        for (int off = DCH; off < 64; off *= 2) v += __shfl_xor(v, off);
-        acc[hh][c][e] = v;
-      }
-    // l for query c lives in lanes with col == c; broadcast.
-    float lc[4], mc;
-    mc = m_run[hh];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) lc[c] = __shfl(l, c);
-    if (pv_tg == 0) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (c >= a.rep) break;
-        const float inv = lc[c] > 0.f ? 1.f / lc[c] : 0.f;
-        float* orow = a.ws_o + (ws_row_base + kvh * a.rep + c) * D + pv_dc * 8;
-        float4 o0 = make_float4(acc[hh][c][0] * inv, acc[hh][c][1] * inv, acc[hh][c][2] * inv, acc[hh][c][3] * inv);
-        float4 o1 = make_float4(acc[hh][c][4] * inv, acc[hh][c][5] * inv, acc[hh][c][6] * inv, acc[hh][c][7] * inv);
-        reinterpret_cast<float4*>(orow)[0] = o0;
-        reinterpret_cast<float4*>(orow)[1] = o1;
-      }
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[c][e];
+      // Lanes with equal pv_dc hold the same d for different key subgroups.
+      for (int off = DCH; off < 64; off *= 2) v += __shfl_xor(v, off);
+      acc[c][e] = v;
     }
-    if (lane < a.rep && lane < 4) {
-      const float lt = lc[lane];
-      a.ws_lse[ws_row_base + kvh * a.rep + lane] = lt > 0.f ? (mc + __log2f(lt)) * kLn2 : -INFINITY;
+  float lc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) lc[c] = __shfl(l, c);
+  if (pv_tg == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c >= a.rep) break;
+      const float inv = lc[c] > 0.f ? 1.f / lc[c] : 0.f;
+      float* orow = a.ws_o + (ws_row_base + kvh * a.rep + c) * D + pv_dc * 8;
+      reinterpret_cast<float4*>(orow)[0] =
+          make_float4(acc[c][0] * inv, acc[c][1] * inv, acc[c][2] * inv, acc[c][3] * inv);
+      reinterpret_cast<float4*>(orow)[1] =
+          make_float4(acc[c][4] * inv, acc[c][5] * inv, acc[c][6] * inv, acc[c][7] * inv);
     }
+  }
+  if (lane < a.rep && lane < 4) {
+    const float lt = lc[lane];
+    a.ws_lse[ws_row_base + kvh * a.rep + lane] = lt > 0.f ? (m_run + __log2f(lt)) * kLn2 : -INFINITY;
   }
 }
 
@@ -263,14 +265,16 @@ struct DecodePlan {
   int64_t g_begin;
 };
 
-DecodePlan plan_decode(int batch, int64_t t0, int64_t t1) {
+DecodePlan plan_decode(int batch, int hkv, int64_t t0, int64_t t1) {
   DecodePlan p;
   p.g_begin = t0 / 16;
   const int64_t g_end = t1 > t0 ? (t1 + 15) / 16 : p.g_begin;
   p.n_groups = static_cast<int>(g_end - p.g_begin);
-  // Aim for ~8 workgroups per CU on 256 CUs, at least 4 groups (64 keys) per split.
-  const int target = 2048;
-  int splits = static_cast<int>(ceil_div(target, std::max(batch, 1)));
+  // Aim for ~16 workgroups per CU on 256 CUs (grid = splits x batch x kv-head groups),
+  // at least 4 groups (64 keys) per split.
+  const int target = 4096;
+  const int per_split = std::max(batch, 1) * ((hkv + kDecWaves - 1) / kDecWaves);
+  int splits = static_cast<int>(ceil_div(target, per_split));
   splits = std::max(1, std::min(splits, 64));
   int gps = static_cast<int>(ceil_div(std::max(p.n_groups, 1), splits));
   gps = std::max(gps, 4);
@@ -279,8 +283,8 @@ DecodePlan plan_decode(int batch, int64_t t0, int64_t t1) {
   return p;
 }
 
-size_t decode_workspace_bytes(int batch, int hq, int d, int64_t t0, int64_t t1) {
-  const DecodePlan p = plan_decode(batch, t0, t1);
+size_t decode_workspace_bytes(int batch, int hq, int hkv, int d, int64_t t0, int64_t t1) {
+  const DecodePlan p = plan_decode(batch, hkv, t0, t1);
   const size_t rows = static_cast<size_t>(p.splits) * batch * hq;
   auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   return al(rows * d * sizeof(float)) + al(rows * sizeof(float));
@@ -292,12 +296,11 @@ void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const voi
                          const int32_t* seq_lens, int64_t t0, int64_t t1, float scale, float* o,
                          float* lse, void* ws, size_t ws_bytes, int* err, hipStream_t stream) {
   require(hq % hkv == 0 && hq / hkv <= 4, "paged_decode: num_q_heads/num_kv_heads must be <= 4");
-  require(hkv <= kDecWaves * kMaxHeadsPerWave, "paged_decode: num_kv_heads must be <= 16");
   require(bs % 16 == 0, "paged_decode: block_size must be a multiple of 16");
   require(d == 64 || d == 128, "paged_decode: head_dim must be 64 or 128");
   require(dtype == kBF16 || dtype == kF16, "paged_decode: dtype must be BF16 or F16");
-  const DecodePlan p = plan_decode(batch, t0, t1);
-  require(ws_bytes >= decode_workspace_bytes(batch, hq, d, t0, t1), "paged_decode: workspace too small");
+  const DecodePlan p = plan_decode(batch, hkv, t0, t1);
+  require(ws_bytes >= decode_workspace_bytes(batch, hq, hkv, d, t0, t1), "paged_decode: workspace too small");
   auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   const size_t rows = static_cast<size_t>(p.splits) * batch * hq;
   float* ws_o = static_cast<float*>(ws);
@@ -328,21 +331,15 @@ void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const voi
   a.ws_lse = ws_lse;
   a.batch = batch;
   a.err = err;
-  const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(batch));
-  const int hpw = (hkv + kDecWaves - 1) / kDecWaves;
-#define HCP_DEC(D_, DT_)                                                               \
-  switch (hpw) {                                                                       \
-    case 1: paged_decode_kernel<D_, DT_, 1><<<grid, 256, 0, stream>>>(a); break;        \
-    case 2: paged_decode_kernel<D_, DT_, 2><<<grid, 256, 0, stream>>>(a); break;        \
-    case 3: paged_decode_kernel<D_, DT_, 3><<<grid, 256, 0, stream>>>(a); break;        \
-    default: paged_decode_kernel<D_, DT_, 4><<<grid, 256, 0, stream>>>(a); break;       \
-  }
+  const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(batch),
+                  static_cast<unsigned>((hkv + kDecWaves - 1) / kDecWaves));
   if (dtype == kBF16) {
-    if (d == 128) { HCP_DEC(128, kBF16) } else { HCP_DEC(64, kBF16) }
+    if (d == 128) paged_decode_kernel<128, kBF16><<<grid, 256, 0, stream>>>(a);
+    else paged_decode_kernel<64, kBF16><<<grid, 256, 0, stream>>>(a);
   } else {
-    if (d == 128) { HCP_DEC(128, kF16) } else { HCP_DEC(64, kF16) }
+    if (d == 128) paged_decode_kernel<128, kF16><<<grid, 256, 0, stream>>>(a);
+    else paged_decode_kernel<64, kF16><<<grid, 256, 0, stream>>>(a);
   }
-#undef HCP_DEC
   HCP_HIP(hipGetLastError());
   // Merge the splits of every (sequence, head): rows = batch*hq, one token each.
   const float* o_parts[64];

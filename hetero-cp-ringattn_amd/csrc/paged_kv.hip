@@ -15,10 +15,11 @@
 
 namespace hcp {
 
-struct PagedCopyArgs {
-  uint8_t* pool;            // plane 0 (K); plane 1 at + plane_bytes
-  int64_t plane_bytes;
-  int64_t num_blocks;
+// Up to kMaxRanges ranges (each: a sequence's block table and a token range) are
+// copied by one launch; blockIdx.x walks the concatenation of their table entries.
+constexpr int kMaxRanges = 16;
+
+struct PagedRange {
   const int32_t* table;
   int64_t table_seq_offset;
   int64_t t0, t1;
@@ -27,15 +28,30 @@ struct PagedCopyArgs {
   uint8_t* v_buf;
   int64_t head_stride_b;    // bytes between heads
   int64_t seq_stride_b;     // bytes between tokens
+};
+
+struct PagedCopyArgs {
+  uint8_t* pool;            // plane 0 (K); plane 1 at + plane_bytes
+  int64_t plane_bytes;
+  int64_t num_blocks;
   int32_t bs, hkv, row_bytes;
   int32_t zero_tail;
+  int32_t n_ranges;
+  int32_t block_begin[kMaxRanges + 1];  // prefix sums of blocks per range
+  PagedRange r[kMaxRanges];
   int* err;
 };
 
-template <typename V, bool kGather>
+// Each thread moves kU vectors of each plane per pass: all 2*kU loads are issued before
+// any store, so a 256-thread workgroup keeps 2*kU*256*sizeof(V) bytes in flight.
+template <typename V, bool kGather, int kU>
 __global__ __launch_bounds__(256) void paged_copy_kernel(PagedCopyArgs a) {
-  const int64_t entry = a.first_entry + blockIdx.x;
-  const int32_t blk = a.table[entry];
+  const int bid = blockIdx.x;
+  int ri = 0;
+  while (ri + 1 < a.n_ranges && bid >= a.block_begin[ri + 1]) ++ri;
+  const PagedRange& R = a.r[ri];
+  const int64_t entry = R.first_entry + (bid - a.block_begin[ri]);
+  const int32_t blk = R.table[entry];
   if (blk < 0 || blk >= a.num_blocks) {
     if (threadIdx.x == 0) atomicOr(a.err, 1);
     return;
@@ -44,52 +60,51 @@ __global__ __launch_bounds__(256) void paged_copy_kernel(PagedCopyArgs a) {
   const int vec_per_row = a.row_bytes / kVec;
   const int vec_per_slot = vec_per_row * a.hkv;
   const int total = vec_per_slot * a.bs;
-  const int64_t block_tok0 = a.table_seq_offset + entry * a.bs;  // global token of slot 0
+  const int64_t block_tok0 = R.table_seq_offset + entry * a.bs;  // token of slot 0
   const int64_t block_bytes = static_cast<int64_t>(a.bs) * a.hkv * a.row_bytes;
   uint8_t* pk = a.pool + static_cast<int64_t>(blk) * block_bytes;
   uint8_t* pv = pk + a.plane_bytes;
 
-  constexpr int kUnroll = 4;
-  for (int base = threadIdx.x; base < total; base += 256 * kUnroll) {
-    V rk[kUnroll], rv[kUnroll];
-    int64_t boff[kUnroll];
-    bool ok[kUnroll];
+  for (int base = threadIdx.x; base < total; base += 256 * kU) {
+    V rk[kU], rv[kU];
+    int64_t boff[kU];
+    bool ok[kU];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kU; ++u) {
       const int c = base + u * 256;
       const int slot = c / vec_per_slot;
       const int rem = c - slot * vec_per_slot;
       const int h = rem / vec_per_row;
       const int cv = rem - h * vec_per_row;
       const int64_t tok = block_tok0 + slot;
-      ok[u] = (c < total) && tok >= a.t0 && tok < a.t1;
-      boff[u] = h * a.head_stride_b + (tok - a.t0) * a.seq_stride_b + static_cast<int64_t>(cv) * kVec;
+      ok[u] = (c < total) && tok >= R.t0 && tok < R.t1;
+      boff[u] = h * R.head_stride_b + (tok - R.t0) * R.seq_stride_b + static_cast<int64_t>(cv) * kVec;
       if (ok[u]) {
         if constexpr (kGather) {
-          rk[u] = *reinterpret_cast<const V*>(pk + static_cast<int64_t>(c) * kVec);
-          rv[u] = *reinterpret_cast<const V*>(pv + static_cast<int64_t>(c) * kVec);
+          rk[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(pk + static_cast<int64_t>(c) * kVec));
+          rv[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(pv + static_cast<int64_t>(c) * kVec));
         } else {
-          rk[u] = *reinterpret_cast<const V*>(a.k_buf + boff[u]);
-          rv[u] = *reinterpret_cast<const V*>(a.v_buf + boff[u]);
+          rk[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(R.k_buf + boff[u]));
+          rv[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(R.v_buf + boff[u]));
         }
       }
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kU; ++u) {
       const int c = base + u * 256;
       if (ok[u]) {
         if constexpr (kGather) {
-          *reinterpret_cast<V*>(a.k_buf + boff[u]) = rk[u];
-          *reinterpret_cast<V*>(a.v_buf + boff[u]) = rv[u];
+          __builtin_nontemporal_store(rk[u], reinterpret_cast<V*>(R.k_buf + boff[u]));
+          __builtin_nontemporal_store(rv[u], reinterpret_cast<V*>(R.v_buf + boff[u]));
         } else {
-          *reinterpret_cast<V*>(pk + static_cast<int64_t>(c) * kVec) = rk[u];
-          *reinterpret_cast<V*>(pv + static_cast<int64_t>(c) * kVec) = rv[u];
+          __builtin_nontemporal_store(rk[u], reinterpret_cast<V*>(pk + static_cast<int64_t>(c) * kVec));
+          __builtin_nontemporal_store(rv[u], reinterpret_cast<V*>(pv + static_cast<int64_t>(c) * kVec));
         }
       } else if (!kGather && a.zero_tail && c < total) {
         // Slots after the last written token of the sequence's last block.
         const int slot = c / vec_per_slot;
         const int64_t tok = block_tok0 + slot;
-        if (tok >= a.t1) {
+        if (tok >= R.t1) {
           V z;
           __builtin_memset(&z, 0, sizeof(V));
           *reinterpret_cast<V*>(pk + static_cast<int64_t>(c) * kVec) = z;
@@ -101,48 +116,73 @@ __global__ __launch_bounds__(256) void paged_copy_kernel(PagedCopyArgs a) {
 }
 
 // Host launcher shared by gather and scatter.  Shapes were validated by the caller.
+void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs, int hkv, int d,
+                             int elem_bytes, int n, const PagedRangeDesc* ranges, int zero_tail,
+                             int* err, hipStream_t stream) {
+  int next = 0;
+  while (next < n) {
+    PagedCopyArgs a;
+    a.row_bytes = d * elem_bytes;
+    a.pool = static_cast<uint8_t*>(pool);
+    a.plane_bytes = num_blocks * bs * hkv * static_cast<int64_t>(a.row_bytes);
+    a.num_blocks = num_blocks;
+    a.bs = bs;
+    a.hkv = hkv;
+    a.zero_tail = zero_tail;
+    a.err = err;
+    int m = 0;
+    int blocks = 0;
+    bool al16 = a.row_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(pool) % 16 == 0;
+    bool al4 = a.row_bytes % 4 == 0 && reinterpret_cast<uintptr_t>(pool) % 4 == 0;
+    for (; next < n && m < kMaxRanges; ++next) {
+      const PagedRangeDesc& d_ = ranges[next];
+      if (d_.t1 <= d_.t0) continue;
+      PagedRange& R = a.r[m];
+      R.table = d_.table;
+      R.table_seq_offset = d_.table_seq_offset;
+      R.t0 = d_.t0;
+      R.t1 = d_.t1;
+      R.first_entry = (d_.t0 - d_.table_seq_offset) / bs;
+      const int64_t last_entry = (d_.t1 - 1 - d_.table_seq_offset) / bs;
+      R.k_buf = static_cast<uint8_t*>(d_.k_buf);
+      R.v_buf = static_cast<uint8_t*>(d_.v_buf);
+      R.head_stride_b = d_.head_stride * elem_bytes;
+      R.seq_stride_b = d_.seq_stride * elem_bytes;
+      a.block_begin[m] = blocks;
+      blocks += static_cast<int>(last_entry - R.first_entry + 1);
+      auto ok = [&](int v) {
+        return R.head_stride_b % v == 0 && R.seq_stride_b % v == 0 &&
+               reinterpret_cast<uintptr_t>(R.k_buf) % v == 0 && reinterpret_cast<uintptr_t>(R.v_buf) % v == 0;
+      };
+      al16 = al16 && ok(16);
+      al4 = al4 && ok(4);
+      ++m;
+    }
+    if (m == 0) continue;
+    a.n_ranges = m;
+    a.block_begin[m] = blocks;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    // Widest access that every row start and stride allows.
+    if (al16) {
+      if (gather) paged_copy_kernel<u32x4, true, 8><<<grid, 256, 0, stream>>>(a);
+      else paged_copy_kernel<u32x4, false, 8><<<grid, 256, 0, stream>>>(a);
+    } else if (al4) {
+      if (gather) paged_copy_kernel<uint32_t, true, 8><<<grid, 256, 0, stream>>>(a);
+      else paged_copy_kernel<uint32_t, false, 8><<<grid, 256, 0, stream>>>(a);
+    } else {
+      if (gather) paged_copy_kernel<uint16_t, true, 8><<<grid, 256, 0, stream>>>(a);
+      else paged_copy_kernel<uint16_t, false, 8><<<grid, 256, 0, stream>>>(a);
+    }
+    HCP_HIP(hipGetLastError());
+  }
+}
+
 void launch_paged_copy(bool gather, void* pool, int64_t num_blocks, int bs, int hkv, int d,
                        int elem_bytes, const int32_t* table, int64_t table_seq_offset,
                        int64_t t0, int64_t t1, void* k_buf, void* v_buf, int64_t head_stride,
                        int64_t seq_stride, int zero_tail, int* err, hipStream_t stream) {
-  if (t1 <= t0) return;
-  PagedCopyArgs a;
-  a.row_bytes = d * elem_bytes;
-  a.pool = static_cast<uint8_t*>(pool);
-  a.plane_bytes = num_blocks * bs * hkv * static_cast<int64_t>(a.row_bytes);
-  a.num_blocks = num_blocks;
-  a.table = table;
-  a.table_seq_offset = table_seq_offset;
-  a.t0 = t0;
-  a.t1 = t1;
-  a.first_entry = (t0 - table_seq_offset) / bs;
-  const int64_t last_entry = (t1 - 1 - table_seq_offset) / bs;
-  a.k_buf = static_cast<uint8_t*>(k_buf);
-  a.v_buf = static_cast<uint8_t*>(v_buf);
-  a.head_stride_b = head_stride * elem_bytes;
-  a.seq_stride_b = seq_stride * elem_bytes;
-  a.bs = bs;
-  a.hkv = hkv;
-  a.zero_tail = zero_tail;
-  a.err = err;
-  const dim3 grid(static_cast<unsigned>(last_entry - a.first_entry + 1));
-  // Widest access that every row start and stride allows.
-  auto aligned = [&](int v) {
-    return a.row_bytes % v == 0 && a.head_stride_b % v == 0 && a.seq_stride_b % v == 0 &&
-           reinterpret_cast<uintptr_t>(pool) % v == 0 && reinterpret_cast<uintptr_t>(k_buf) % v == 0 &&
-           reinterpret_cast<uintptr_t>(v_buf) % v == 0;
-  };
-  if (aligned(16)) {
-    if (gather) paged_copy_kernel<uint4, true><<<grid, 256, 0, stream>>>(a);
-    else paged_copy_kernel<uint4, false><<<grid, 256, 0, stream>>>(a);
-  } else if (aligned(4)) {
-    if (gather) paged_copy_kernel<uint32_t, true><<<grid, 256, 0, stream>>>(a);
-    else paged_copy_kernel<uint32_t, false><<<grid, 256, 0, stream>>>(a);
-  } else {
-    if (gather) paged_copy_kernel<uint16_t, true><<<grid, 256, 0, stream>>>(a);
-    else paged_copy_kernel<uint16_t, false><<<grid, 256, 0, stream>>>(a);
-  }
-  HCP_HIP(hipGetLastError());
+  PagedRangeDesc r{table, table_seq_offset, t0, t1, k_buf, v_buf, head_stride, seq_stride};
+  launch_paged_copy_batch(gather, pool, num_blocks, bs, hkv, d, elem_bytes, 1, &r, zero_tail, err, stream);
 }
 
 }  // namespace hcp

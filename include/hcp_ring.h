@@ -172,6 +172,21 @@ int hcp_paged_kv_scatter(const hcp_paged_pool* pool, const int32_t* block_table,
                          hcp_ring_view k_in, hcp_ring_view v_in, int32_t zero_tail,
                          void* stream);
 
+/* Many gathers from one pool in one launch (e.g. every domain's chunk of a ring step);
+ * each range has the meaning of one hcp_paged_kv_gather call.  ranges is a HOST array. */
+typedef struct hcp_paged_range {
+  const int32_t* block_table; /* DEVICE int32 array of table_len entries */
+  int64_t table_len;
+  int64_t table_seq_offset;
+  int64_t t0;
+  int64_t t1;
+  hcp_ring_view k_out;
+  hcp_ring_view v_out;        /* same strides as k_out */
+} hcp_paged_range;
+
+int hcp_paged_kv_gather_batch(const hcp_paged_pool* pool, int32_t num_ranges,
+                              const hcp_paged_range* ranges, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * (4) Paged single-query decode partial over one domain chunk.
  *

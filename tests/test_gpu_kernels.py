@@ -299,3 +299,26 @@ def test_ring_replay_paged_matches_unpaged(gpu):
     o2, l2 = H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, chunks)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_paged_gather_batch_bit_exact(gpu):
+    # several ranges (different tables, offsets and unaligned bounds) in one launch
+    nb, bs, hkv, d = 128, 16, 8, 128
+    rng = np.random.default_rng(12)
+    pool_np = rng.integers(0, 2**16, size=(2, nb, bs, hkv, d), dtype=np.uint16)
+    pool = torch.from_numpy(pool_np.view(np.int16)).view(torch.bfloat16).cuda()
+    perm = I.permuted_block_table(13, nb)
+    specs = [(perm[:30], 0, 0, 480), (perm[30:70], 64, 70, 600), (perm[70:90], 0, 5, 5), (perm[90:128], 16, 17, 610)]
+    ranges, refs = [], []
+    for tab, off, t0, t1 in specs:
+        ko = torch.zeros(hkv, t1 - t0, d, dtype=torch.bfloat16, device="cuda")
+        vo = torch.zeros_like(ko)
+        ranges.append((torch.from_numpy(np.ascontiguousarray(tab)).cuda(), off, t0, t1, ko, vo))
+        refs.append(clib.paged_gather(pool_np, tab, off, t0, t1) if t1 > t0 else None)
+    H.paged_kv_gather_batch(pool, ranges)
+    torch.cuda.synchronize()
+    for (tab, off, t0, t1, ko, vo), ref in zip(ranges, refs):
+        if ref is None:
+            continue
+        assert np.array_equal(_np_bits(ko), ref[0]) and np.array_equal(_np_bits(vo), ref[1])
+    assert H.fetch_device_errors() == 0
