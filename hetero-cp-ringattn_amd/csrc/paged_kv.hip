@@ -45,8 +45,7 @@ struct PagedCopyArgs {
 // Each thread moves kU vectors of each plane per pass: all 2*kU loads are issued before
 // any store, so a 256-thread workgroup keeps 2*kU*256*sizeof(V) bytes in flight.
 template <typename V, bool kGather, int kU>
-__global__ __launch_bounds__(256) void paged_copy_kernel(PagedCopyArgs a) {
-  const int bid = blockIdx.x;
+__device__ __forceinline__ void paged_copy_entry(const PagedCopyArgs& a, int bid) {
   int ri = 0;
   while (ri + 1 < a.n_ranges && bid >= a.block_begin[ri + 1]) ++ri;
   const PagedRange& R = a.r[ri];
@@ -115,6 +114,13 @@ __global__ __launch_bounds__(256) void paged_copy_kernel(PagedCopyArgs a) {
   }
 }
 
+template <typename V, bool kGather, int kU>
+__global__ __launch_bounds__(256) void paged_copy_kernel(PagedCopyArgs a) {
+  // Workgroup i copies table entries i, i + grid, ... of the concatenated ranges.
+  for (int bid = blockIdx.x; bid < a.block_begin[a.n_ranges]; bid += gridDim.x)
+    paged_copy_entry<V, kGather, kU>(a, bid);
+}
+
 // Host launcher shared by gather and scatter.  Shapes were validated by the caller.
 void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs, int hkv, int d,
                              int elem_bytes, int n, const PagedRangeDesc* ranges, int zero_tail,
@@ -161,7 +167,8 @@ void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs
     if (m == 0) continue;
     a.n_ranges = m;
     a.block_begin[m] = blocks;
-    const dim3 grid(static_cast<unsigned>(blocks));
+    // About two table entries per workgroup (128 KiB for bs=16, Hkv=8, D=128 bf16).
+    const dim3 grid(static_cast<unsigned>(blocks > 2048 ? (blocks + 1) / 2 : blocks));
     // Widest access that every row start and stride allows.
     if (al16) {
       if (gather) paged_copy_kernel<u32x4, true, 8><<<grid, 256, 0, stream>>>(a);
