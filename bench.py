@@ -280,6 +280,19 @@ def cpu_baseline(torch, tensors, budget_s: float = 10.0):
                        f"algorithmic causal FLOPs of those domains / time")
 
 
+def copy_calibration():
+    """Three copies of 1 GiB by torch's plain copy kernel: the PMC counters of these
+    dispatches convert FETCH_SIZE / WRITE_SIZE readings into bytes."""
+    import torch
+
+    a = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_dispatch": a.numel() * 4, "dispatches": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -288,7 +301,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run three plain 1 GiB device copies (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.only_prefill:
         args.no_extra = args.no_cpu = True
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
