@@ -136,11 +136,16 @@ def bench_prefill(H, torch, steps: int, warmup: int):
         rows = c["hq"] * c["chunks"][t]
         mbytes += rows * (parts * (4 * c["d"] + 4) + 2 * c["d"] + 4)
     merge_gbs = mbytes * steps / (mrg_ms * 1e-3) / 1e9
+    # block kernel: Q + K + V reads and fp32 O + LSE writes of every (target, source) pair
+    blk_bytes = sum(c["chunks"][t] * c["hq"] * c["d"] * 2 + 2 * c["chunks"][s_] * c["hkv"] * c["d"] * 2
+                    + c["chunks"][t] * c["hq"] * (c["d"] + 1) * 4
+                    for t in range(n) for s_ in range(n) if offs[s_] <= offs[t] + c["chunks"][t] - 1)
     finite = bool(torch.isfinite(lse).all().item()) and bool(torch.isfinite(out.float()).all().item())
     del ws
     return dict(ms_step=ms_step, tflops=tflops, flops=flops, blk_launches=blk_n // steps,
                 avg_blk_ms=avg_blk_ms, per_launch_flops=per_launch_flops, achieved=achieved,
                 merge_ms=mrg_ms / steps, merge_gbs=merge_gbs, merge_bytes=mbytes, finite=finite,
+                alg_bytes_per_launch=blk_bytes * steps // blk_n,
                 tensors=(q, k, v))
 
 
@@ -280,6 +285,21 @@ def cpu_baseline(torch, tensors, budget_s: float = 10.0):
                        f"algorithmic causal FLOPs of those domains / time")
 
 
+def profiled_traffic(name: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a plain-copy calibration);
+    None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def copy_calibration():
     """Three copies of 1 GiB by torch's plain copy kernel: the PMC counters of these
     dispatches convert FETCH_SIZE / WRITE_SIZE readings into bytes."""
@@ -365,7 +385,9 @@ def main():
                    "flops_per_step": pre["flops"], "frac_mfma_peak": round(pre["tflops"] / PEAK_BF16_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "kernel": "flash_block_kernel",
                      "achieved": round(pre["achieved"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(pre["achieved"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(pre["achieved"] / PEAK_BF16_TFLOPS, 4),
+                     "traffic": profiled_traffic("flash_block_kernel_c3_prefill.md"),
+                     "algorithmic_bytes_per_launch": pre["alg_bytes_per_launch"],
                      "launches_per_step": pre["blk_launches"], "avg_launch_ms": round(pre["avg_blk_ms"], 4),
                      "flops_per_launch": pre["per_launch_flops"]},
         "cpu_baseline": cpu,

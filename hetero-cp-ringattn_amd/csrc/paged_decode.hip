@@ -7,13 +7,13 @@
 // sequence's block table -- no gather, no GQA expand copy.
 //
 // Work split (HBM-bound: every K/V byte is read exactly once):
-//   * grid = (splits, batch).  A workgroup (4 waves) owns one sequence and a
-//     contiguous run of 16-token groups of the chunk, for ALL kv heads, so per 16
-//     tokens it reads the whole K and V rows of those slots (one contiguous span per
-//     plane when bs >= 16).  Wave w handles kv heads w, w+4, ...
-//   * Scores: S^T = K Q^T on MFMA 16x16x32 (A = 16 key rows loaded straight from the
-//     pool, 16 bytes per lane; B = the rep <= 16 query heads of the kv head, zero-padded
-//     to 16 columns, held in registers for the whole kernel).
+//   * grid = (splits, batch, ceil(Hkv / 4)).  A workgroup (4 waves) owns one sequence,
+//     a contiguous run of 16-token groups of the chunk and 4 kv heads: wave w handles
+//     kv head 4*blockIdx.z + w, so per 16 tokens a wave reads 16 K rows and 16 V rows
+//     of its head (4 KiB each for D=128, bf16) straight from the pool.
+//   * Scores: S^T = K Q^T on MFMA 16x16x32 (A = 16 key rows loaded from the pool, 16
+//     bytes per lane; B = the rep <= 4 query heads of the kv head, zero-padded to 16
+//     columns, held in registers for the whole kernel).
 //   * Online softmax per query head in the log2 domain; P goes through a small LDS
 //     slot (broadcast reads) and PV runs on VALU with each lane owning 8 head-dim
 //     values of 4 of the 16 keys (fp32 accumulators), reduced across lanes once at the

@@ -127,6 +127,25 @@ def test_merge_of_partition_equals_full_attention():
     np.testing.assert_allclose(o, parts[0][0], atol=1e-15)
 
 
+@pytest.mark.parametrize("mistake", ["swapped_weights", "lse_without_max", "unnormalised"])
+def test_planted_merge_mistakes_are_caught(mistake):
+    """A merge with a planted mistake no longer reproduces full attention from a partition."""
+    q, k, v = _rand(7, (6, 2, 8)), _rand(8, (20, 2, 8)), _rand(9, (20, 2, 8))
+    qp, kp = np.arange(14, 20), np.arange(20)
+    full_o, full_l = C.attention_f64(q, k, v, qp, kp, 0.3)
+    (o1, l1), (o2, l2) = (C.attention_f64(q, k[a:b], v[a:b], qp, kp[a:b], 0.3) for a, b in ((0, 7), (7, 20)))
+    m = np.maximum(l1, l2)
+    w1, w2 = np.exp(l1 - m), np.exp(l2 - m)
+    if mistake == "swapped_weights":
+        w1, w2 = w2, w1
+    o = (w1[..., None] * o1 + w2[..., None] * o2)
+    if mistake != "unnormalised":
+        o = o / (w1 + w2)[..., None]
+    lse = np.log(w1 + w2) + (0.0 if mistake == "lse_without_max" else m)
+    err = max(np.abs(o - full_o).max(), np.abs(lse - full_l).max())
+    assert err > 1e-3, f"planted {mistake} not detected (err={err})"
+
+
 # ------------------------------------------------------------------ tch restatement ----
 def test_single_block_fold_equals_softmax():
     # ring.rs:2150-2226: one non-causal fold from rm=-inf equals softmax(QK^T)V.
