@@ -3,8 +3,9 @@
 Headline (BASELINE.json ``metric``): ring-prefill TFLOP/s at 32k on the Llama-3-8B
 shape (config c3: S=32768 in 4 uneven domains [12288, 8192, 8192, 4096], 32 query /
 8 KV heads, head_dim 128, bf16, causal).  One step = one full single-GPU ring replay
-(every domain's ring steps, one partial per (domain, source) pair, then the LSE
-merge) through ``hcp_ring_prefill_replay``, inputs resident in HBM.  ``value`` counts
+(every domain's ring steps: one block-kernel launch per non-empty (domain, source)
+pair, each folding its source into the domain's running state, the last one writing
+the output rows) through ``hcp_ring_prefill_replay``, inputs resident in HBM.  ``value`` counts
 algorithmic FLOPs of causal pairs only: 2 GEMMs x 2 x D x Hq x S(S+1)/2.
 
 Also reported on the same line: paged decode GB/s (config c4), KV staging gather GB/s
@@ -123,19 +124,11 @@ def bench_prefill(H, torch, steps: int, warmup: int):
     ms_step = elapsed * 1e3 / steps
     tflops = flops / (ms_step * 1e-3) / 1e12
     blk_ms, blk_n = tm["block"]
-    mrg_ms, mrg_n = tm["merge"]
     per_launch_flops = flops * steps / blk_n
     avg_blk_ms = blk_ms / blk_n
     achieved = per_launch_flops / (avg_blk_ms * 1e-3) / 1e12
-    # merge: algorithmic bytes = partial o+lse reads + bf16 out + fp32 lse writes
     n = len(c["chunks"])
     offs = [sum(c["chunks"][:i]) for i in range(n)]
-    mbytes = 0
-    for t in range(n):
-        parts = sum(1 for s_ in range(n) if offs[s_] <= offs[t] + c["chunks"][t] - 1)
-        rows = c["hq"] * c["chunks"][t]
-        mbytes += rows * (parts * (4 * c["d"] + 4) + 2 * c["d"] + 4)
-    merge_gbs = mbytes * steps / (mrg_ms * 1e-3) / 1e9
     # block kernel: Q + K + V reads and fp32 O + LSE writes of every (target, source) pair
     blk_bytes = sum(c["chunks"][t] * c["hq"] * c["d"] * 2 + 2 * c["chunks"][s_] * c["hkv"] * c["d"] * 2
                     + c["chunks"][t] * c["hq"] * (c["d"] + 1) * 4
@@ -143,10 +136,44 @@ def bench_prefill(H, torch, steps: int, warmup: int):
     finite = bool(torch.isfinite(lse).all().item()) and bool(torch.isfinite(out.float()).all().item())
     del ws
     return dict(ms_step=ms_step, tflops=tflops, flops=flops, blk_launches=blk_n // steps,
-                avg_blk_ms=avg_blk_ms, per_launch_flops=per_launch_flops, achieved=achieved,
-                merge_ms=mrg_ms / steps, merge_gbs=merge_gbs, merge_bytes=mbytes, finite=finite,
+                avg_blk_ms=avg_blk_ms, per_launch_flops=per_launch_flops, achieved=achieved, finite=finite,
                 alg_bytes_per_launch=blk_bytes * steps // blk_n,
                 tensors=(q, k, v))
+
+
+# ------------------------------------------------------------------ c3 merge ----
+def bench_merge(H, torch, steps: int, warmup: int):
+    """The LSE merge kernel (hcp_ring_lse_merge) on the c3 shapes: per target domain,
+    its non-empty ring partials (o [Hq, L, D] + lse [Hq, L] fp32) -> bf16 rows + fp32
+    LSE.  The ring replay itself folds sources as they arrive, so this is the merge
+    entry point's own measurement (the decode path uses it after every chunk)."""
+    c = C3
+    n = len(c["chunks"])
+    offs = [sum(c["chunks"][:i]) for i in range(n)]
+    jobs, mbytes, off = [], 0, 0
+    for t in range(n):
+        parts = sum(1 for s_ in range(n) if offs[s_] <= offs[t] + c["chunks"][t] - 1)
+        L = c["chunks"][t]
+        os_ = [torch.empty(c["hq"], L, c["d"], dtype=torch.float32, device="cuda") for _ in range(parts)]
+        ls_ = [torch.empty(c["hq"], L, dtype=torch.float32, device="cuda") for _ in range(parts)]
+        for x in os_ + ls_:
+            H.synth_normals(c["seed"] + 1, off, x.numel(), x)
+            off += x.numel()
+        out = torch.empty(c["hq"], L, c["d"], dtype=torch.bfloat16, device="cuda")
+        lse = torch.empty(c["hq"], L, dtype=torch.float32, device="cuda")
+        jobs.append((os_, ls_, out, lse))
+        mbytes += c["hq"] * L * (parts * (4 * c["d"] + 4) + 2 * c["d"] + 4)
+
+    def step():
+        for os_, ls_, out, lse in jobs:
+            H.lse_merge(os_, ls_, out=out, lse_out=lse)
+
+    for _ in range(warmup):
+        step()
+    ms = time_cuda(torch, step, steps)
+    res = dict(merge_ms=ms, merge_gbs=mbytes / (ms * 1e-3) / 1e9, merge_bytes=mbytes)
+    del jobs
+    return res
 
 
 # ------------------------------------------------------------------ c4 decode ----
@@ -346,6 +373,8 @@ def main():
         dec = bench_decode(H, torch, args.steps, args.warmup)
         log(f"c4 decode {dec['gbs']:.1f} GB/s")
         stg = bench_staged(H, torch, args.steps, args.warmup)
+        mrg = bench_merge(H, torch, args.steps, args.warmup)
+        log(f"c3 lse merge {mrg['merge_gbs']:.1f} GB/s")
         log(f"c5 gather {stg['gather_gbs']:.1f} GB/s, prefill {stg.get('prefill_tflops', 0):.1f} TFLOP/s")
         extra = dict(
             paged_decode={"workload": "c4: B=64, ctx 16384 in [8192,5120,3072], 32q/8kv, D=128, bf16, bs=16",
@@ -360,8 +389,10 @@ def main():
             staged_prefill_128k={"value": round(stg.get("prefill_tflops", 0.0), 1), "unit": "TFLOP/s",
                                  "ms": round(stg.get("prefill_ms", 0.0), 3),
                                  "frac_mfma": round(stg.get("prefill_tflops", 0.0) / PEAK_BF16_TFLOPS, 4)},
-            lse_merge={"value": round(pre["merge_gbs"], 1), "unit": "GB/s", "ms_per_step": round(pre["merge_ms"], 4),
-                       "frac_hbm": round(pre["merge_gbs"] / PEAK_HBM_GBS, 4), "bytes": pre["merge_bytes"]},
+            lse_merge={"workload": "c3 ring partials of the 4 target domains (10 x [32, L, 128] fp32 + LSE) "
+                                   "-> bf16 rows + fp32 LSE, one hcp_ring_lse_merge per domain",
+                       "value": round(mrg["merge_gbs"], 1), "unit": "GB/s", "ms_per_step": round(mrg["merge_ms"], 4),
+                       "frac_hbm": round(mrg["merge_gbs"] / PEAK_HBM_GBS, 4), "bytes": mrg["merge_bytes"]},
         )
     cpu = None
     if not args.no_cpu:

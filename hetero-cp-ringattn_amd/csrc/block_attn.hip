@@ -44,6 +44,11 @@ struct BlockArgs {
   int32_t causal, accumulate;
   float scale_log2;        // softmax scale * log2(e)
   int32_t n_qtiles, n_groups;
+  void* fin_out;           // final mode when non-null (see BlockLaunch)
+  int32_t fin_dtype;
+  int64_t fin_hs, fin_ss;
+  float* fin_lse;
+  int64_t fin_lse_hs;
 };
 
 namespace {
@@ -132,6 +137,74 @@ __device__ __forceinline__ float max_xor32(float x) {
 __device__ __forceinline__ float sum_xor32(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Stores 4 consecutive fp32 values as `dtype` at element offset `off` of `base`.
+__device__ __forceinline__ void store4(void* base, int dtype, int64_t off, float x0, float x1, float x2, float x3) {
+  if (dtype == kF32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(base) + off) = make_float4(x0, x1, x2, x3);
+  } else {
+    u32x2 w;
+    if (dtype == kBF16) {
+      w[0] = static_cast<uint32_t>(f32_to_bf16_bits(x0)) | (static_cast<uint32_t>(f32_to_bf16_bits(x1)) << 16);
+      w[1] = static_cast<uint32_t>(f32_to_bf16_bits(x2)) | (static_cast<uint32_t>(f32_to_bf16_bits(x3)) << 16);
+    } else {
+      w[0] = static_cast<uint32_t>(f32_to_f16_bits(x0)) | (static_cast<uint32_t>(f32_to_f16_bits(x1)) << 16);
+      w[1] = static_cast<uint32_t>(f32_to_f16_bits(x2)) | (static_cast<uint32_t>(f32_to_f16_bits(x3)) << 16);
+    }
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + off) = w;
+  }
+}
+
+// Epilogue of one (head, query row): normalise O, LSE in natural log; in accumulate
+// mode merge with the running fp32 partial in (o, lse) (the rm = lse, rs = 1 re-entry
+// of ring.rs:585-587 in closed form); write either the fp32 state or, in final mode,
+// the output rows in the query dtype.  Lanes l and l + 32 hold the two interleaved
+// 4-wide d slices of each 8-wide group.
+template <int D>
+__device__ __forceinline__ void write_row(const BlockArgs& a, int head, int my_q, int lhalf,
+                                          const f32x16 (&oacc)[D / 32], float m_run, float l_tot) {
+  constexpr int DB = D / 32;
+  const bool any = l_tot > 0.f;
+  const float inv = any ? 1.f / l_tot : 0.f;
+  const float lse_new = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+  const int64_t row = static_cast<int64_t>(head) * a.lq + my_q;
+  float* orow = a.o + row * D;
+  float c_old = 0.f, c_new = inv, lse_out = lse_new;
+  if (a.accumulate) {
+    const float lse_old = a.lse[row];
+    const float m = fmaxf(lse_old, lse_new);
+    const bool m_ok = m != -INFINITY;
+    const float w_old = m_ok ? __expf(lse_old - m) : 0.f;
+    const float w_new = m_ok ? __expf(lse_new - m) : 0.f;
+    const float den = w_old + w_new;
+    const float rden = den > 0.f ? 1.f / den : 0.f;
+    c_old = w_old * rden;
+    c_new = w_new * rden * inv;
+    lse_out = m_ok ? m + __logf(den) : -INFINITY;
+  }
+  const int64_t fin_row = head * a.fin_hs + static_cast<int64_t>(my_q) * a.fin_ss;
+#pragma unroll
+  for (int b = 0; b < DB; ++b)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int dcol = 32 * b + 8 * j + 4 * lhalf;
+      float x0 = c_new * oacc[b][4 * j], x1 = c_new * oacc[b][4 * j + 1];
+      float x2 = c_new * oacc[b][4 * j + 2], x3 = c_new * oacc[b][4 * j + 3];
+      if (a.accumulate) {
+        const float4 old = *reinterpret_cast<const float4*>(orow + dcol);
+        x0 += c_old * old.x; x1 += c_old * old.y; x2 += c_old * old.z; x3 += c_old * old.w;
+      }
+      if (a.fin_out) store4(a.fin_out, a.fin_dtype, fin_row + dcol, x0, x1, x2, x3);
+      else *reinterpret_cast<float4*>(orow + dcol) = make_float4(x0, x1, x2, x3);
+    }
+  if (lhalf == 0) {
+    if (a.fin_out) {
+      if (a.fin_lse) a.fin_lse[head * a.fin_lse_hs + my_q] = lse_out;
+    } else {
+      a.lse[row] = lse_out;
+    }
+  }
 }
 
 template <int D, int DT, int G>
@@ -368,43 +441,288 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 
   // ---- epilogue: normalise, LSE (natural log), optional merge with running partial ----
   if (my_q >= a.lq) return;
-  const float l_tot = sum_xor32(l_run);
-  const bool any = l_tot > 0.f;
-  const float inv = any ? 1.f / l_tot : 0.f;
-  const float lse_new = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
-  const int64_t row = static_cast<int64_t>(head) * a.lq + my_q;
-  float* orow = a.o + row * D;
-  if (!a.accumulate) {
-#pragma unroll
-    for (int b = 0; b < DB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float4 v = make_float4(oacc[b][4 * j] * inv, oacc[b][4 * j + 1] * inv, oacc[b][4 * j + 2] * inv,
-                               oacc[b][4 * j + 3] * inv);
-        *reinterpret_cast<float4*>(orow + 32 * b + 8 * j + 4 * lhalf) = v;
-      }
-    if (lhalf == 0) a.lse[row] = lse_new;
-  } else {
-    const float lse_old = a.lse[row];
-    const float m = fmaxf(lse_old, lse_new);
-    const bool m_ok = m != -INFINITY;
-    const float w_old = m_ok ? __expf(lse_old - m) : 0.f;
-    const float w_new = m_ok ? __expf(lse_new - m) : 0.f;
-    const float den = w_old + w_new;
-    const float rden = den > 0.f ? 1.f / den : 0.f;
-    const float c_old = w_old * rden;
-    const float c_new = w_new * rden * inv;
-#pragma unroll
-    for (int b = 0; b < DB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float4* p = reinterpret_cast<float4*>(orow + 32 * b + 8 * j + 4 * lhalf);
-        const float4 old = *p;
-        *p = make_float4(c_old * old.x + c_new * oacc[b][4 * j], c_old * old.y + c_new * oacc[b][4 * j + 1],
-                         c_old * old.z + c_new * oacc[b][4 * j + 2], c_old * old.w + c_new * oacc[b][4 * j + 3]);
-      }
-    if (lhalf == 0) a.lse[row] = m_ok ? m + __logf(den) : -INFINITY;
+  write_row<D>(a, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run));
+}
+
+// ----------------------------------------------------------------------------------
+// Head-dim-128 kernel with asynchronous global->LDS loads.
+//
+// Same wave layout and math as flash_block_kernel (8 waves, one query head and 32
+// query tokens per wave, S^T = K Q^T with K rows in kperm order, P^T straight from the
+// S^T accumulators), but the K and V tiles reach LDS without passing through
+// registers:
+//   * buffer_load_dwordx4 ... lds writes 1 KiB per wave instruction (4 rows of 64 keys
+//     x 128 dims); three tiles in flight (triple-buffered LDS, loads of tile t+2 issued
+//     while tile t is computed), so there are no staging registers, no VALU transpose
+//     and no LDS stores on the compute waves' path.
+//   * For LDS chunk p of row r the DMA fetches global chunk p ^ swz(r): K rows use
+//     swz = r & 15, V rows 4 * (r & 3), which makes the fragment reads below
+//     bank-conflict free.
+//   * K fragments (A of S^T) are ds_read_b128; V^T fragments (A of O^T = V^T P^T) come
+//     from row-major V through ds_read_b64_tr_b16: two reads give one lane the 8 keys
+//     of its head-dim column.
+//   * The loop is unrolled by the buffer count so each LDS address is a per-lane
+//     register set up once plus an immediate offset.
+// ----------------------------------------------------------------------------------
+constexpr int kNBuf3 = 3;
+constexpr int kD3 = 128;
+constexpr int kTile3 = kBK * kD3 * 2;  // bytes of one K or V tile (16 KiB)
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// Buffer descriptor as four SGPRs (base, stride 0, num_records, flags): reads past the
+// end return zeros.
+__device__ __forceinline__ u32x4 make_srd(const void* base, int64_t bytes) {
+  const uint32_t n = bytes <= 0 ? 0u : (bytes > 0x7ffffff0LL ? 0x7ffffff0u : static_cast<uint32_t>(bytes));
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane(n);
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// One wave-wide 16-byte-per-lane load straight into LDS at lds_addr + 16 * lane.  The
+// compiler does not track it: callers wait with s_waitcnt vmcnt themselves.
+__device__ __forceinline__ void dma16(u32x4 srd, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(srd), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);  // vmcnt(N), expcnt/lgkmcnt unconstrained
+}
+
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
+template <int DT, int G>
+__global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs a) {
+  using Ops = MfmaOps<DT>;
+  using frag = typename Ops::frag;
+  constexpr int D = kD3;
+  constexpr int TB = kWaves / G;
+  constexpr int TQ = 32 * TB;
+  constexpr int KS = D / 16;
+  constexpr int DB = D / 32;
+  constexpr int kDmaPerWave = kBK / 4 / kWaves;  // 1 KiB DMA instructions per wave per tile (K or V)
+
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kNBuf3 * kBK * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[kNBuf3 * kBK * D];
+
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int hg = logical / a.n_qtiles;
+  const int qt = a.n_qtiles - 1 - logical % a.n_qtiles;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int lcol = lane & 31;
+  const int lhalf = lane >> 5;
+
+  const int head = hg * G + (wave % G);
+  const int kvh = (hg * G) / a.rep;
+  const int tq0 = qt * TQ;
+  const int wq0 = tq0 + (wave / G) * 32;
+  const int my_q = wq0 + lcol;
+  const int q_end = min(a.lq, tq0 + TQ);
+
+  int n_kv = a.lk;
+  if (a.causal) {
+    const int64_t lim = a.q_off + q_end - a.k_off;
+    n_kv = static_cast<int>(lim <= 0 ? 0 : (lim < a.lk ? lim : a.lk));
   }
+  const int n_tiles = (n_kv + kBK - 1) / kBK;
+
+  // ---- DMA set-up: wave w fills rows 8w .. 8w+7 of every K and V tile ----
+  const uint16_t* kbase = a.k + kvh * a.k_hs;
+  const uint16_t* vbase = a.v + kvh * a.v_hs;
+  const uint32_t k_lds0 = lds_offset(k_lds) + wave * (kDmaPerWave * 1024);
+  const uint32_t v_lds0 = lds_offset(v_lds) + wave * (kDmaPerWave * 1024);
+  uint32_t k_voff[kDmaPerWave], v_voff[kDmaPerWave];
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int r = (wave * kDmaPerWave + j) * 4 + (lane >> 4);  // tile row this lane loads
+    const int p = lane & 15;                                     // LDS chunk of the row
+    k_voff[j] = static_cast<uint32_t>(r * a.k_ss * 2 + ((p ^ (r & 15)) << 4));
+    v_voff[j] = static_cast<uint32_t>(r * a.v_ss * 2 + ((p ^ (4 * (r & 3))) << 4));
+  }
+  auto issue_tile = [&](int t, int buf) __attribute__((always_inline)) {
+    const int kv0 = t * kBK;
+    const u32x4 ks = make_srd(kbase + static_cast<int64_t>(kv0) * a.k_ss, static_cast<int64_t>(a.lk - kv0) * a.k_ss * 2);
+    const u32x4 vs = make_srd(vbase + static_cast<int64_t>(kv0) * a.v_ss, static_cast<int64_t>(a.lk - kv0) * a.v_ss * 2);
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j) dma16(ks, k_voff[j], k_lds0 + buf * kTile3 + j * 1024);
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j) dma16(vs, v_voff[j], v_lds0 + buf * kTile3 + j * 1024);
+  };
+
+  if (n_tiles > 0) issue_tile(0, 0);
+  if (n_tiles > 1) issue_tile(1, 1);
+
+  frag qf[KS];
+  {
+    const uint16_t* qbase = a.q + head * a.q_hs + static_cast<int64_t>(wq0) * a.q_ss;
+    const auto qr = make_rsrc(qbase, static_cast<int64_t>(a.lq - wq0) * a.q_ss * 2);
+    const int32_t qoff = (lcol * static_cast<int32_t>(a.q_ss) + lhalf * 8) * 2;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = as_frag<frag>(buf_load16(qr, qoff + 32 * s));
+  }
+
+  // ---- per-lane LDS read addresses (byte offsets within buffer 0) ----
+  // K: row 32b + kperm(lcol), chunk (lhalf + 2s) ^ swz, swz = row & 15 = kperm(lcol) & 15.
+  const int krow = kperm(lcol);
+  uint32_t k_rd[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) k_rd[s] = krow * (D * 2) + (((lhalf + 2 * s) ^ (krow & 15)) << 4);
+  // V (transposing reads): lane group g = lane / 16 and sub-lane sl = lane % 16 read row
+  // 16s + 8(g/2) + 4h + sl/4 (h = 0, 1 for the two reads), dims 32b + 16(g%2) + 4(sl%4).
+  const int g16 = lane >> 4, sl = lane & 15;
+  uint32_t v_rd[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b)
+    v_rd[b] = (8 * (g16 >> 1) + (sl >> 2)) * (D * 2) +
+              ((4 * (b ^ (sl >> 2)) + 2 * (g16 & 1) + ((sl & 3) >> 1)) << 4) + 8 * (sl & 1);
+  const char* k_lds_c = reinterpret_cast<const char*>(k_lds);
+  const char* v_lds_c = reinterpret_cast<const char*>(v_lds);
+
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
+  float m_run = kInitMax;
+  float l_run = 0.f;
+
+  const float c = a.scale_log2;
+  const int64_t qlim64 = a.q_off + my_q - a.k_off;
+  const int64_t wave_lim_first = a.q_off + wq0 - a.k_off;
+  const int64_t wave_lim_last = a.q_off + min(wq0 + 31, a.lq - 1) - a.k_off;
+
+  __builtin_amdgcn_s_waitcnt(0);  // Q fragments and tiles 0, 1 resident
+  __syncthreads();
+
+  auto compute = [&](int t, auto bufc) __attribute__((always_inline)) {
+    constexpr int bf = decltype(bufc)::value;
+    const int kv0 = t * kBK;
+    const bool wave_live = !a.causal || kv0 <= wave_lim_last;
+    if (!(wave_live && wq0 < a.lq)) return;
+    const bool need_mask = (kv0 + kBK > a.lk) || (a.causal && kv0 + kBK - 1 > wave_lim_first);
+
+    // ---- S^T = K Q^T for two 32-key blocks ----
+    f32x16 sacc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[b][r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const frag kf = as_frag<frag>(
+            *reinterpret_cast<const u32x4*>(k_lds_c + k_rd[s] + (bf * kTile3 + b * 32 * D * 2)));
+        sacc[b] = Ops::mma(kf, qf[s], sacc[b]);
+      }
+    }
+    // Keep four K fragment reads in flight ahead of the MFMAs that consume them.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // 4 LDS reads
+#pragma unroll
+    for (int i = 0; i < 2 * KS - 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // last 4 MFMAs
+
+    // ---- mask (boundary tiles only), tile max, lazy rescale ----
+    if (need_mask) {
+      int64_t lim64 = a.lk - 1 - kv0;
+      if (a.causal) lim64 = min(lim64, qlim64 - kv0);
+      const int lim = static_cast<int>(max(min(lim64, static_cast<int64_t>(kBK)), static_cast<int64_t>(-1))) - 8 * lhalf;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = r >> 2, i = r & 3;
+          const int kl0 = 32 * b + 16 * (j >> 1) + 4 * (j & 1) + i;
+          sacc[b][r] = kl0 <= lim ? sacc[b][r] : -INFINITY;
+        }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[b][r]);
+    tmax = max_xor32(tmax) * c;
+    const bool grow = tmax > m_run + kRescaleThreshold;
+    if (__any(grow)) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int b = 0; b < DB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
+      m_run = m_new;
+    }
+
+    // ---- P = 2^(s*c - m) as 16-bit B operands, row-sum partial ----
+    frag pf[4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][r], c, -m_run));
+        l_run += p[r];
+      }
+      pf[2 * b] = Ops::pack(p);
+      pf[2 * b + 1] = Ops::pack(p + 8);
+    }
+
+    // ---- O^T += V^T P^T, V^T fragments by transposing reads of row-major V ----
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int b = 0; b < DB; ++b) {
+        const char* p0 = v_lds_c + v_rd[b] + (bf * kTile3 + s * 16 * D * 2);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0 + 4 * D * 2));
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+        oacc[b] = Ops::mma(as_frag<frag>(u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}), pf[s], oacc[b]);
+      }
+    }
+  };
+
+  // One step per buffer: issue tile t+2, compute tile t, wait for this wave's loads of
+  // tile t+1 (the newer t+2 loads may stay in flight), barrier.
+  auto step = [&](int t, auto bufc) __attribute__((always_inline)) {
+    constexpr int bf = decltype(bufc)::value;
+    const bool ahead = t + 2 < n_tiles;
+    if (ahead) issue_tile(t + 2, (bf + 2) % kNBuf3);
+    compute(t, bufc);
+    if (t + 1 < n_tiles) {
+      if (ahead) wait_vmcnt<2 * kDmaPerWave>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+    }
+  };
+  for (int t = 0; t < n_tiles; t += kNBuf3) {
+    step(t, IntC<0>{});
+    if (t + 1 < n_tiles) step(t + 1, IntC<1>{});
+    if (t + 2 < n_tiles) step(t + 2, IntC<2>{});
+  }
+
+  if (my_q >= a.lq) return;
+  write_row<D>(a, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run));
 }
 
 // ----------------------------------------------------------------------------------
@@ -421,6 +739,11 @@ struct GenArgs {
   int64_t q_off, k_off;
   int32_t causal, accumulate;
   float scale;
+  void* fin_out;
+  int32_t fin_dtype;
+  int64_t fin_hs, fin_ss;
+  float* fin_lse;
+  int64_t fin_lse_hs;
 };
 
 constexpr int kGenRows = 64;
@@ -480,10 +803,8 @@ __global__ __launch_bounds__(kGenRows) void general_block_kernel(GenArgs a) {
   const float inv = any ? 1.f / l : 0.f;
   const float lse_new = any ? m + __logf(l) : -INFINITY;
   const int64_t orow = static_cast<int64_t>(head) * a.lq + row;
-  if (!a.accumulate) {
-    for (int i = 0; i < d && i < DMAX; ++i) a.o[orow * d + i] = acc[i] * inv;
-    a.lse[orow] = lse_new;
-  } else {
+  float c_old = 0.f, c_new = inv, lse_out = lse_new;
+  if (a.accumulate) {
     const float lse_old = a.lse[orow];
     const float mm = fmaxf(lse_old, lse_new);
     const bool ok = mm != -INFINITY;
@@ -491,9 +812,20 @@ __global__ __launch_bounds__(kGenRows) void general_block_kernel(GenArgs a) {
     const float w_new = ok ? __expf(lse_new - mm) : 0.f;
     const float den = w_old + w_new;
     const float rden = den > 0.f ? 1.f / den : 0.f;
-    for (int i = 0; i < d && i < DMAX; ++i)
-      a.o[orow * d + i] = (w_old * a.o[orow * d + i] + w_new * acc[i] * inv) * rden;
-    a.lse[orow] = ok ? mm + __logf(den) : -INFINITY;
+    c_old = w_old * rden;
+    c_new = w_new * rden * inv;
+    lse_out = ok ? mm + __logf(den) : -INFINITY;
+  }
+  for (int i = 0; i < d && i < DMAX; ++i) {
+    float x = c_new * acc[i];
+    if (a.accumulate) x += c_old * a.o[orow * d + i];
+    if (a.fin_out) store_elem_rt(a.fin_out, a.fin_dtype, head * a.fin_hs + static_cast<int64_t>(row) * a.fin_ss + i, x);
+    else a.o[orow * d + i] = x;
+  }
+  if (a.fin_out) {
+    if (a.fin_lse) a.fin_lse[head * a.fin_lse_hs + row] = lse_out;
+  } else {
+    a.lse[orow] = lse_out;
   }
 }
 
@@ -520,6 +852,8 @@ static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   a.causal = L.causal;
   a.accumulate = L.accumulate;
   a.scale_log2 = L.scale * kLog2e;
+  a.fin_out = L.fin_out; a.fin_dtype = L.fin_dtype; a.fin_hs = L.fin_hs; a.fin_ss = L.fin_ss;
+  a.fin_lse = L.fin_lse; a.fin_lse_hs = L.fin_lse_hs;
   int g = 1;
   for (int cand : {8, 4, 2}) {
     if (a.rep % cand == 0) { g = cand; break; }
@@ -528,6 +862,15 @@ static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   a.n_qtiles = static_cast<int32_t>(ceil_div(L.lq, tq));
   a.n_groups = L.hq / g;
   const dim3 grid(static_cast<unsigned>(a.n_qtiles * a.n_groups));
+  if (D == kD3) {
+    switch (g) {
+      case 8: flash_block_dma_kernel<DT, 8><<<grid, kThreads, 0, stream>>>(a); break;
+      case 4: flash_block_dma_kernel<DT, 4><<<grid, kThreads, 0, stream>>>(a); break;
+      case 2: flash_block_dma_kernel<DT, 2><<<grid, kThreads, 0, stream>>>(a); break;
+      default: flash_block_dma_kernel<DT, 1><<<grid, kThreads, 0, stream>>>(a); break;
+    }
+    return;
+  }
   switch (g) {
     case 8: flash_block_kernel<D, DT, 8><<<grid, kThreads, 0, stream>>>(a); break;
     case 4: flash_block_kernel<D, DT, 4><<<grid, kThreads, 0, stream>>>(a); break;
@@ -547,6 +890,8 @@ static void launch_general(const BlockLaunch& L, hipStream_t stream) {
   a.q_off = L.q_off; a.k_off = L.k_off;
   a.causal = L.causal; a.accumulate = L.accumulate;
   a.scale = L.scale;
+  a.fin_out = L.fin_out; a.fin_dtype = L.fin_dtype; a.fin_hs = L.fin_hs; a.fin_ss = L.fin_ss;
+  a.fin_lse = L.fin_lse; a.fin_lse_hs = L.fin_lse_hs;
   const dim3 grid(static_cast<unsigned>(ceil_div(L.lq, kGenRows)), static_cast<unsigned>(L.hq));
   if (L.d <= 64) general_block_kernel<DT, 64><<<grid, kGenRows, 0, stream>>>(a);
   else if (L.d <= 128) general_block_kernel<DT, 128><<<grid, kGenRows, 0, stream>>>(a);

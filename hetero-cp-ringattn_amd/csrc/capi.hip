@@ -124,7 +124,7 @@ struct ReplayPlan {
   int n;
   std::vector<int64_t> len, off;
   std::vector<std::vector<int>> sources;  // per target, in ring order, non-empty only
-  std::vector<std::vector<size_t>> part_off;  // byte offsets of each (target, source) partial
+  std::vector<size_t> state_off;          // byte offset of each target's running fp32 (o, lse)
   size_t partial_bytes = 0;
   size_t staging_off = 0;
   size_t staging_bytes_per_domain = 0;
@@ -199,7 +199,7 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
   require(acc <= INT32_MAX, "total sequence length must fit in int32");
   p.seq = acc;
   p.sources.resize(p.n);
-  p.part_off.resize(p.n);
+  p.state_off.resize(p.n);
   size_t cur = 0;
   for (int t = 0; t < p.n; ++t) {
     for (int s = 0; s < p.n; ++s) {
@@ -207,7 +207,10 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
       // A source wholly in the target's future contributes nothing (ring.rs:222-228).
       if (d->causal && p.off[src] > p.off[t] + p.len[t] - 1) continue;
       p.sources[t].push_back(src);
-      p.part_off[t].push_back(cur);
+    }
+    // A target with one source writes its output rows directly and needs no state.
+    p.state_off[t] = cur;
+    if (p.sources[t].size() > 1) {
       const size_t rows = static_cast<size_t>(d->num_q_heads) * p.len[t];
       cur += align256(rows * d->head_dim * sizeof(float)) + align256(rows * sizeof(float));
     }
@@ -297,31 +300,27 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
       bd.q_offset = p.off[t];
       bd.kv_offset = p.off[src];
       bd.causal = d->causal;
-      bd.accumulate = 0;
+      // Sources arrive in ring order and are folded into the target's running fp32
+      // state as they come (positioned_merge_compact_partial, ring.rs:574-603); the
+      // last one also normalises into the output rows [off_t, off_t + len_t) and the
+      // LSE, so no separate merge pass is needed.
+      bd.accumulate = idx > 0 ? 1 : 0;
       bd.scale = d->scale;
-      char* part = base + p.part_off[t][idx];
+      char* state = base + p.state_off[t];
       const size_t rows = static_cast<size_t>(d->num_q_heads) * p.len[t];
-      float* po = reinterpret_cast<float*>(part);
-      float* pl = reinterpret_cast<float*>(part + align256(rows * d->head_dim * sizeof(float)));
-      const BlockLaunch L = make_launch(&bd, qv, kv_k, kv_v, po, pl);
+      float* po = reinterpret_cast<float*>(state);
+      float* pl = reinterpret_cast<float*>(state + align256(rows * d->head_dim * sizeof(float)));
+      BlockLaunch L = make_launch(&bd, qv, kv_k, kv_v, po, pl);
+      if (idx + 1 == static_cast<int>(p.sources[t].size())) {
+        L.fin_out = static_cast<char*>(out.data) + p.off[t] * out.seq_stride * es;
+        L.fin_dtype = d->dtype;
+        L.fin_hs = out.head_stride;
+        L.fin_ss = out.seq_stride;
+        L.fin_lse = lse_out ? lse_out + p.off[t] : nullptr;
+        L.fin_lse_hs = p.seq;
+      }
       timed(kTimedBlock, stream, [&] { launch_block_partial(L, stream); });
     }
-  }
-  // Final merge per target domain into the output rows [off_t, off_t + len_t).
-  for (int t = 0; t < p.n; ++t) {
-    std::vector<const float*> os, ls;
-    const size_t rows = static_cast<size_t>(d->num_q_heads) * p.len[t];
-    for (size_t i = 0; i < p.sources[t].size(); ++i) {
-      char* part = base + p.part_off[t][i];
-      os.push_back(reinterpret_cast<const float*>(part));
-      ls.push_back(reinterpret_cast<const float*>(part + align256(rows * d->head_dim * sizeof(float))));
-    }
-    char* o_ptr = static_cast<char*>(out.data) + p.off[t] * out.seq_stride * es;
-    timed(kTimedMerge, stream, [&] {
-      launch_lse_merge(static_cast<int>(os.size()), os.data(), ls.data(), d->num_q_heads, p.len[t],
-                       d->head_dim, d->dtype, o_ptr, out.head_stride, out.seq_stride,
-                       lse_out ? lse_out + p.off[t] : nullptr, p.seq, stream);
-    });
   }
 }
 

@@ -16,6 +16,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 enum DType : int32_t { kF16 = 1, kBF16 = 2, kF32 = 3, kI32 = 4, kI64 = 5 };
 
@@ -93,6 +94,12 @@ __device__ __forceinline__ void store_elem<kBF16>(void* p, int64_t i, float v) {
 template <>
 __device__ __forceinline__ void store_elem<kF16>(void* p, int64_t i, float v) {
   static_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v);
+}
+// Store with the dtype chosen at run time.
+__device__ __forceinline__ void store_elem_rt(void* p, int dtype, int64_t i, float v) {
+  if (dtype == kF32) store_elem<kF32>(p, i, v);
+  else if (dtype == kBF16) store_elem<kBF16>(p, i, v);
+  else store_elem<kF16>(p, i, v);
 }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

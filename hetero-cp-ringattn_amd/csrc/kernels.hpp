@@ -17,6 +17,15 @@ struct BlockLaunch {
   int causal, accumulate;
   float scale;
   bool force_general;  // take the general kernel even where the matrix-core one applies
+  // Final mode (fin_out != nullptr): instead of the fp32 state (o, lse), write the
+  // normalised rows in fin_dtype to fin_out[head * fin_hs + row * fin_ss + d] and the
+  // LSE to fin_lse[head * fin_lse_hs + row] (after merging the running state first
+  // when accumulate is set).
+  void* fin_out = nullptr;
+  int fin_dtype = 0;
+  int64_t fin_hs = 0, fin_ss = 0;
+  float* fin_lse = nullptr;
+  int64_t fin_lse_hs = 0;
 };
 
 bool block_uses_mfma(int dtype, int d);

@@ -232,11 +232,14 @@ int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_
  * split: domain d owns global positions [off_d, off_d + chunk_lens[d]) (vanilla
  * assignment, rust/src/model/attention/strategy.rs:53-63), visits sources
  * (d - s) mod N for s = 0..N-1 (local first, then the predecessor chain), skips
- * sources entirely in its future (ring.rs:222-228), computes one partial per
- * (domain, source) with (1) and merges them with (2).  q/k/v/out cover the whole
+ * sources entirely in its future (ring.rs:222-228), and folds each source into the
+ * domain's running fp32 (o, lse) state as it arrives with (1) in accumulate mode (the
+ * positioned_merge_compact_partial re-entry, ring.rs:574-603); the last source of a
+ * domain writes the normalised rows straight into out.  q/k/v/out cover the whole
  * sequence (global token index = view token index).  out receives the merged
  * attention (dtype = desc->dtype), lse_out (may be NULL) the merged LSE [Hq, S] fp32.
- * Workspace: hcp_ring_replay_workspace_size bytes.
+ * Workspace: hcp_ring_replay_workspace_size bytes (one fp32 state per domain with
+ * more than one source, plus the paged staging area).
  *
  * With a paged pool (hcp_ring_prefill_replay_paged), K/V are not given as views: each
  * source domain's chunk is first gathered with (3) from the pool through block_table

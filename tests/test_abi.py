@@ -52,8 +52,9 @@ def test_paged_rejects_short_table(hcp):
 def test_replay_workspace_size_matches_plan(hcp):
     chunks = [12288, 8192, 8192, 4096]
     n = hcp.replay_workspace_size(torch.bfloat16, 32, 8, 128, chunks)
-    # 10 non-empty (target, source) pairs; per pair o [32, L, 128] + lse [32, L] fp32.
-    rows = 32 * (12288 + 2 * 8192 + 3 * 8192 + 4 * 4096)
+    # One running fp32 state o [32, L, 128] + lse [32, L] per domain with more than one
+    # source: domain 0 only sees itself and writes its rows directly.
+    rows = 32 * (8192 + 8192 + 4096)
     assert n == rows * 128 * 4 + rows * 4
     assert hcp.replay_workspace_size(torch.bfloat16, 32, 8, 128, [5, 0]) == 0
 
