@@ -464,7 +464,7 @@ int hcp_paged_kv_gather_batch(const hcp_paged_pool* pool, int32_t num_ranges, co
 size_t hcp_paged_decode_workspace_size(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool) {
   if (desc == nullptr || pool == nullptr || desc->batch <= 0) return 0;
   (void)pool;
-  return decode_workspace_bytes(desc->batch, desc->num_q_heads, desc->num_kv_heads, desc->head_dim, desc->t0, desc->t1);
+  return decode_workspace_bytes(desc->dtype, desc->batch, desc->num_q_heads, desc->num_kv_heads, desc->head_dim, desc->t0, desc->t1);
 }
 
 int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool, hcp_ring_view q,

@@ -53,7 +53,7 @@ void launch_paged_copy(bool gather, void* pool, int64_t num_blocks, int bs, int 
                        int64_t t1, void* k_buf, void* v_buf, int64_t head_stride, int64_t seq_stride,
                        int zero_tail, int* err, hipStream_t stream);
 
-size_t decode_workspace_bytes(int batch, int hq, int hkv, int d, int64_t t0, int64_t t1);
+size_t decode_workspace_bytes(int dtype, int batch, int hq, int hkv, int d, int64_t t0, int64_t t1);
 void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const void* q, int64_t q_bs,
                          int64_t q_hs, const void* pool, int64_t num_blocks, int bs,
                          const int32_t* tables, int64_t table_stride, int64_t table_len,

@@ -20,6 +20,10 @@
 //     end.
 //   * Each split writes (o, lse) to the workspace; the LSE merge kernel combines the
 //     splits of a sequence (heads = batch*Hq, q_len = 1).
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "kernels.hpp"
 
 namespace hcp {
@@ -265,17 +269,47 @@ struct DecodePlan {
   int64_t g_begin;
 };
 
-DecodePlan plan_decode(int batch, int hkv, int64_t t0, int64_t t1) {
+// Workgroups of the decode kernel resident at once on the current device (CUs x
+// occupancy); 768 (256 CUs x 3) when no device can be queried.
+int decode_slots(int d, int dtype) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 768;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(dev, d, dtype);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int cus = 0, per_cu = 0;
+  const void* fn = dtype == kBF16 ? (d == 128 ? reinterpret_cast<const void*>(&paged_decode_kernel<128, kBF16>)
+                                              : reinterpret_cast<const void*>(&paged_decode_kernel<64, kBF16>))
+                                  : (d == 128 ? reinterpret_cast<const void*>(&paged_decode_kernel<128, kF16>)
+                                              : reinterpret_cast<const void*>(&paged_decode_kernel<64, kF16>));
+  int slots = 768;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) == hipSuccess && cus > 0 && per_cu > 0)
+    slots = cus * per_cu;
+  else
+    (void)hipGetLastError();
+  cache[key] = slots;
+  return slots;
+}
+
+DecodePlan plan_decode(int batch, int hkv, int d, int dtype, int64_t t0, int64_t t1) {
   DecodePlan p;
   p.g_begin = t0 / 16;
   const int64_t g_end = t1 > t0 ? (t1 + 15) / 16 : p.g_begin;
   p.n_groups = static_cast<int>(g_end - p.g_begin);
-  // Aim for ~16 workgroups per CU on 256 CUs (grid = splits x batch x kv-head groups),
-  // at least 4 groups (64 keys) per split.
-  const int target = 4096;
-  const int per_split = std::max(batch, 1) * ((hkv + kDecWaves - 1) / kDecWaves);
-  int splits = static_cast<int>(ceil_div(target, per_split));
-  splits = std::max(1, std::min(splits, 64));
+  // grid = splits x batch x kv-head groups.  One round of resident workgroups: a
+  // partial second round leaves most CUs idle for its whole length (a measured 13-25%
+  // loss at c4), and fewer splits also mean fewer partials to merge.  At least 4 groups
+  // (64 keys) per split.
+  const int rows = std::max(batch, 1) * ((hkv + kDecWaves - 1) / kDecWaves);
+  int splits = std::max(1, decode_slots(d, dtype) / rows);
+  splits = std::min(splits, 64);
   int gps = static_cast<int>(ceil_div(std::max(p.n_groups, 1), splits));
   gps = std::max(gps, 4);
   p.groups_per_split = gps;
@@ -283,8 +317,8 @@ DecodePlan plan_decode(int batch, int hkv, int64_t t0, int64_t t1) {
   return p;
 }
 
-size_t decode_workspace_bytes(int batch, int hq, int hkv, int d, int64_t t0, int64_t t1) {
-  const DecodePlan p = plan_decode(batch, hkv, t0, t1);
+size_t decode_workspace_bytes(int dtype, int batch, int hq, int hkv, int d, int64_t t0, int64_t t1) {
+  const DecodePlan p = plan_decode(batch, hkv, d, dtype, t0, t1);
   const size_t rows = static_cast<size_t>(p.splits) * batch * hq;
   auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   return al(rows * d * sizeof(float)) + al(rows * sizeof(float));
@@ -299,8 +333,8 @@ void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const voi
   require(bs % 16 == 0, "paged_decode: block_size must be a multiple of 16");
   require(d == 64 || d == 128, "paged_decode: head_dim must be 64 or 128");
   require(dtype == kBF16 || dtype == kF16, "paged_decode: dtype must be BF16 or F16");
-  const DecodePlan p = plan_decode(batch, hkv, t0, t1);
-  require(ws_bytes >= decode_workspace_bytes(batch, hq, hkv, d, t0, t1), "paged_decode: workspace too small");
+  const DecodePlan p = plan_decode(batch, hkv, d, dtype, t0, t1);
+  require(ws_bytes >= decode_workspace_bytes(dtype, batch, hq, hkv, d, t0, t1), "paged_decode: workspace too small");
   auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   const size_t rows = static_cast<size_t>(p.splits) * batch * hq;
   float* ws_o = static_cast<float*>(ws);
