@@ -129,16 +129,38 @@ def bench_prefill(H, torch, steps: int, warmup: int):
     achieved = per_launch_flops / (avg_blk_ms * 1e-3) / 1e12
     n = len(c["chunks"])
     offs = [sum(c["chunks"][:i]) for i in range(n)]
-    # block kernel: Q + K + V reads and fp32 O + LSE writes of every (target, source) pair
-    blk_bytes = sum(c["chunks"][t] * c["hq"] * c["d"] * 2 + 2 * c["chunks"][s_] * c["hkv"] * c["d"] * 2
-                    + c["chunks"][t] * c["hq"] * (c["d"] + 1) * 4
-                    for t in range(n) for s_ in range(n) if offs[s_] <= offs[t] + c["chunks"][t] - 1)
+    blk_bytes = sum(b for _, _, b in block_launch_bytes(c))
     finite = bool(torch.isfinite(lse).all().item()) and bool(torch.isfinite(out.float()).all().item())
     del ws
     return dict(ms_step=ms_step, tflops=tflops, flops=flops, blk_launches=blk_n // steps,
                 avg_blk_ms=avg_blk_ms, per_launch_flops=per_launch_flops, achieved=achieved, finite=finite,
                 alg_bytes_per_launch=blk_bytes * steps // blk_n,
                 tensors=(q, k, v))
+
+
+def block_launch_bytes(c):
+    """Algorithmic HBM bytes of every block-kernel launch of one replay step, in launch
+    order (ring step by ring step, targets ascending): Q + K + V reads, plus the
+    running fp32 state (O + LSE) written by a domain's first source, read and written
+    by its middle sources, read by its last source, which writes the output rows
+    (bf16) and the fp32 LSE instead."""
+    n = len(c["chunks"])
+    offs = [sum(c["chunks"][:i]) for i in range(n)]
+    d, hq, hkv = c["d"], c["hq"], c["hkv"]
+    srcs = {t: [(t - s) % n for s in range(n) if offs[(t - s) % n] <= offs[t] + c["chunks"][t] - 1] for t in range(n)}
+    out = []
+    for step in range(n):
+        for t in range(n):
+            src = (t - step) % n
+            if src not in srcs[t]:
+                continue
+            i, last = srcs[t].index(src), len(srcs[t]) - 1
+            rows = c["chunks"][t] * hq
+            b = rows * d * 2 + 2 * c["chunks"][src] * hkv * d * 2
+            b += rows * (d + 1) * 4 * ((i > 0) + (i < last))   # state read / write
+            b += rows * (2 * d + 4) * (i == last)               # output rows + LSE
+            out.append((t, src, b))
+    return out
 
 
 # ------------------------------------------------------------------ c3 merge ----
@@ -243,9 +265,8 @@ def bench_staged(H, torch, steps: int, warmup: int, full_prefill: bool = True):
 
     ranges = [(table, 0, o, o + L, stage_k[:, o:o + L], stage_v[:, o:o + L]) for o, L in zip(offs, c["chunks"])]
 
-    def gather_all():
-        # every domain's chunk staged by one batched launch (8 ranges)
-        H.paged_kv_gather_batch(pool, ranges)
+    # every domain's chunk staged by one batched launch (8 ranges); descriptors built once
+    gather_all = H.paged_gather_plan(pool, ranges)
 
     for _ in range(warmup):
         gather_all()

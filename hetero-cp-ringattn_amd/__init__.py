@@ -277,12 +277,25 @@ def paged_kv_scatter(pool, block_table, table_seq_offset, t0, t1, k_in, v_in, ze
 
 def paged_kv_gather_batch(pool, ranges, stream=None):
     """ranges: list of (block_table, table_seq_offset, t0, t1, k_out, v_out); one launch."""
+    paged_gather_plan(pool, ranges, stream)()
+
+
+def paged_gather_plan(pool, ranges, stream=None):
+    """Builds the descriptors of a batched gather once and returns a callable that
+    launches it (for repeated staging of the same ranges without per-call host work).
+    The tensors must stay alive while the callable is used."""
     n = len(ranges)
     arr = (PagedRange * max(n, 1))()
     for i, (tab, off, t0, t1, ko, vo) in enumerate(ranges):
         arr[i] = PagedRange(tab.data_ptr(), tab.numel(), off, t0, t1, view(ko), view(vo))
     pp = paged_pool(pool)
-    _check(lib().hcp_paged_kv_gather_batch(ctypes.byref(pp), n, arr, _stream(stream)))
+    st = _stream(stream)
+    fn = lib().hcp_paged_kv_gather_batch
+
+    def run():
+        _check(fn(ctypes.byref(pp), n, arr, st))
+
+    return run
 
 
 def fetch_device_errors(stream=None) -> int:
