@@ -72,6 +72,12 @@ class PagedRange(ctypes.Structure):
                 ("k_out", View), ("v_out", View)]
 
 
+class DecodeShard(ctypes.Structure):
+    _fields_ = [("block_tables", ctypes.c_void_p), ("table_stride", ctypes.c_int64),
+                ("table_len", ctypes.c_int64), ("seq_lens", ctypes.c_void_p),
+                ("max_len", ctypes.c_int64)]
+
+
 class DecodeDesc(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int32), ("batch", ctypes.c_int32),
                 ("num_q_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
@@ -119,6 +125,12 @@ def lib() -> ctypes.CDLL:
                                              ctypes.POINTER(PagedPool)], ctypes.c_size_t),
         "hcp_paged_decode_partial": ([ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedPool), View,
                                       vp, vp, vp, vp, vp, ctypes.c_size_t, vp], ctypes.c_int),
+        "hcp_decode_ring_owner": ([i64, i32], ctypes.c_int),
+        "hcp_decode_ring_workspace_size": ([ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedPool), i32,
+                                            ctypes.POINTER(DecodeShard)], ctypes.c_size_t),
+        "hcp_decode_ring_replay": ([ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedPool), View, i32,
+                                    ctypes.POINTER(DecodeShard), i32, View, vp, vp, ctypes.c_size_t, vp],
+                                   ctypes.c_int),
         "hcp_ring_replay_workspace_size": ([ctypes.POINTER(ReplayDesc), i32], ctypes.c_size_t),
         "hcp_ring_prefill_replay": ([ctypes.POINTER(ReplayDesc), View, View, View, View, vp, vp,
                                      ctypes.c_size_t, vp], ctypes.c_int),
@@ -339,6 +351,55 @@ def decode_local_compact_partial(q, pool, block_tables, t0, t1, seq_lens=None, s
                                           _ptr(block_tables), _ptr(seq_lens), _ptr(o), _ptr(lse),
                                           _ptr(workspace), workspace.numel(), _stream(stream)))
     return o, lse
+
+
+# ---------------------------------------------------------------------------------
+# (4b) decode Q-ring with growth sharding
+# ---------------------------------------------------------------------------------
+def decode_ring_owner(global_pos: int, num_domains: int) -> int:
+    """Domain that persists the decode token at global_pos (ring.rs:1921-1942)."""
+    r = lib().hcp_decode_ring_owner(global_pos, num_domains)
+    if r < 0:
+        raise HcpRingError(r, "bad position or domain count")
+    return r
+
+
+def _shards(shards):
+    arr = (DecodeShard * len(shards))()
+    for i, (tables, seq_lens, max_len) in enumerate(shards):
+        arr[i] = DecodeShard(tables.data_ptr() if tables is not None else None,
+                             tables.stride(0) if tables is not None else 0,
+                             tables.shape[1] if tables is not None else 0,
+                             seq_lens.data_ptr() if seq_lens is not None else None, max_len)
+    return arr
+
+
+def decode_ring_replay(q, pool, shards, seed_domain, scale=None, out=None, lse_out=None, workspace=None,
+                       stream=None):
+    """ring_decode_attention (ring.rs:665-818) for a batch on one GPU.
+
+    q [B, Hq, D]; shards: per domain (block_tables [B, n] int32, seq_lens [B] int32 or
+    None, max_len); the packet starts at seed_domain and visits its successors.
+    Returns (out [B, Hq, D] in q's dtype, lse [B, Hq] fp32)."""
+    torch = _torch()
+    b, hq, d = q.shape
+    desc = DecodeDesc(dtype_code(q.dtype), b, hq, pool.shape[3], d, 0, 0, 0, 0, 0,
+                      scale if scale is not None else 1.0 / math.sqrt(d))
+    pp = paged_pool(pool)
+    arr = _shards(shards)
+    n = len(shards)
+    need = lib().hcp_decode_ring_workspace_size(ctypes.byref(desc), ctypes.byref(pp), n, arr)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+    if lse_out is None:
+        lse_out = torch.empty((b, hq), dtype=torch.float32, device=q.device)
+    qv = View(q.data_ptr(), q.stride(1), q.stride(0))
+    ov = View(out.data_ptr(), out.stride(1), out.stride(0))
+    _check(lib().hcp_decode_ring_replay(ctypes.byref(desc), ctypes.byref(pp), qv, n, arr, seed_domain, ov,
+                                        _ptr(lse_out), _ptr(workspace), workspace.numel(), _stream(stream)))
+    return out, lse_out
 
 
 # ---------------------------------------------------------------------------------

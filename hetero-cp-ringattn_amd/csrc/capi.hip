@@ -491,6 +491,93 @@ int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_
   });
 }
 
+// ---- decode Q-ring replay ----
+namespace {
+struct DecodeRingPlan {
+  size_t part_o = 0, part_lse = 0, part_bytes = 0, dec_off = 0, total = 0;
+};
+DecodeRingPlan plan_decode_ring(const hcp_paged_decode_desc* desc, int n, const hcp_decode_shard* shards) {
+  require(desc != nullptr && shards != nullptr, "null descriptor or shards");
+  require(n >= 1 && n <= 64, "num_domains must be in [1, 64]");
+  require(desc->batch > 0 && desc->num_q_heads > 0 && desc->head_dim > 0, "bad decode shape");
+  DecodeRingPlan p;
+  const size_t rows = static_cast<size_t>(desc->batch) * desc->num_q_heads;
+  p.part_o = align256(rows * desc->head_dim * sizeof(float));
+  p.part_lse = align256(rows * sizeof(float));
+  p.part_bytes = p.part_o + p.part_lse;
+  p.dec_off = p.part_bytes * n;
+  size_t dec = 0;
+  for (int i = 0; i < n; ++i) {
+    require(shards[i].max_len >= 0, "shard max_len must be >= 0");
+    dec = std::max(dec, decode_workspace_bytes(desc->dtype, desc->batch, desc->num_q_heads, desc->num_kv_heads,
+                                               desc->head_dim, 0, shards[i].max_len));
+  }
+  p.total = p.dec_off + align256(dec);
+  return p;
+}
+}  // namespace
+
+int hcp_decode_ring_owner(int64_t global_pos, int32_t num_domains) {
+  if (num_domains <= 0 || global_pos < 0) return HCP_RING_E_INVALID;
+  return static_cast<int>(global_pos % num_domains);
+}
+
+size_t hcp_decode_ring_workspace_size(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool,
+                                      int32_t num_domains, const hcp_decode_shard* shards) {
+  (void)pool;
+  try {
+    return plan_decode_ring(desc, num_domains, shards).total;
+  } catch (...) {
+    return 0;
+  }
+}
+
+int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool, hcp_ring_view q,
+                           int32_t num_domains, const hcp_decode_shard* shards, int32_t seed_domain,
+                           hcp_ring_view out, float* lse_out, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  return guarded(__func__, [&] {
+    const DecodeRingPlan plan = plan_decode_ring(desc, num_domains, shards);
+    check_pool(pool);
+    require(seed_domain >= 0 && seed_domain < num_domains, "seed_domain out of range");
+    require(desc->num_kv_heads == pool->num_kv_heads && desc->head_dim == pool->head_dim,
+            "descriptor does not match the pool");
+    require(pool->elem_bytes == 2, "paged decode needs a 16-bit pool");
+    require(desc->scale > 0.f, "scale must be positive");
+    require(workspace != nullptr && workspace_bytes >= plan.total,
+            "workspace too small: need " + std::to_string(plan.total) + " bytes");
+    check_view(q, "q", 1);
+    require(mfma_layout_ok(q), "q must be 16-byte aligned with strides multiple of 8");
+    check_view(out, "out", 1);
+    check_out_view(out, desc->dtype);
+    require(out.seq_stride == static_cast<int64_t>(desc->num_q_heads) * out.head_stride,
+            "out must hold the [batch, Hq] rows at one stride (seq_stride == Hq * head_stride)");
+    char* base = static_cast<char*>(workspace);
+    std::vector<const float*> os, ls;
+    for (int j = 0; j < num_domains; ++j) {
+      // Journey order: the seed domain's partial first, then its successors.
+      const int dom = (seed_domain + j) % num_domains;
+      const hcp_decode_shard& sh = shards[dom];
+      float* po = reinterpret_cast<float*>(base + static_cast<size_t>(j) * plan.part_bytes);
+      float* pl = reinterpret_cast<float*>(base + static_cast<size_t>(j) * plan.part_bytes + plan.part_o);
+      if (sh.max_len > 0) {
+        require(sh.block_tables != nullptr, "null block table of a non-empty shard");
+        require(sh.table_len >= 1 && sh.table_stride >= sh.table_len, "bad shard table shape");
+        require((sh.max_len - 1) / pool->block_size < sh.table_len, "shard block table too short");
+      }
+      launch_paged_decode(desc->dtype, desc->batch, desc->num_q_heads, desc->num_kv_heads, desc->head_dim, q.data,
+                          q.seq_stride, q.head_stride, pool->data, pool->num_blocks, pool->block_size,
+                          sh.block_tables, sh.table_stride, std::max<int64_t>(sh.table_len, 1), sh.seq_lens, 0,
+                          sh.max_len, desc->scale, po, pl, base + plan.dec_off, workspace_bytes - plan.dec_off,
+                          device_error_flags(), as_stream(stream));
+      os.push_back(po);
+      ls.push_back(pl);
+    }
+    launch_lse_merge(num_domains, os.data(), ls.data(), desc->batch * desc->num_q_heads, 1, desc->head_dim,
+                     desc->dtype, out.data, out.head_stride, out.head_stride, lse_out, 1, as_stream(stream));
+  });
+}
+
 size_t hcp_ring_replay_workspace_size(const hcp_ring_replay_desc* desc, int32_t paged) {
   try {
     return plan_replay(desc, paged != 0).total;

@@ -100,7 +100,10 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   int64_t t_end = a.t1;
   if (a.seq_lens != nullptr) t_end = min(t_end, static_cast<int64_t>(a.seq_lens[b]));
   const int g0 = split * a.groups_per_split;
-  const int g1 = min(a.n_groups, g0 + a.groups_per_split);
+  // Stop at this sequence's own last group: table entries past its length may be
+  // padding (ragged batches) and are neither read nor validated.
+  const int64_t g_seq = t_end > a.t0 ? (t_end + 15) / 16 - a.g_begin : 0;
+  const int g1 = static_cast<int>(min(static_cast<int64_t>(min(a.n_groups, g0 + a.groups_per_split)), g_seq));
   const int32_t* table = a.tables + static_cast<int64_t>(b) * a.table_stride;
 
   // Q^T fragments: lane (col, grp) holds Q[head kvh*rep + col][grp*8 + 32*s .. +8].

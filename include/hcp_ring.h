@@ -196,7 +196,8 @@ int hcp_paged_kv_gather_batch(const hcp_paged_pool* pool, int32_t num_ranges,
  * and attends, without a causal mask (ring.rs:631-637), to its tokens
  * [t0, min(t1, seq_lens[b])) read straight from the paged pool through row b of
  * block_tables (token t in block block_tables[b*table_stride + t/block_size]).
- * seq_lens may be NULL (every sequence covers [t0, t1)).  Outputs fp32:
+ * seq_lens may be NULL (every sequence covers [t0, t1)); table entries past a
+ * sequence's own range are neither read nor validated (ragged padding).  Outputs fp32:
  *     o [batch, num_q_heads, head_dim], lse [batch, num_q_heads] (-inf, o = 0 when the
  *     range is empty).
  * The chunk is split across workgroups; workspace holds the split partials
@@ -224,6 +225,45 @@ int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_
                              hcp_ring_view q, const int32_t* block_tables,
                              const int32_t* seq_lens, float* o, float* lse, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * (4b) Decode Q-ring with growth sharding (ring_decode_attention, ring.rs:665-818;
+ * ownership rule ring.rs:1921-1942; KvCache::update_sharded, cache.rs:40-48,104-121).
+ *
+ * Each of num_domains domains holds its own shard of every sequence's KV in the paged
+ * pool: its prefill chunk plus the decode tokens it owns (the token at global
+ * position p is persisted only by domain hcp_decode_ring_owner(p, N) = p mod N; the
+ * other domains drop it).  Together the shards hold every token once, the new token
+ * included: its owner appends it (hcp_paged_kv_scatter) before the call, as
+ * update_sharded(keep = true) does.  The ring starts a packet (q, o, lse) at
+ * seed_domain with the partial over that domain's shard, and the packet visits
+ * seed+1, seed+2, ... (mod N), each domain merging its shard into the accumulator
+ * (decode_merge_packet, ring.rs:647-663).  After N-1 hops the accumulator is the
+ * layer's attention output; the seed only fixes the merge order.
+ * This entry replays the whole journey on one GPU: one hcp_paged_decode_partial-style
+ * pass per shard, then the closed-form merge in journey order into out (q dtype,
+ * [batch, Hq, D] as a view with head_stride / seq_stride = batch stride) and lse_out
+ * ([batch, Hq] fp32, may be NULL).  An empty shard passes the packet through
+ * unchanged (lse + log 1).  desc->t0/t1 are ignored: shard s covers tokens
+ * [0, shards[s].max_len) of its table, clipped per sequence by shards[s].seq_lens.
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_decode_shard {
+  const int32_t* block_tables; /* DEVICE int32 [batch, table_stride], this domain's tables */
+  int64_t table_stride;
+  int64_t table_len;           /* entries used per sequence (>= ceil(max_len / block_size)) */
+  const int32_t* seq_lens;     /* DEVICE int32 [batch] tokens held per sequence, or NULL */
+  int64_t max_len;             /* upper bound of seq_lens (tokens) */
+} hcp_decode_shard;
+
+int hcp_decode_ring_owner(int64_t global_pos, int32_t num_domains);
+
+size_t hcp_decode_ring_workspace_size(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool,
+                                      int32_t num_domains, const hcp_decode_shard* shards);
+
+int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool,
+                           hcp_ring_view q, int32_t num_domains, const hcp_decode_shard* shards,
+                           int32_t seed_domain, hcp_ring_view out, float* lse_out, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * (5) Single-GPU ring replay of a whole prefill (the ring_attention driver).

@@ -14,6 +14,7 @@ this module replays the same ATen op sequence through PyTorch's CPU backend:
 * :func:`positioned_merge_compact_partial`  ring.rs:574-603
 * :func:`decode_local_partial`        ring.rs:625-639 (+ compact variant :515-523)
 * :func:`decode_merge_packet`         ring.rs:647-663 (+ compact variant :525-536)
+* :func:`ring_decode_attention`       ring.rs:665-818 (the decode Q-ring, one packet's journey)
 * :func:`ring_attention`              ring.rs:861-1398 (tiling, order, early exit, output)
 * :func:`ring_attention_replay`       CS2 of the reference tests (ring.rs:3014-3165,
                                       3230-3364): every domain driven in one process,
@@ -140,6 +141,27 @@ def decode_merge_packet(scale, q, o, lse, k, v):
     k_pos = torch.zeros(k.shape[2], dtype=torch.int64)
     rm, rs, obh = process_kv_block(scale, q, q_pos, k, v, k_pos, rm, rs, obh, False)
     return obh, (rm + rs.log()).to(torch.float32)
+
+
+def ring_decode_attention(scale, q, durable, cur_k, cur_v, seed: int):
+    """One packet's journey of ring_decode_attention (ring.rs:665-818).
+
+    durable[d] = (k, v) of domain d before this step, compact heads [B, Hkv, L_d, D]
+    (growth sharding, ring.rs:1930-1936); cur_k / cur_v = the new token [B, Hkv, 1, D].
+    Phase 0 seeds the packet at domain `seed` with the partial over its local segment
+    [durable; current token] (decode_local_partial); each of the N-1 rounds merges the
+    next domain's durable segment without the current token (k_peer = narrow(0,
+    local_len - 1), decode_merge_packet), visiting seed+1, ..., seed-1 (mod N).  An
+    empty durable segment passes the packet through unchanged (lse + log 1)."""
+    n = len(durable)
+    k, v = durable[seed]
+    o, lse = decode_local_compact_partial(scale, q, torch.cat([k, cur_k], 2), torch.cat([v, cur_v], 2))
+    for j in range(1, n):
+        k, v = durable[(seed + j) % n]
+        if k.shape[2] == 0:
+            continue
+        o, lse = decode_merge_compact_partial(scale, q, o, lse, k, v)
+    return o, lse
 
 
 def decode_merge_compact_partial(scale, q, o, lse, k, v):

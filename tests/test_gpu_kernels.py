@@ -322,3 +322,82 @@ def test_paged_gather_batch_bit_exact(gpu):
             continue
         assert np.array_equal(_np_bits(ko), ref[0]) and np.array_equal(_np_bits(vo), ref[1])
     assert H.fetch_device_errors() == 0
+
+
+DECODE_RING_CASES = [
+    # name, prefill chunk per domain, decode steps per sequence, Hq, Hkv, D, block_size
+    ("three_domains_uneven", [300, 200, 200], [5, 9, 2], 16, 4, 128, 16),
+    ("four_domains_one_empty", [160, 96, 64, 0], [0, 1, 2], 8, 2, 64, 32),
+    ("four_domains_ragged_zero", [160, 96, 64, 0], [1, 2, 3], 32, 8, 128, 16),
+]
+
+
+@pytest.mark.parametrize("case", DECODE_RING_CASES, ids=[c[0] for c in DECODE_RING_CASES])
+def test_decode_ring_growth_sharding(gpu, case):
+    """ring_decode_attention (ring.rs:665-818) over growth-sharded paged shards: every
+    seed gives full-KV attention of the new token, and matches the oracle's journey."""
+    name, chunks, steps, hq, hkv, d, bs = case
+    n, b = len(chunks), len(steps)
+    prefill = sum(chunks)
+    starts = np.concatenate([[0], np.cumsum(chunks)])
+    pos = [prefill + s for s in steps]            # the new token's global position
+    total = max(pos) + 1
+    (q, k_all, v_all), (q32, k32, v32) = draw(70 + n, [(b, hq, d), (b, total, hkv, d), (b, total, hkv, d)],
+                                               torch.bfloat16)
+    # shard[dom][i] = global positions domain dom holds for sequence i, the new token
+    # included at its owner (update_sharded keep = true appends before attention)
+    shard = [[list(range(starts[dom], starts[dom + 1])) +
+              [p for p in range(prefill, pos[i] + 1) if H.decode_ring_owner(p, n) == dom] for i in range(b)]
+             for dom in range(n)]
+    nblk = [[-(-len(shard[dom][i]) // bs) for i in range(b)] for dom in range(n)]
+    nb = sum(map(sum, nblk)) + 3
+    perm = I.permuted_block_table(80 + n, nb)
+    pool = torch.zeros((2, nb, bs, hkv, d), dtype=torch.bfloat16)
+    kc, vc = k_all.cpu(), v_all.cpu()
+    shards, cursor = [], 0
+    for dom in range(n):
+        width = max(max(nblk[dom]), 1)
+        tab = np.full((b, width), -1, dtype=np.int32)   # ragged padding is never read
+        for i in range(b):
+            tab[i, :nblk[dom][i]] = perm[cursor:cursor + nblk[dom][i]]
+            cursor += nblk[dom][i]
+            for j, p in enumerate(shard[dom][i]):
+                pool[0, tab[i, j // bs], j % bs] = kc[i, p]
+                pool[1, tab[i, j // bs], j % bs] = vc[i, p]
+        lens = [len(shard[dom][i]) for i in range(b)]
+        max_len = max(lens)
+        shards.append((torch.from_numpy(tab).cuda() if max_len else None,
+                       torch.tensor(lens, dtype=torch.int32).cuda(), max_len))
+    pool = pool.cuda()
+    scale = 1 / math.sqrt(d)
+    for seed in range(n):
+        out, lse = H.decode_ring_replay(q, pool, shards, seed)
+        torch.cuda.synchronize()
+        out, lse = out.float().cpu().numpy(), lse.cpu().numpy()
+        assert H.fetch_device_errors() == 0
+        for i in range(b):
+            kp, vp = k32[i, :pos[i] + 1], v32[i, :pos[i] + 1]
+            ref_o, ref_l = C.attention_f64(q32[i:i + 1], kp, vp, np.zeros(1), np.zeros(pos[i] + 1), scale,
+                                           causal=False)
+            assert np.abs(out[i] - ref_o[0]).max() <= OUT_TOL, (name, seed, i)
+            assert np.abs(lse[i] - ref_l[0]).max() <= LSE_TOL, (name, seed, i)
+            # the oracle's journey on fp32 upcasts: durable shards without the new token
+            durable = []
+            for dom in range(n):
+                idx = [p for p in shard[dom][i] if p != pos[i]]
+                durable.append((bhsd(k32[i, idx]), bhsd(v32[i, idx])))
+            cur = pos[i]
+            to, tl = T.ring_decode_attention(scale, bhsd(q32[i:i + 1]), durable, bhsd(k32[i, cur:cur + 1]),
+                                             bhsd(v32[i, cur:cur + 1]), seed)
+            assert np.abs(out[i] - to[0, :, 0].numpy()).max() <= OUT_TOL, (name, seed, i)
+            assert np.abs(lse[i] - tl[0, :, 0].numpy()).max() <= LSE_TOL, (name, seed, i)
+
+
+def test_decode_ring_rejects_bad_seed_and_owner(gpu):
+    q = torch.zeros(1, 4, 64, dtype=torch.bfloat16, device="cuda")
+    pool = torch.zeros(2, 2, 16, 1, 64, dtype=torch.bfloat16, device="cuda")
+    tab = torch.zeros(1, 1, dtype=torch.int32, device="cuda")
+    with pytest.raises(H.HcpRingError):
+        H.decode_ring_replay(q, pool, [(tab, None, 4), (tab, None, 4)], 2)
+    with pytest.raises(H.HcpRingError):
+        H.decode_ring_owner(5, 0)

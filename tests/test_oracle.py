@@ -216,6 +216,58 @@ def test_decode_partial_merge_matches_closed_form():
     assert np.abs(l[0, :, 0].numpy() - ref_l[0]).max() < 1e-5
 
 
+def _growth_shards(k, v, chunks, upto, n):
+    """Durable segments after growth sharding: prefill chunk of each domain plus the
+    decode tokens it owns (position p kept by domain p mod N, ring.rs:1930-1936)."""
+    f = lambda x: _bhsd(x.astype(np.float32))
+    prefill = chunks[-1][1]
+    out = []
+    for d, (a, b) in enumerate(chunks):
+        idx = list(range(a, b)) + [p for p in range(prefill, upto) if p % n == d]
+        out.append((f(k[idx]), f(v[idx])))
+    return out
+
+
+@pytest.mark.parametrize("double_count", [False, True])
+def test_decode_q_ring_growth_sharding_matches_closed_form(double_count):
+    # The reference's own decode Q-ring check (ring.rs:3400-3560): three domains with
+    # uneven prefill chunks [0,3) [3,5) [5,7), growth-sharded decode steps, every node's
+    # final packet equals full-KV attention.  The planted mistake merges the current
+    # token again in Phase 2 (k instead of k_peer) and must be rejected.
+    n, chunks, steps = 3, [(0, 3), (3, 5), (5, 7)], 4
+    total = chunks[-1][1] + steps
+    k, v = _rand(30, (total, 2, 16)), _rand(31, (total, 2, 16))
+    qs = _rand(32, (steps, 1, 4, 16))
+    f = lambda x: _bhsd(x.astype(np.float32))
+    for t in range(steps):
+        pos = chunks[-1][1] + t
+        ref_o, ref_l = C.attention_f64(qs[t], k[:pos + 1], v[:pos + 1], np.array([0]), np.arange(pos + 1), 0.25,
+                                       causal=False)
+        durable = _growth_shards(k, v, chunks, pos, n)
+        if double_count:
+            durable = [(torch.cat([a, f(k[pos:pos + 1])], 2), torch.cat([b, f(v[pos:pos + 1])], 2))
+                       for a, b in durable]
+        for seed in range(n):
+            o, l = T.ring_decode_attention(0.25, f(qs[t]), durable, f(k[pos:pos + 1]), f(v[pos:pos + 1]), seed)
+            err = np.abs(o[0, :, 0].numpy() - ref_o[0]).max()
+            if double_count:
+                assert err > 1e-3, f"double-counted current token not detected (err={err})"
+            else:
+                assert err < 1e-5
+                assert np.abs(l[0, :, 0].numpy() - ref_l[0]).max() < 1e-5
+
+
+def test_decode_q_ring_empty_durable_segment_passes_packet():
+    # A domain that owns nothing yet (N > prefill chunks' owners) leaves the packet as is.
+    k, v, q = _rand(33, (5, 1, 8)), _rand(34, (5, 1, 8)), _rand(35, (1, 2, 8))
+    f = lambda x: _bhsd(x.astype(np.float32))
+    durable = [(f(k[:4]), f(v[:4])), (f(k[:0]), f(v[:0]))]
+    ref_o, _ = C.attention_f64(q, k, v, np.array([0]), np.arange(5), 0.3, causal=False)
+    for seed in (0, 1):
+        o, _ = T.ring_decode_attention(0.3, f(q), durable, f(k[4:]), f(v[4:]), seed)
+        assert np.abs(o[0, :, 0].numpy() - ref_o[0]).max() < 1e-5
+
+
 def test_fully_future_source_gives_zero_and_neg_inf():
     q, k, v = (torch.randn(1, 2, 3, 4) for _ in range(3))
     o, l = T.positioned_local_compact_partial(0.5, q, torch.arange(3), k, v, torch.arange(5, 8))
