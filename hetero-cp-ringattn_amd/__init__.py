@@ -91,7 +91,21 @@ class ReplayDesc(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int32), ("num_q_heads", ctypes.c_int32),
                 ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
                 ("num_domains", ctypes.c_int32), ("causal", ctypes.c_int32),
-                ("chunk_lens", ctypes.POINTER(ctypes.c_int64)), ("scale", ctypes.c_float)]
+                ("chunk_lens", ctypes.POINTER(ctypes.c_int64)), ("scale", ctypes.c_float),
+                ("strategy", ctypes.c_int32)]
+
+
+# RingSchedulingStrategy (strategy.rs:14-24) -> HCP_STRATEGY_*
+STRATEGIES = {"vanilla": 0, "striped": 1, "zigzag": 2}
+
+
+def strategy_code(strategy) -> int:
+    if isinstance(strategy, int):
+        return strategy
+    key = str(strategy).lower()
+    if key not in STRATEGIES:
+        raise ValueError(f"unknown strategy {strategy!r} (vanilla, striped or zigzag)")
+    return STRATEGIES[key]
 
 
 _lib = None
@@ -113,6 +127,12 @@ def lib() -> ctypes.CDLL:
         "hcp_ring_fetch_device_errors": ([vp, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
         "hcp_ring_block_partial": ([ctypes.POINTER(BlockDesc), View, View, View, vp, vp, vp],
                                    ctypes.c_int),
+        "hcp_ring_block_partial_positioned_workspace_size": ([ctypes.POINTER(BlockDesc)], ctypes.c_size_t),
+        "hcp_ring_block_partial_positioned": ([ctypes.POINTER(BlockDesc), View, vp, View, View, vp, vp, vp, vp,
+                                               ctypes.c_size_t, vp], ctypes.c_int),
+        "hcp_ring_build_assignment": ([i32, i32, ctypes.POINTER(i64), ctypes.POINTER(i32)], ctypes.c_int),
+        "hcp_ring_domain_positions": ([i32, i32, ctypes.POINTER(i64), ctypes.POINTER(i64)], ctypes.c_int),
+        "hcp_ring_inverse_perm": ([i32, i32, ctypes.POINTER(i64), ctypes.POINTER(i64)], ctypes.c_int),
         "hcp_ring_lse_merge": ([i32, ctypes.POINTER(vp), ctypes.POINTER(vp), i32, i64, i32, i32,
                                 View, vp, vp], ctypes.c_int),
         "hcp_paged_kv_gather": ([ctypes.POINTER(PagedPool), vp, i64, i64, i64, i64, View, View,
@@ -222,17 +242,52 @@ def block_partial(q, k, v, q_offset: int, kv_offset: int, causal: bool = True,
     return o, lse
 
 
+def block_partial_positioned(q, q_positions, k, v, kv_positions, causal: bool = True,
+                             scale: float | None = None, o=None, lse=None, accumulate: bool = False,
+                             workspace=None, stream=None):
+    """As :func:`block_partial` with explicit global positions: q_positions [Lq] and
+    kv_positions [Lk] (device int64, keys non-decreasing); key j is visible to query i
+    iff kv_positions[j] <= q_positions[i] (ring.rs:249-273)."""
+    torch = _torch()
+    hq, lq, d = q.shape
+    hkv, lk, _ = k.shape
+    if o is None:
+        o = torch.empty((hq, lq, d), dtype=torch.float32, device=q.device)
+    if lse is None:
+        lse = torch.empty((hq, lq), dtype=torch.float32, device=q.device)
+    desc = BlockDesc(dtype_code(q.dtype), hq, hkv, d, lq, lk, 0, 0, 1 if causal else 0, 1 if accumulate else 0,
+                     scale if scale is not None else 1.0 / math.sqrt(d))
+    for name, t, n in (("q_positions", q_positions, lq), ("kv_positions", kv_positions, lk)):
+        if t.dtype != torch.int64 or t.numel() != n or not t.is_contiguous() or t.device != q.device:
+            raise ValueError(f"{name} must be a contiguous int64 tensor of {n} elements on {q.device}")
+    need = lib().hcp_ring_block_partial_positioned_workspace_size(ctypes.byref(desc))
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    _check(lib().hcp_ring_block_partial_positioned(ctypes.byref(desc), view(q), _ptr(q_positions), view(k),
+                                                   view(v), _ptr(kv_positions), _ptr(o), _ptr(lse),
+                                                   _ptr(workspace), workspace.numel(), _stream(stream)))
+    return o, lse
+
+
 def positioned_local_compact_partial(q, q_offset, k, v, kv_offset, scale=None, stream=None):
-    """ring.rs:538-571 on the GPU: causal partial over one source -> (o fp32, lse fp32)."""
-    return block_partial(q, k, v, q_offset, kv_offset, True, scale, stream=stream)
+    """ring.rs:538-571 on the GPU: causal partial over one source -> (o fp32, lse fp32).
+
+    q_offset / kv_offset are either the global start of contiguous positions (ints) or
+    position tensors (device int64, as the reference's q_pos / k_pos)."""
+    if isinstance(q_offset, int) and isinstance(kv_offset, int):
+        return block_partial(q, k, v, q_offset, kv_offset, True, scale, stream=stream)
+    return block_partial_positioned(q, q_offset, k, v, kv_offset, True, scale, stream=stream)
 
 
 def positioned_merge_compact_partial(q, q_offset, o, lse, k, v, kv_offset, scale=None,
                                      stream=None):
     """ring.rs:574-603 on the GPU: merge (o, lse) with one more causal source (new tensors)."""
     o2, l2 = o.clone(), lse.clone()
-    return block_partial(q, k, v, q_offset, kv_offset, True, scale, o=o2, lse=l2,
-                         accumulate=True, stream=stream)
+    if isinstance(q_offset, int) and isinstance(kv_offset, int):
+        return block_partial(q, k, v, q_offset, kv_offset, True, scale, o=o2, lse=l2,
+                             accumulate=True, stream=stream)
+    return block_partial_positioned(q, q_offset, k, v, kv_offset, True, scale, o=o2, lse=l2,
+                                    accumulate=True, stream=stream)
 
 
 # ---------------------------------------------------------------------------------
@@ -405,26 +460,29 @@ def decode_ring_replay(q, pool, shards, seed_domain, scale=None, out=None, lse_o
 # ---------------------------------------------------------------------------------
 # (5) ring replay
 # ---------------------------------------------------------------------------------
-def replay_desc(dtype, hq, hkv, d, chunks, causal=True, scale=None):
+def replay_desc(dtype, hq, hkv, d, chunks, causal=True, scale=None, strategy="vanilla"):
     arr = (ctypes.c_int64 * len(chunks))(*chunks)
     desc = ReplayDesc(dtype_code(dtype), hq, hkv, d, len(chunks), 1 if causal else 0, arr,
-                      scale if scale is not None else 1.0 / math.sqrt(d))
+                      scale if scale is not None else 1.0 / math.sqrt(d), strategy_code(strategy))
     return desc, arr
 
 
-def replay_workspace_size(dtype, hq, hkv, d, chunks, causal=True, paged=False) -> int:
-    desc, _arr = replay_desc(dtype, hq, hkv, d, chunks, causal)
+def replay_workspace_size(dtype, hq, hkv, d, chunks, causal=True, paged=False, strategy="vanilla") -> int:
+    desc, _arr = replay_desc(dtype, hq, hkv, d, chunks, causal, strategy=strategy)
     return lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 1 if paged else 0)
 
 
 def ring_attention_replay(q, k, v, chunks, causal=True, scale=None, out=None, lse_out=None,
-                          workspace=None, stream=None):
+                          workspace=None, stream=None, strategy="vanilla"):
     """Every domain's ring on one GPU.  q [Hq, S, D], k/v [Hkv, S, D] (strided views ok)
-    -> (out [Hq, S, D] in q's dtype, lse [Hq, S] fp32)."""
+    -> (out [Hq, S, D] in q's dtype, lse [Hq, S] fp32).
+
+    Rows are in domain-major order (row r = position ``domain_positions(chunks,
+    strategy)[r]``; the global order for "vanilla"); ``inverse_perm`` maps back."""
     torch = _torch()
     hq, s, d = q.shape
     hkv = k.shape[0]
-    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale)
+    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale, strategy)
     need = lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 0)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
@@ -440,12 +498,13 @@ def ring_attention_replay(q, k, v, chunks, causal=True, scale=None, out=None, ls
 
 
 def ring_attention_replay_paged(q, pool, block_table, chunks, causal=True, scale=None, out=None,
-                                lse_out=None, workspace=None, stream=None):
-    """As :func:`ring_attention_replay`, K/V gathered per ring step from a paged pool."""
+                                lse_out=None, workspace=None, stream=None, strategy="vanilla"):
+    """As :func:`ring_attention_replay`, K/V gathered per ring step from a paged pool
+    (the pool holds the sequence in the same domain-major order)."""
     torch = _torch()
     hq, s, d = q.shape
     hkv = pool.shape[3]
-    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale)
+    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale, strategy)
     need = lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 1)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
@@ -508,6 +567,31 @@ def vanilla_assignment(chunks) -> list[int]:
     for d, c in enumerate(chunks):
         out.extend([d] * c)
     return out
+
+
+def _strategy_call(fn, ctype, chunks, strategy):
+    n = len(chunks)
+    arr = (ctypes.c_int64 * n)(*chunks)
+    out = (ctype * max(sum(chunks), 1))()
+    _check(getattr(lib(), fn)(strategy_code(strategy), n, arr, out))
+    return list(out[:sum(chunks)])
+
+
+def build_assignment(chunks, strategy="vanilla") -> list[int]:
+    """Domain owning each global position (build_assignment, strategy.rs:53-110)."""
+    return _strategy_call("hcp_ring_build_assignment", ctypes.c_int32, chunks, strategy)
+
+
+def domain_positions(chunks, strategy="vanilla") -> list[int]:
+    """Every domain's ascending positions, concatenated in domain order
+    (build_domain_positions, strategy.rs:114-121)."""
+    return _strategy_call("hcp_ring_domain_positions", ctypes.c_int64, chunks, strategy)
+
+
+def inverse_perm(chunks, strategy="vanilla") -> list[int]:
+    """Row of each global position in the domain-major concatenation
+    (build_inverse_perm, strategy.rs:129-143)."""
+    return _strategy_call("hcp_ring_inverse_perm", ctypes.c_int64, chunks, strategy)
 
 
 def ring_sources(target: int, num_domains: int) -> list[int]:

@@ -23,7 +23,10 @@
 //   * K/V tiles of 64 keys are double-buffered in LDS; global loads of tile t+1 are in
 //     flight while tile t is computed.  One barrier per tile.
 //   * Causal: tiles wholly in a wave's future are skipped, tiles wholly visible are
-//     unmasked, only tiles straddling the diagonal (or the kv tail) are masked.
+//     unmasked, only tiles straddling the diagonal (or the kv tail) are masked.  The
+//     visible keys of a row are a prefix of the chunk: j <= q_off + i - k_off for
+//     contiguous positions, j < q_lim[i] for explicit positions (Striped / ZigZag,
+//     ring.rs:1024-1046, with non-decreasing key positions; see positions.hip).
 //
 // General path (fp32, or any head_dim <= 256): one thread per (query row, head), K/V
 // tiles staged in LDS as fp32.  Used for the fp32 CPU-smoke config.
@@ -49,6 +52,7 @@ struct BlockArgs {
   int64_t fin_hs, fin_ss;
   float* fin_lse;
   int64_t fin_lse_hs;
+  const int32_t* q_lim;    // positions mode when non-null (causal): row i sees keys [0, q_lim[i])
 };
 
 namespace {
@@ -137,6 +141,51 @@ __device__ __forceinline__ float max_xor32(float x) {
 __device__ __forceinline__ float sum_xor32(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Causal visibility of a workgroup of the matrix-core kernels: key j of the chunk is
+// visible to a query row iff j <= that row's limit.  n_kv = keys visible to some row of
+// the workgroup; lane = this lane's row limit; wave_first / wave_last = the smallest /
+// largest limit over the wave's rows inside the chunk.  Contiguous positions give
+// limit = q_off + row - k_off (monotone in the row); explicit positions give
+// limit = q_lim[row] - 1, reduced over the wave and, through `red` (one barrier that
+// every thread of the workgroup reaches), over the workgroup.
+struct RowLimits {
+  int n_kv;
+  int64_t lane, wave_first, wave_last;
+};
+__device__ __forceinline__ RowLimits row_limits(const BlockArgs& a, int q_end, int wq0, int my_q, int wave,
+                                                int lane, int* red) {
+  RowLimits r;
+  r.n_kv = a.lk;
+  if (a.q_lim == nullptr) {
+    r.lane = a.q_off + my_q - a.k_off;
+    r.wave_first = a.q_off + wq0 - a.k_off;
+    r.wave_last = a.q_off + min(wq0 + 31, a.lq - 1) - a.k_off;
+    if (a.causal) {
+      const int64_t lim = a.q_off + q_end - a.k_off;  // keys j < lim are visible to the last row
+      r.n_kv = static_cast<int>(lim <= 0 ? 0 : (lim < a.lk ? lim : a.lk));
+    }
+    return r;
+  }
+  const bool valid = my_q < a.lq;
+  const int mine = valid ? min(max(a.q_lim[my_q], 0), a.lk) : 0;
+  int lo = valid ? mine : a.lk, hi = mine;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    lo = min(lo, __shfl_xor(lo, off));
+    hi = max(hi, __shfl_xor(hi, off));
+  }
+  if (lane == 0) red[wave] = hi;
+  __syncthreads();
+  int wg = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) wg = max(wg, red[w]);
+  r.lane = mine - 1;
+  r.wave_first = lo - 1;
+  r.wave_last = hi - 1;
+  if (a.causal) r.n_kv = wg;
+  return r;
 }
 
 // Stores 4 consecutive fp32 values as `dtype` at element offset `off` of `base`.
@@ -246,11 +295,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
   const int q_end = min(a.lq, tq0 + TQ);
 
   // Keys visible to some row of this workgroup.
-  int n_kv = a.lk;
-  if (a.causal) {
-    const int64_t lim = a.q_off + q_end - a.k_off;  // keys j < lim are visible to the last row
-    n_kv = static_cast<int>(lim <= 0 ? 0 : (lim < a.lk ? lim : a.lk));
-  }
+  __shared__ int lim_red[kWaves];
+  const RowLimits rl = row_limits(a, q_end, wq0, my_q, wave, lane, lim_red);
+  const int n_kv = rl.n_kv;
   const int n_tiles = (n_kv + kBK - 1) / kBK;
 
   // Q^T fragments (B operand): Q[my_q][lhalf*8 + 16*s .. +8]; rows past lq read zeros.
@@ -344,9 +391,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
   const int krow0 = kperm(lcol);  // permuted K row fed by this lane (within a 32-block)
   const float c = a.scale_log2;
   // Causal limit of this lane relative to key 0 of the chunk: key j visible iff j <= qlim.
-  const int64_t qlim64 = a.q_off + my_q - a.k_off;
-  const int64_t wave_lim_first = a.q_off + wq0 - a.k_off;                  // first row of the wave
-  const int64_t wave_lim_last = a.q_off + min(wq0 + 31, a.lq - 1) - a.k_off;  // last row
+  const int64_t qlim64 = rl.lane;
+  const int64_t wave_lim_first = rl.wave_first;
+  const int64_t wave_lim_last = rl.wave_last;
 
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
@@ -536,11 +583,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
   const int my_q = wq0 + lcol;
   const int q_end = min(a.lq, tq0 + TQ);
 
-  int n_kv = a.lk;
-  if (a.causal) {
-    const int64_t lim = a.q_off + q_end - a.k_off;
-    n_kv = static_cast<int>(lim <= 0 ? 0 : (lim < a.lk ? lim : a.lk));
-  }
+  __shared__ int lim_red[kWaves];
+  const RowLimits rl = row_limits(a, q_end, wq0, my_q, wave, lane, lim_red);
+  const int n_kv = rl.n_kv;
   const int n_tiles = (n_kv + kBK - 1) / kBK;
 
   // ---- DMA set-up: wave w fills rows 8w .. 8w+7 of every K and V tile ----
@@ -604,9 +649,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
   float l_run = 0.f;
 
   const float c = a.scale_log2;
-  const int64_t qlim64 = a.q_off + my_q - a.k_off;
-  const int64_t wave_lim_first = a.q_off + wq0 - a.k_off;
-  const int64_t wave_lim_last = a.q_off + min(wq0 + 31, a.lq - 1) - a.k_off;
+  const int64_t qlim64 = rl.lane;
+  const int64_t wave_lim_first = rl.wave_first;
+  const int64_t wave_lim_last = rl.wave_last;
 
   __builtin_amdgcn_s_waitcnt(0);  // Q fragments and tiles 0, 1 resident
   __syncthreads();
@@ -744,6 +789,7 @@ struct GenArgs {
   int64_t fin_hs, fin_ss;
   float* fin_lse;
   int64_t fin_lse_hs;
+  const int32_t* q_lim;
 };
 
 constexpr int kGenRows = 64;
@@ -764,12 +810,22 @@ __global__ __launch_bounds__(kGenRows) void general_block_kernel(GenArgs a) {
     acc[i] = 0.f;
   }
   float m = -INFINITY, l = 0.f;
-  const int64_t qpos = a.q_off + row;
+  // Causal: this row sees keys [0, row_lim) of the chunk (a prefix, see row_limits).
+  int64_t row_lim = a.lk;
   int n_kv = a.lk;
   if (a.causal) {
-    const int last = min(a.lq, static_cast<int>(blockIdx.x + 1) * kGenRows) - 1;
-    const int64_t lim = a.q_off + last + 1 - a.k_off;
-    n_kv = static_cast<int>(lim <= 0 ? 0 : (lim < a.lk ? lim : a.lk));
+    if (a.q_lim != nullptr) {
+      row_lim = live ? min(max(a.q_lim[row], 0), a.lk) : 0;
+      int hi = static_cast<int>(row_lim);  // one wave per workgroup
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off));
+      n_kv = hi;
+    } else {
+      row_lim = a.q_off + row + 1 - a.k_off;
+      const int last = min(a.lq, static_cast<int>(blockIdx.x + 1) * kGenRows) - 1;
+      const int64_t lim = a.q_off + last + 1 - a.k_off;
+      n_kv = static_cast<int>(lim <= 0 ? 0 : (lim < a.lk ? lim : a.lk));
+    }
   }
   for (int kv0 = 0; kv0 < n_kv; kv0 += kGenBK) {
     __syncthreads();
@@ -783,8 +839,7 @@ __global__ __launch_bounds__(kGenRows) void general_block_kernel(GenArgs a) {
     if (!live) continue;
     const int nk = min(kGenBK, n_kv - kv0);
     for (int r = 0; r < nk; ++r) {
-      const int64_t kpos = a.k_off + kv0 + r;
-      if (a.causal && kpos > qpos) continue;
+      if (kv0 + r >= row_lim) continue;
       float s = 0.f;
       for (int i = 0; i < DMAX; ++i)
         if (i < d) s += qv[i] * ks[r][i];
@@ -854,6 +909,7 @@ static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   a.scale_log2 = L.scale * kLog2e;
   a.fin_out = L.fin_out; a.fin_dtype = L.fin_dtype; a.fin_hs = L.fin_hs; a.fin_ss = L.fin_ss;
   a.fin_lse = L.fin_lse; a.fin_lse_hs = L.fin_lse_hs;
+  a.q_lim = L.causal ? L.q_lim : nullptr;
   int g = 1;
   for (int cand : {8, 4, 2}) {
     if (a.rep % cand == 0) { g = cand; break; }
@@ -892,6 +948,7 @@ static void launch_general(const BlockLaunch& L, hipStream_t stream) {
   a.scale = L.scale;
   a.fin_out = L.fin_out; a.fin_dtype = L.fin_dtype; a.fin_hs = L.fin_hs; a.fin_ss = L.fin_ss;
   a.fin_lse = L.fin_lse; a.fin_lse_hs = L.fin_lse_hs;
+  a.q_lim = L.causal ? L.q_lim : nullptr;
   const dim3 grid(static_cast<unsigned>(ceil_div(L.lq, kGenRows)), static_cast<unsigned>(L.hq));
   if (L.d <= 64) general_block_kernel<DT, 64><<<grid, kGenRows, 0, stream>>>(a);
   else if (L.d <= 128) general_block_kernel<DT, 128><<<grid, kGenRows, 0, stream>>>(a);

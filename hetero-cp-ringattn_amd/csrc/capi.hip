@@ -119,10 +119,31 @@ BlockLaunch make_launch(const hcp_ring_block_desc* d, hcp_ring_view q, hcp_ring_
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+StrategySpec make_spec(int32_t strategy, int32_t n, const int64_t* chunks, bool allow_empty) {
+  require(strategy == kStrategyVanilla || strategy == kStrategyStriped || strategy == kStrategyZigZag,
+          "strategy must be 0 (vanilla), 1 (striped) or 2 (zigzag)");
+  require(n >= 1 && n <= kMaxDomains, "num_domains must be in [1, 64]");
+  require(chunks != nullptr, "null chunk_lens");
+  StrategySpec sp{};
+  sp.strategy = strategy;
+  sp.n = n;
+  int64_t total = 0;
+  for (int d = 0; d < n; ++d) {
+    require(chunks[d] >= (allow_empty ? 0 : 1), allow_empty ? "chunk lengths must be >= 0" : "every chunk length must be >= 1");
+    sp.chunks[d] = chunks[d];
+    total += chunks[d];
+    require(total <= INT32_MAX, "total sequence length must fit in int32");
+  }
+  return sp;
+}
+
 // ---- ring replay planning ----
 struct ReplayPlan {
   int n;
-  std::vector<int64_t> len, off;
+  StrategySpec spec;
+  bool positioned = false;                // causal with explicit positions (Striped / ZigZag)
+  size_t pos_off = 0, lim_off = 0;        // workspace: positions int64 [S], key limits int32 [N, S]
+  std::vector<int64_t> len, off, first, last;
   std::vector<std::vector<int>> sources;  // per target, in ring order, non-empty only
   std::vector<size_t> state_off;          // byte offset of each target's running fp32 (o, lse)
   size_t partial_bytes = 0;
@@ -178,6 +199,7 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
   require(d != nullptr, "null descriptor");
   require(d->num_domains >= 1 && d->num_domains <= 64, "num_domains must be in [1, 64]");
   require(d->chunk_lens != nullptr, "null chunk_lens");
+  const StrategySpec spec = make_spec(d->strategy, d->num_domains, d->chunk_lens, false);
   require(d->num_q_heads > 0 && d->num_kv_heads > 0 && d->num_q_heads % d->num_kv_heads == 0,
           "bad head counts");
   require(d->head_dim > 0 && d->head_dim <= 256, "head_dim must be in [1, 256]");
@@ -186,17 +208,21 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
   const int es = elem_size(d->dtype);
   ReplayPlan p;
   p.n = d->num_domains;
+  p.spec = spec;
+  p.positioned = d->causal && d->strategy != kStrategyVanilla;
   int64_t acc = 0;
   int64_t max_len = 0;
   for (int i = 0; i < p.n; ++i) {
     const int64_t l = d->chunk_lens[i];
-    require(l >= 1, "every chunk length must be >= 1");
     p.len.push_back(l);
     p.off.push_back(acc);
+    // Domain-major storage: rows [off, off + len) hold domain i's tokens in ascending
+    // position order, first and last of which bound its positions.
+    p.first.push_back(strategy_position(spec, i, 0));
+    p.last.push_back(strategy_position(spec, i, l - 1));
     acc += l;
     max_len = std::max(max_len, l);
   }
-  require(acc <= INT32_MAX, "total sequence length must fit in int32");
   p.seq = acc;
   p.sources.resize(p.n);
   p.state_off.resize(p.n);
@@ -205,7 +231,7 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
     for (int s = 0; s < p.n; ++s) {
       const int src = ((t - s) % p.n + p.n) % p.n;
       // A source wholly in the target's future contributes nothing (ring.rs:222-228).
-      if (d->causal && p.off[src] > p.off[t] + p.len[t] - 1) continue;
+      if (d->causal && p.first[src] > p.last[t]) continue;
       p.sources[t].push_back(src);
     }
     // A target with one source writes its output rows directly and needs no state.
@@ -216,6 +242,12 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
     }
   }
   p.partial_bytes = cur;
+  if (p.positioned) {
+    p.pos_off = cur;
+    cur += align256(static_cast<size_t>(p.seq) * sizeof(int64_t));
+    p.lim_off = cur;
+    cur += align256(static_cast<size_t>(p.n) * p.seq * sizeof(int32_t));
+  }
   p.staging_off = cur;
   if (paged) {
     p.staging_bytes_per_domain =
@@ -250,6 +282,28 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
   } else {
     check_view(k, "k", p.seq);
     check_view(v, "v", p.seq);
+  }
+  // Explicit positions: generate every domain's positions in HBM, then the key limits
+  // of every (target row, source) pair, once per replay.
+  int32_t* lims = nullptr;
+  if (p.positioned) {
+    int64_t* pos = reinterpret_cast<int64_t*>(base + p.pos_off);
+    lims = reinterpret_cast<int32_t*>(base + p.lim_off);
+    launch_domain_positions(p.spec, p.seq, pos, stream);
+    KeyLimitArgs la{};
+    la.q_pos = pos;
+    la.n_q = p.seq;
+    la.k_pos = pos;
+    int64_t max_len = 0;
+    for (int i = 0; i < p.n; ++i) {
+      la.k_off[i] = p.off[i];
+      la.k_len[i] = p.len[i];
+      max_len = std::max(max_len, p.len[i]);
+    }
+    la.lim = lims;
+    la.lim_stride = p.seq;
+    la.err = device_error_flags();
+    launch_key_limits(la, p.n, max_len, stream);
   }
   // Ring step s: domain t consumes source (t - s) mod N (local first, then the
   // predecessor chain, as the mock ring delivers it: mock.rs:143-149).
@@ -311,6 +365,7 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
       float* po = reinterpret_cast<float*>(state);
       float* pl = reinterpret_cast<float*>(state + align256(rows * d->head_dim * sizeof(float)));
       BlockLaunch L = make_launch(&bd, qv, kv_k, kv_v, po, pl);
+      if (lims != nullptr) L.q_lim = lims + static_cast<int64_t>(src) * p.seq + p.off[t];
       if (idx + 1 == static_cast<int>(p.sources[t].size())) {
         L.fin_out = static_cast<char*>(out.data) + p.off[t] * out.seq_stride * es;
         L.fin_dtype = d->dtype;
@@ -370,6 +425,75 @@ int hcp_ring_block_partial(const hcp_ring_block_desc* desc, hcp_ring_view q, hcp
     check_view(v, "v", desc->kv_len);
     if (desc->q_len > 0) require(o != nullptr && lse != nullptr, "null o or lse");
     launch_block_partial(make_launch(desc, q, k, v, o, lse), as_stream(stream));
+  });
+}
+
+size_t hcp_ring_block_partial_positioned_workspace_size(const hcp_ring_block_desc* desc) {
+  if (desc == nullptr || desc->q_len < 0) return 0;
+  return align256(static_cast<size_t>(desc->q_len) * sizeof(int32_t));
+}
+
+int hcp_ring_block_partial_positioned(const hcp_ring_block_desc* desc, hcp_ring_view q, const int64_t* q_positions,
+                                      hcp_ring_view k, hcp_ring_view v, const int64_t* kv_positions, float* o,
+                                      float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded(__func__, [&] {
+    check_block_desc(desc);
+    check_view(q, "q", desc->q_len);
+    check_view(k, "k", desc->kv_len);
+    check_view(v, "v", desc->kv_len);
+    if (desc->q_len == 0) return;
+    require(o != nullptr && lse != nullptr, "null o or lse");
+    BlockLaunch L = make_launch(desc, q, k, v, o, lse);
+    if (desc->causal) {
+      const size_t need = hcp_ring_block_partial_positioned_workspace_size(desc);
+      require(q_positions != nullptr, "null q_positions");
+      require(kv_positions != nullptr || desc->kv_len == 0, "null kv_positions");
+      require(workspace != nullptr && workspace_bytes >= need,
+              "workspace too small: need " + std::to_string(need) + " bytes");
+      KeyLimitArgs la{};
+      la.q_pos = q_positions;
+      la.n_q = desc->q_len;
+      la.k_pos = kv_positions;
+      la.k_off[0] = 0;
+      la.k_len[0] = desc->kv_len;
+      la.lim = static_cast<int32_t*>(workspace);
+      la.lim_stride = 0;
+      la.err = device_error_flags();
+      launch_key_limits(la, 1, desc->kv_len, as_stream(stream));
+      L.q_lim = la.lim;
+    }
+    launch_block_partial(L, as_stream(stream));
+  });
+}
+
+int hcp_ring_build_assignment(int32_t strategy, int32_t num_domains, const int64_t* chunk_lens,
+                              int32_t* assignment) {
+  return guarded(__func__, [&] {
+    const StrategySpec sp = make_spec(strategy, num_domains, chunk_lens, true);
+    require(assignment != nullptr, "null assignment");
+    for (int d = 0; d < sp.n; ++d)
+      for (int64_t i = 0; i < sp.chunks[d]; ++i) assignment[strategy_position(sp, d, i)] = d;
+  });
+}
+
+int hcp_ring_domain_positions(int32_t strategy, int32_t num_domains, const int64_t* chunk_lens,
+                              int64_t* positions) {
+  return guarded(__func__, [&] {
+    const StrategySpec sp = make_spec(strategy, num_domains, chunk_lens, true);
+    require(positions != nullptr, "null positions");
+    int64_t r = 0;
+    for (int d = 0; d < sp.n; ++d)
+      for (int64_t i = 0; i < sp.chunks[d]; ++i) positions[r++] = strategy_position(sp, d, i);
+  });
+}
+
+int hcp_ring_inverse_perm(int32_t strategy, int32_t num_domains, const int64_t* chunk_lens, int64_t* inverse) {
+  return guarded(__func__, [&] {
+    const StrategySpec sp = make_spec(strategy, num_domains, chunk_lens, true);
+    require(inverse != nullptr, "null inverse");
+    int64_t r = 0;
+    for (int d = 0; d < sp.n; ++d)
+      for (int64_t i = 0; i < sp.chunks[d]; ++i) inverse[strategy_position(sp, d, i)] = r++;
   });
 }
 

@@ -38,7 +38,8 @@ inline void require(bool ok, const std::string& msg) {
   if (!ok) throw Error(-6, msg);
 }
 
-// Sticky device-side error flags (bit 0: paged block id out of range).
+// Sticky device-side error flags (bit 0: paged block id out of range; bit 1: key
+// positions not non-decreasing).
 // Defined in capi.hip; kernels set bits with atomicOr through this pointer
 // argument resolved once per device by the host (hipGetSymbolAddress).
 int* device_error_flags();

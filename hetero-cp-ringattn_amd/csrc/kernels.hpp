@@ -26,6 +26,9 @@ struct BlockLaunch {
   int64_t fin_hs = 0, fin_ss = 0;
   float* fin_lse = nullptr;
   int64_t fin_lse_hs = 0;
+  // Positions mode (causal only, q_lim != nullptr): row i of the query chunk sees keys
+  // [0, q_lim[i]) of the KV chunk instead of those with k_off + j <= q_off + i.
+  const int32_t* q_lim = nullptr;
 };
 
 bool block_uses_mfma(int dtype, int d);
@@ -59,6 +62,33 @@ void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const voi
                          const int32_t* tables, int64_t table_stride, int64_t table_len,
                          const int32_t* seq_lens, int64_t t0, int64_t t1, float scale, float* o,
                          float* lse, void* ws, size_t ws_bytes, int* err, hipStream_t stream);
+
+// Scheduling strategies (strategy.rs:14-24) and their closed-form positions; see
+// positions.hip.
+constexpr int kMaxDomains = 64;
+enum Strategy : int32_t { kStrategyVanilla = 0, kStrategyStriped = 1, kStrategyZigZag = 2 };
+struct StrategySpec {
+  int32_t strategy;
+  int32_t n;
+  int64_t chunks[kMaxDomains];
+};
+// Global position of the i-th token (local storage order) of domain d.
+__host__ __device__ int64_t strategy_position(const StrategySpec& s, int d, int64_t i);
+void launch_domain_positions(const StrategySpec& s, int64_t seq, int64_t* out, hipStream_t stream);
+
+// lim[src * lim_stride + r] = #{j < k_len[src] : k_pos[k_off[src] + j] <= q_pos[r]} for
+// r < n_q; sets error bit 1 when a key list is not non-decreasing.
+struct KeyLimitArgs {
+  const int64_t* q_pos;
+  int64_t n_q;
+  const int64_t* k_pos;
+  int64_t k_off[kMaxDomains];
+  int64_t k_len[kMaxDomains];
+  int32_t* lim;
+  int64_t lim_stride;
+  int* err;
+};
+void launch_key_limits(const KeyLimitArgs& a, int n_src, int64_t max_k_len, hipStream_t stream);
 
 void launch_synth_normals(uint64_t seed, int64_t offset, int64_t count, int dtype, void* out,
                           hipStream_t stream);

@@ -82,7 +82,8 @@ int hcp_ring_device_count(int* count);
 
 /*
  * Reads and clears the sticky device-side error flags of the current device
- * (bit 0: a paged block id outside [0, num_blocks) was met and that row skipped).
+ * (bit 0: a paged block id outside [0, num_blocks) was met and that row skipped;
+ * bit 1: a list of key positions given to the positions mode was not non-decreasing).
  * Synchronises `stream`.
  */
 int hcp_ring_fetch_device_errors(void* stream, int* flags);
@@ -123,6 +124,52 @@ typedef struct hcp_ring_block_desc {
 
 int hcp_ring_block_partial(const hcp_ring_block_desc* desc, hcp_ring_view q, hcp_ring_view k,
                            hcp_ring_view v, float* o, float* lse, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * (1b) Block partial with explicit positions (Striped / ZigZag and any other
+ * non-contiguous split): positioned_local_compact_partial /
+ * positioned_merge_compact_partial with position tensors (ring.rs:538-603; the
+ * KvBlock position_ids of block.rs:32-34, used by ring.rs:1024-1046).
+ *
+ * As (1), with desc->q_offset / kv_offset ignored: query i has global position
+ * q_positions[i], key j has kv_positions[j] (DEVICE int64 arrays, the reference's
+ * Int64 position tensors), and with causal=1 a key is visible iff
+ * kv_positions[j] <= q_positions[i].  kv_positions must be non-decreasing (as every
+ * strategy's local order is, strategy.rs:114-121, and any slice of it); otherwise
+ * device error bit 1 is set.  q_positions may be in any order.  The workspace
+ * (hcp_ring_block_partial_positioned_workspace_size bytes) holds one int32 per query
+ * row.  With causal=0 positions are not read.
+ * ------------------------------------------------------------------------------- */
+size_t hcp_ring_block_partial_positioned_workspace_size(const hcp_ring_block_desc* desc);
+
+int hcp_ring_block_partial_positioned(const hcp_ring_block_desc* desc, hcp_ring_view q,
+                                      const int64_t* q_positions, hcp_ring_view k, hcp_ring_view v,
+                                      const int64_t* kv_positions, float* o, float* lse,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * (1c) Scheduling strategies (RingSchedulingStrategy, strategy.rs:14-24) -- host only.
+ *
+ * hcp_ring_build_assignment: assignment[p] = domain owning global position p
+ *     (build_assignment, strategy.rs:53-110); chunk_lens[d] >= 0 positions each.
+ * hcp_ring_domain_positions: every domain's positions in ascending (local storage)
+ *     order, concatenated in domain order (build_domain_positions, :114-121).
+ * hcp_ring_inverse_perm: inverse[p] = row of position p in that concatenation
+ *     (build_inverse_perm, :129-143).
+ * Output arrays are HOST arrays of sum(chunk_lens) elements.  No GPU is used.
+ * ------------------------------------------------------------------------------- */
+enum {
+  HCP_STRATEGY_VANILLA = 0,
+  HCP_STRATEGY_STRIPED = 1,
+  HCP_STRATEGY_ZIGZAG = 2
+};
+
+int hcp_ring_build_assignment(int32_t strategy, int32_t num_domains, const int64_t* chunk_lens,
+                              int32_t* assignment);
+int hcp_ring_domain_positions(int32_t strategy, int32_t num_domains, const int64_t* chunk_lens,
+                              int64_t* positions);
+int hcp_ring_inverse_perm(int32_t strategy, int32_t num_domains, const int64_t* chunk_lens,
+                          int64_t* inverse);
 
 /* ---------------------------------------------------------------------------------
  * (2) LSE merge of ring-step partials.
@@ -268,18 +315,25 @@ int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_po
 /* ---------------------------------------------------------------------------------
  * (5) Single-GPU ring replay of a whole prefill (the ring_attention driver).
  *
- * Replays ring_attention (ring.rs:861-1398) for every domain of a contiguous uneven
- * split: domain d owns global positions [off_d, off_d + chunk_lens[d]) (vanilla
- * assignment, rust/src/model/attention/strategy.rs:53-63), visits sources
+ * Replays ring_attention (ring.rs:861-1398) for every domain of an uneven split.
+ * desc->strategy picks the assignment (strategy.rs:53-110, see (1c)): with
+ * HCP_STRATEGY_VANILLA domain d owns global positions [off_d, off_d + chunk_lens[d]);
+ * with STRIPED or ZIGZAG it owns the positions hcp_ring_domain_positions lists, and
+ * the causal masks follow them (the position_ids path of ring.rs:1024-1046, as in
+ * the reference's run_uneven_ring_attention, ring.rs:3226-3360).  Domain d visits sources
  * (d - s) mod N for s = 0..N-1 (local first, then the predecessor chain), skips
  * sources entirely in its future (ring.rs:222-228), and folds each source into the
  * domain's running fp32 (o, lse) state as it arrives with (1) in accumulate mode (the
  * positioned_merge_compact_partial re-entry, ring.rs:574-603); the last source of a
  * domain writes the normalised rows straight into out.  q/k/v/out cover the whole
- * sequence (global token index = view token index).  out receives the merged
+ * sequence in domain-major order: rows [off_d, off_d + chunk_lens[d]) hold domain d's
+ * tokens in its local order (for VANILLA this is the global order; otherwise row r
+ * holds position hcp_ring_domain_positions[r], and hcp_ring_inverse_perm maps the
+ * output back to global order).  out receives the merged
  * attention (dtype = desc->dtype), lse_out (may be NULL) the merged LSE [Hq, S] fp32.
  * Workspace: hcp_ring_replay_workspace_size bytes (one fp32 state per domain with
- * more than one source, plus the paged staging area).
+ * more than one source, the positions and per-row key limits of a causal STRIPED /
+ * ZIGZAG replay, plus the paged staging area).
  *
  * With a paged pool (hcp_ring_prefill_replay_paged), K/V are not given as views: each
  * source domain's chunk is first gathered with (3) from the pool through block_table
@@ -294,6 +348,7 @@ typedef struct hcp_ring_replay_desc {
   int32_t causal;
   const int64_t* chunk_lens; /* HOST array of num_domains lengths (each >= 1) */
   float scale;
+  int32_t strategy;          /* HCP_STRATEGY_* (0 = vanilla) */
 } hcp_ring_replay_desc;
 
 size_t hcp_ring_replay_workspace_size(const hcp_ring_replay_desc* desc, int32_t paged);

@@ -20,6 +20,8 @@ this module replays the same ATen op sequence through PyTorch's CPU backend:
                                       3230-3364): every domain driven in one process,
                                       peers delivered by a mock transport
                                       (rust/src/model/transport/mock.rs:99-159).
+* :func:`ring_attention_replay_strategy`  run_uneven_ring_attention (ring.rs:3226-3364)
+                                      with Striped / ZigZag positions.
 
 Tensor layout follows the reference: ``[batch, heads, seq, head_dim]``; positions are
 int64 CPU tensors.  The running state (rm, rs, obh) is kept in the query dtype, as the
@@ -188,6 +190,7 @@ class KvMicroBlock:
     v: torch.Tensor
     micro_block_idx: int
     total_micro_blocks: int
+    position_ids: torch.Tensor | None = None  # block.rs:32-34 (Striped / ZigZag)
 
 
 @dataclass
@@ -199,7 +202,7 @@ class RingStats:
 
 def ring_attention(scale, q, k, v, query_positions, global_seq_start: int, num_domains: int,
                    peer_rounds, apply_causal: bool = True, return_lse: bool = False,
-                   stats: RingStats | None = None):
+                   stats: RingStats | None = None, local_kv_positions=None):
     """Per-domain driver (ring.rs:861-1398) with an in-memory transport.
 
     ``q`` [1,H,S_d,D], ``k``/``v`` [1,H,S_d,D] (post-expand, ring.rs:1962-1984),
@@ -208,7 +211,10 @@ def ring_attention(scale, q, k, v, query_positions, global_seq_start: int, num_d
     Phase 1 folds local KV tiles of ``kv_chunk`` per q-chunk state (:1208-1229); Phase 2
     folds every received micro block into every q-chunk state, in arrival order
     (:1239-1311).  Returns ``cat(obh)`` along seq (:1397); with ``return_lse`` also
-    ``rm + log(rs)`` in fp32 (the reference driver itself returns no LSE).
+    ``rm + log(rs)`` in fp32 (the reference driver itself returns no LSE).  Key
+    positions: ``local_kv_positions`` narrowed per tile, else contiguous from
+    ``global_seq_start`` (build_k_pos, :1024-1034); a peer block's ``position_ids``,
+    else its [start, end) range (peer_k_pos, :1037-1046).
     """
     seq_len = q.shape[2]
     local_kv_len = k.shape[2]
@@ -236,11 +242,17 @@ def ring_attention(scale, q, k, v, query_positions, global_seq_start: int, num_d
     for st in states:  # Phase 1
         for ks in range(0, local_kv_len, kv_chunk):
             ke = min(ks + kv_chunk, local_kv_len)
-            kp = torch.arange(global_seq_start + ks, global_seq_start + ke, dtype=torch.int64)
+            if local_kv_positions is not None:
+                kp = local_kv_positions[ks:ke]
+            else:
+                kp = torch.arange(global_seq_start + ks, global_seq_start + ke, dtype=torch.int64)
             fold(st, k[:, :, ks:ke], v[:, :, ks:ke], kp, ("local", global_seq_start + ks))
     for r, blocks in enumerate(peer_rounds):  # Phase 2
         for blk in blocks:
-            kp = torch.arange(blk.global_seq_start, blk.global_seq_end, dtype=torch.int64)
+            if blk.position_ids is not None:
+                kp = blk.position_ids
+            else:
+                kp = torch.arange(blk.global_seq_start, blk.global_seq_end, dtype=torch.int64)
             for st in states:
                 fold(st, blk.k, blk.v, kp, ("peer", r, blk.global_seq_start))
     out = torch.cat([st[4] for st in states], dim=2)
@@ -250,8 +262,10 @@ def ring_attention(scale, q, k, v, query_positions, global_seq_start: int, num_d
     return out, lse
 
 
-def local_micro_blocks(k, v, global_seq_start: int, num_domains: int, micro_override: int = 0):
-    """Split a domain's (expanded) K/V into its sent micro blocks (ring.rs:980-1020)."""
+def local_micro_blocks(k, v, global_seq_start: int, num_domains: int, micro_override: int = 0,
+                       positions=None):
+    """Split a domain's (expanded) K/V into its sent micro blocks (ring.rs:980-1020);
+    each block carries the matching slice of ``positions`` when given."""
     seq_len = k.shape[2]
     _, _, micro = chunk_sizes(seq_len, num_domains, micro_override)
     n = -(-seq_len // micro)
@@ -259,8 +273,46 @@ def local_micro_blocks(k, v, global_seq_start: int, num_domains: int, micro_over
     for i in range(n):
         s, e = i * micro, min((i + 1) * micro, seq_len)
         out.append(KvMicroBlock(global_seq_start + s, global_seq_start + e, k[:, :, s:e],
-                                v[:, :, s:e], i, n))
+                                v[:, :, s:e], i, n, None if positions is None else positions[s:e]))
     return out
+
+
+def ring_attention_replay_strategy(scale, q_all, k_all, v_all, chunks, strategy: str,
+                                   causal: bool = True, return_lse: bool = False):
+    """run_uneven_ring_attention (ring.rs:3226-3364) for any strategy: gather every
+    domain's Q/K/V at its positions (build_domain_positions), run each domain's ring with
+    those positions for its queries, local KV and the peer blocks it receives, then put
+    the outputs back in global order with build_inverse_perm.  Inputs and outputs are
+    in global order, ``[1, H, S, D]``."""
+    from oracle import strategy as SP
+    n = len(chunks)
+    seq = q_all.shape[2]
+    if sum(chunks) != seq:
+        raise ValueError(f"chunk sum {sum(chunks)} != seq_len {seq}")
+    assign = SP.build_assignment(list(chunks), strategy)
+    positions = SP.build_domain_positions(assign)
+    inverse = torch.tensor(SP.build_inverse_perm(assign), dtype=torch.int64)
+    num_rep = q_all.shape[1] // k_all.shape[1]
+    kx = repeat_kv_heads(k_all, num_rep)
+    vx = repeat_kv_heads(v_all, num_rep)
+    pos_t = [torch.tensor(p, dtype=torch.int64) for p in positions]
+    sent = [local_micro_blocks(kx.index_select(2, pos_t[d]), vx.index_select(2, pos_t[d]), positions[d][0], n,
+                               positions=pos_t[d]) for d in range(n)]
+    outs, lses = [], []
+    for d in range(n):
+        rounds = [sent[(d - 1 - r) % n] for r in range(n - 1)]
+        res = ring_attention(scale, q_all.index_select(2, pos_t[d]), kx.index_select(2, pos_t[d]),
+                             vx.index_select(2, pos_t[d]), pos_t[d], positions[d][0], n, rounds,
+                             apply_causal=causal, return_lse=return_lse, local_kv_positions=pos_t[d])
+        if return_lse:
+            outs.append(res[0])
+            lses.append(res[1])
+        else:
+            outs.append(res)
+    out = torch.cat(outs, dim=2).index_select(2, inverse)
+    if not return_lse:
+        return out
+    return out, torch.cat(lses, dim=2).index_select(2, inverse)
 
 
 def ring_attention_replay(scale, q_all, k_all, v_all, chunks, causal: bool = True,

@@ -106,6 +106,16 @@ def kats(name):
         "ring_sources": {"source": "rust/src/model/transport/mock.rs:143-149 (round r from (d-1-r) mod N)",
                          "num_domains": 4,
                          "expected": {"0": [0, 3, 2, 1], "1": [1, 0, 3, 2], "2": [2, 1, 0, 3], "3": [3, 2, 1, 0]}},
+        "strategies": [
+            {"source": "rust/src/model/attention/strategy.rs:165-170", "strategy": "striped",
+             "chunks": [3, 1], "assignment": [0, 1, 0, 0]},
+            {"source": "rust/src/model/attention/strategy.rs:172-181", "strategy": "zigzag",
+             "chunks": [3, 1], "assignment": [0, 0, 1, 0], "positions": [[0, 1, 3], [2]]},
+            {"source": "rust/src/model/attention/strategy.rs:183-192", "strategy": "zigzag",
+             "chunks": [4, 4], "assignment": [0, 0, 1, 1, 1, 1, 0, 0], "positions": [[0, 1, 6, 7], [2, 3, 4, 5]]},
+            {"source": "rust/src/model/attention/strategy.rs:194-201", "strategy": "striped",
+             "chunks": [3, 1], "inverse_perm": [0, 3, 1, 2]},
+        ],
     }
     with open(os.path.join(HERE, name), "w") as f:
         json.dump(data, f, indent=1)

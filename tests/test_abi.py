@@ -3,6 +3,8 @@ and validates arguments before touching a device."""
 import ctypes
 import math
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -74,3 +76,28 @@ def test_device_count_without_gpu(hcp):
     c = ctypes.c_int(-1)
     assert hcp.lib().hcp_ring_device_count(ctypes.byref(c)) == -5
     assert c.value == 0
+
+
+@pytest.mark.parametrize("strategy", ["vanilla", "striped", "zigzag"])
+def test_strategy_helpers_match_oracle_procedure(strategy):
+    # The library's closed-form positions (host helpers, no GPU) against the oracle's
+    # step-by-step restatement of strategy.rs:53-143, zero-length chunks included.
+    from oracle import strategy as SP
+    rng = np.random.default_rng(5)
+    cases = [[3, 1], [4, 4], [6, 0, 3], [1], [0, 5], [2, 7, 1, 9]]
+    cases += [list(rng.integers(0, 40, size=rng.integers(2, 9))) for _ in range(30)]
+    for chunks in cases:
+        chunks = [int(c) for c in chunks]
+        if sum(chunks) == 0:
+            continue
+        a = SP.build_assignment(chunks, strategy)
+        assert H.build_assignment(chunks, strategy) == a, chunks
+        assert H.domain_positions(chunks, strategy) == sum(SP.build_domain_positions(a), []), chunks
+        assert H.inverse_perm(chunks, strategy) == SP.build_inverse_perm(a), chunks
+
+
+def test_strategy_helpers_reject_bad_arguments():
+    with pytest.raises(H.HcpRingError):
+        H.build_assignment([3, 1], 7)
+    with pytest.raises(H.HcpRingError):
+        H.build_assignment([3, -1], "striped")

@@ -144,6 +144,25 @@ def test_reference_known_answers():
         assert H.ring_sources(int(tgt), r["num_domains"]) == srcs
 
 
+def test_strategy_known_answers_oracle_and_library():
+    # strategy.rs:157-201 asserted by the reference; the oracle's procedure and the
+    # library's closed forms (host helpers, no GPU) must both reproduce them.
+    from oracle import strategy as SP
+    with open(os.path.join(GOLD, "reference_kats.json")) as f:
+        kat = json.load(f)
+    for case in kat["strategies"]:
+        chunks, strat = case["chunks"], case["strategy"]
+        a = SP.build_assignment(chunks, strat)
+        if "assignment" in case:
+            assert a == case["assignment"] and H.build_assignment(chunks, strat) == case["assignment"]
+        if "positions" in case:
+            assert SP.build_domain_positions(a) == case["positions"]
+            assert H.domain_positions(chunks, strat) == sum(case["positions"], [])
+        if "inverse_perm" in case:
+            assert SP.build_inverse_perm(a) == case["inverse_perm"]
+            assert H.inverse_perm(chunks, strat) == case["inverse_perm"]
+
+
 # ------------------------------------------------------------------------ GPU ----
 def dev(bits, dtype=torch.bfloat16):
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(dtype).cuda()

@@ -401,3 +401,136 @@ def test_decode_ring_rejects_bad_seed_and_owner(gpu):
         H.decode_ring_replay(q, pool, [(tab, None, 4), (tab, None, 4)], 2)
     with pytest.raises(H.HcpRingError):
         H.decode_ring_owner(5, 0)
+
+
+def _strategy_rows(chunks, strategy):
+    from oracle import strategy as SP
+    a = SP.build_assignment(chunks, strategy)
+    pos = SP.build_domain_positions(a)
+    return pos, np.array(SP.build_inverse_perm(a))
+
+
+POSITIONED_CASES = [
+    # name, Lq, Lk, Hq, Hkv, D, dtype, position pattern
+    ("striped_peer_d128", 300, 200, 8, 2, 128, torch.bfloat16, "striped"),
+    ("zigzag_local_d128", 320, 320, 8, 2, 128, torch.bfloat16, "zigzag_local"),
+    ("gaps_unsorted_q_d128", 257, 333, 16, 2, 128, torch.bfloat16, "gaps"),
+    ("striped_d64_f16", 200, 300, 4, 4, 64, torch.float16, "striped_rev"),
+    ("gaps_fp32_general", 150, 190, 4, 2, 64, torch.float32, "gaps"),
+]
+
+
+def _positions(pattern, lq, lk, seed):
+    rng = np.random.default_rng(seed)
+    if pattern == "striped":        # target domain 0, source domain 1 of a striped split
+        pos, _ = _strategy_rows([lq, lk], "striped")
+        return np.array(pos[0]), np.array(pos[1])
+    if pattern == "striped_rev":    # target domain 1, source domain 0
+        pos, _ = _strategy_rows([lk, lq], "striped")
+        return np.array(pos[1]), np.array(pos[0])
+    if pattern == "zigzag_local":   # a zigzag domain against its own keys
+        pos, _ = _strategy_rows([lq, 2 * lq, lq], "zigzag")
+        return np.array(pos[0]), np.array(pos[0])
+    qp = rng.choice(4 * (lq + lk), size=lq, replace=False)          # any order
+    kp = np.sort(rng.choice(4 * (lq + lk), size=lk, replace=False))  # non-decreasing
+    return qp, kp
+
+
+@pytest.mark.parametrize("case", POSITIONED_CASES, ids=[c[0] for c in POSITIONED_CASES])
+def test_block_partial_positioned_matches_closed_form(gpu, case):
+    name, lq, lk, hq, hkv, d, dt, pattern = case
+    qp, kp = _positions(pattern, lq, lk, lq + lk)
+    (q, k, v), (q32, k32, v32) = draw(lq * 3 + lk, [(lq, hq, d), (lk, hkv, d), (lk, hkv, d)], dt)
+    scale = 1 / math.sqrt(d)
+    qpt, kpt = torch.from_numpy(qp.astype(np.int64)).cuda(), torch.from_numpy(kp.astype(np.int64)).cuda()
+    o, lse = H.positioned_local_compact_partial(q.permute(1, 0, 2), qpt, k.permute(1, 0, 2), v.permute(1, 0, 2),
+                                                kpt)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    o, lse = o.cpu().numpy(), lse.cpu().numpy()
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, qp, kp, scale)
+    ref_o, ref_l = ref_o.transpose(1, 0, 2), ref_l.T
+    assert np.array_equal(np.isneginf(lse), np.isneginf(ref_l)), name
+    fin = np.isfinite(ref_l)
+    tol = 1e-4 if dt == torch.float32 else OUT_TOL
+    assert np.abs(o - ref_o).max() <= tol, name
+    assert np.abs(lse[fin] - ref_l[fin]).max() <= (1e-4 if dt == torch.float32 else LSE_TOL), name
+    assert np.all(o[~fin] == 0)
+    # op-for-op restatement with the same position tensors (ring.rs:538-571)
+    to, tl = T.positioned_local_compact_partial(scale, bhsd(q32), torch.from_numpy(qp.astype(np.int64)),
+                                                T.repeat_kv_heads(bhsd(k32), hq // hkv),
+                                                T.repeat_kv_heads(bhsd(v32), hq // hkv),
+                                                torch.from_numpy(kp.astype(np.int64)))
+    assert np.abs(o - to[0].numpy()).max() <= tol, name
+
+
+def test_block_partial_positioned_merge_and_flag(gpu):
+    # positioned_merge_compact_partial with positions (ring.rs:574-603): a striped
+    # target merged with two sources; then a non-monotone key list raises flag bit 1.
+    pos, _ = _strategy_rows([160, 96, 64], "striped")
+    (q, k, v), (q32, k32, v32) = draw(91, [(320, 8, 128), (320, 2, 128), (320, 2, 128)], torch.bfloat16)
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    t = lambda a: torch.tensor(a, dtype=torch.int64, device="cuda")
+    o, l = H.positioned_local_compact_partial(qh[:, :160], t(pos[0]), kh[:, :160], vh[:, :160], t(pos[0]))
+    o, l = H.positioned_merge_compact_partial(qh[:, :160], t(pos[0]), o, l, kh[:, 256:], vh[:, 256:], t(pos[2]))
+    o, l = H.positioned_merge_compact_partial(qh[:, :160], t(pos[0]), o, l, kh[:, 160:256], vh[:, 160:256],
+                                              t(pos[1]))
+    torch.cuda.synchronize()
+    flat = np.array(sum(pos, []))
+    ref_o, ref_l = C.attention_f64(q32[:160], k32, v32, flat[:160], flat, 1 / math.sqrt(128))
+    assert np.abs(o.cpu().numpy() - ref_o.transpose(1, 0, 2)).max() <= OUT_TOL
+    assert np.abs(l.cpu().numpy() - ref_l.T).max() <= LSE_TOL
+    assert H.fetch_device_errors() == 0
+    bad = t(pos[1][::-1].copy())
+    H.positioned_local_compact_partial(qh[:, :160], t(pos[0]), kh[:, 160:256], vh[:, 160:256], bad)
+    assert H.fetch_device_errors() & 2
+
+
+STRATEGY_RING_CASES = [
+    # name, chunks, Hq, Hkv, D, dtype, seed   (ring.rs:3168-3224 is 3:1 fp32)
+    ("fp32_3to1", [768, 256], 4, 4, 64, torch.float32, 60),
+    ("bf16_uneven4", [900, 300, 500, 348], 8, 2, 128, torch.bfloat16, 61),
+    ("f16_d64_three", [400, 250, 150], 4, 2, 64, torch.float16, 62),
+]
+
+
+@pytest.mark.parametrize("strategy", ["striped", "zigzag"])
+@pytest.mark.parametrize("case", STRATEGY_RING_CASES, ids=[c[0] for c in STRATEGY_RING_CASES])
+def test_ring_replay_strategy_matches_full_attention(gpu, case, strategy):
+    name, chunks, hq, hkv, d, dt, seed = case
+    s = sum(chunks)
+    (q, k, v), (q32, k32, v32) = draw(seed, [(s, hq, d), (s, hkv, d), (s, hkv, d)], dt)
+    pos, inv = _strategy_rows(chunks, strategy)
+    rows = torch.tensor(sum(pos, []), device="cuda")
+    # domain-major inputs: row r holds global position rows[r]
+    qd, kd, vd = (x.index_select(0, rows).permute(1, 0, 2) for x in (q, k, v))
+    out, lse = H.ring_attention_replay(qd, kd, vd, chunks, strategy=strategy)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    out = out.float().cpu().numpy()[:, inv]
+    lse = lse.cpu().numpy()[:, inv]
+    p = np.arange(s)
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, p, p, 1 / math.sqrt(d))
+    tol_o = 1e-4 if dt == torch.float32 else OUT_TOL
+    tol_l = 1e-4 if dt == torch.float32 else LSE_TOL
+    assert np.abs(out - ref_o.transpose(1, 0, 2)).max() <= tol_o, (name, strategy)
+    assert np.abs(lse - ref_l.T).max() <= tol_l, (name, strategy)
+    if dt == torch.float32:
+        # the reference's own driver with these positions, on the same fp32 inputs
+        ro = T.ring_attention_replay_strategy(1 / math.sqrt(d), bhsd(q32), bhsd(k32), bhsd(v32), chunks, strategy)
+        assert np.abs(out - ro[0].numpy()).max() <= 1e-4
+
+
+def test_ring_replay_paged_strategy_matches_unpaged(gpu):
+    chunks = [256, 96, 160]
+    s, hq, hkv, d, bs = sum(chunks), 8, 2, 128, 16
+    (q, k, v), _ = draw(79, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
+    nb = s // bs + 5
+    table = torch.from_numpy(I.permuted_block_table(80, nb)[: s // bs]).cuda()
+    pool = torch.zeros(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.paged_kv_scatter(pool, table, 0, 0, s, k.permute(1, 0, 2), v.permute(1, 0, 2))
+    o1, l1 = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
+                                     strategy="zigzag")
+    o2, l2 = H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, chunks, strategy="zigzag")
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)

@@ -321,6 +321,73 @@ def test_planted_mistakes_are_caught(mistake):
     assert err > 1e-2, f"planted {mistake} not detected (err={err})"
 
 
+# ------------------------------------------------------------------ strategies ----
+STRATEGY_CHUNKS = [[3, 1], [4, 4], [5, 3, 2], [7, 1, 4, 2], [1, 9], [2, 2, 2, 2, 3], [6, 0, 3]]
+
+
+@pytest.mark.parametrize("chunks", STRATEGY_CHUNKS)
+@pytest.mark.parametrize("strategy", ["vanilla", "striped", "zigzag"])
+def test_strategy_assignment_invariants(chunks, strategy):
+    # build_assignment's contract (strategy.rs:49-52): domain i owns exactly chunks[i]
+    # positions; the positions partition [0, S); the inverse permutation inverts the
+    # domain-major concatenation.
+    from oracle import strategy as SP
+    a = SP.build_assignment(chunks, strategy)
+    assert len(a) == sum(chunks)
+    assert [a.count(d) for d in range(len(chunks))] == chunks
+    pos = SP.build_domain_positions(a)
+    flat = sum(pos, [])
+    assert sorted(flat) == list(range(sum(chunks)))
+    assert all(p == sorted(p) for p in pos)
+    inv = SP.build_inverse_perm(a)
+    assert [flat[inv[p]] for p in range(len(a))] == list(range(len(a)))
+
+
+def test_zigzag_classic_and_striped_round_robin():
+    # Equal chunks: ZigZag is the classic 2N-segment layout, Striped is p mod N.
+    from oracle import strategy as SP
+    n, c = 4, 6
+    a = SP.build_assignment([c] * n, "zigzag")
+    seg = c // 2
+    assert a == sum([[d] * seg for d in range(n)] + [[d] * seg for d in reversed(range(n))], [])
+    assert SP.build_assignment([c] * n, "striped") == [p % n for p in range(n * c)]
+
+
+@pytest.mark.parametrize("strategy", ["striped", "zigzag"])
+@pytest.mark.parametrize("chunks", [[48, 16], [30, 20, 14]])
+def test_strategy_ring_matches_closed_form(strategy, chunks):
+    # run_uneven_ring_attention (ring.rs:3226-3364) at a small size: every strategy's
+    # ring, put back in global order, is full causal attention.
+    s = sum(chunks)
+    q, k, v = _rand(40, (s, 4, 16)), _rand(41, (s, 2, 16)), _rand(42, (s, 2, 16))
+    pos = np.arange(s)
+    ref_o, ref_l = C.attention_f64(q, k, v, pos, pos, 0.25)
+    f = lambda x: _bhsd(x.astype(np.float32))
+    o, l = T.ring_attention_replay_strategy(0.25, f(q), f(k), f(v), chunks, strategy, return_lse=True)
+    assert np.abs(o[0].permute(1, 0, 2).numpy() - ref_o).max() < 1e-5
+    assert np.abs(l[0].permute(1, 0).numpy() - ref_l).max() < 1e-5
+
+
+def test_strategy_ring_with_contiguous_positions_is_caught():
+    # Planted mistake: feed the striped layout but let every block claim contiguous
+    # positions (drop the position_ids) -- the closed form must reject it.
+    from oracle import strategy as SP
+    chunks = [48, 16]
+    s = sum(chunks)
+    q, k, v = _rand(43, (s, 2, 16)), _rand(44, (s, 2, 16)), _rand(45, (s, 2, 16))
+    pos = np.arange(s)
+    ref_o, _ = C.attention_f64(q, k, v, pos, pos, 0.25)
+    f = lambda x: _bhsd(x.astype(np.float32))
+    a = SP.build_assignment(chunks, "striped")
+    perm = torch.tensor(sum(SP.build_domain_positions(a), []))
+    inv = torch.tensor(SP.build_inverse_perm(a))
+    # the vanilla driver on permuted inputs = contiguous positions on striped data
+    o = T.ring_attention_replay(0.25, f(q).index_select(2, perm), f(k).index_select(2, perm),
+                                f(v).index_select(2, perm), chunks).index_select(2, inv)
+    err = np.abs(o[0].permute(1, 0, 2).numpy() - ref_o).max()
+    assert err > 1e-2, f"contiguous positions on a striped layout not detected (err={err})"
+
+
 # ------------------------------------------------------------------ paged KV ----
 def test_paged_gather_index_math_known_answer():
     # python/hcp_vllm_block_ring_plugin.py:322-327: block (t - off)//bs, slot (t - off)%bs.
