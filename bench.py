@@ -9,7 +9,8 @@ the output rows) through ``hcp_ring_prefill_replay``, inputs resident in HBM.  `
 algorithmic FLOPs of causal pairs only: 2 GEMMs x 2 x D x Hq x S(S+1)/2.
 
 Also reported on the same line: paged decode GB/s (config c4), KV staging gather GB/s
-and the staged 128k prefill (config c5), the LSE merge GB/s, a roofline object for the
+and the staged 128k prefill (config c5), the LSE merge GB/s, the c3 prefill with Striped
+and ZigZag positions, a roofline object for the
 dominant kernel (the flash block kernel, from HIP events recorded by the replay
 driver on its launch stream over the timed region) and the CPU baseline (the oracle's
 op-for-op libtorch restatement of ring.rs timed on this host on a bounded sample).
@@ -164,6 +165,36 @@ def block_launch_bytes(c):
 
 
 # ------------------------------------------------------------------ c3 merge ----
+def bench_strategies(H, torch, tensors, steps: int, warmup: int):
+    """c3 ring prefill with Striped and ZigZag positions (strategy.rs:53-110): the same
+    causal FLOPs, rows in domain-major order, masks from the per-row key limits."""
+    c = C3
+    seq = sum(c["chunks"])
+    qh, kh, vh = (x.permute(1, 0, 2) for x in tensors)
+    out = torch.empty(c["hq"], seq, c["d"], dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(c["hq"], seq, dtype=torch.float32, device="cuda")
+    res = {}
+    for strat in ("striped", "zigzag"):
+        ws = torch.empty(H.replay_workspace_size(torch.bfloat16, c["hq"], c["hkv"], c["d"], c["chunks"],
+                                                 strategy=strat), dtype=torch.uint8, device="cuda")
+        step = lambda: H.ring_attention_replay(qh, kh, vh, c["chunks"], out=out, lse_out=lse, workspace=ws,
+                                               strategy=strat)
+        for _ in range(warmup):
+            step()
+        log(f"c3 prefill ({strat}) timed x{steps}")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        res[strat] = {"value": round(causal_flops(seq, c["hq"], c["d"]) / (ms * 1e-3) / 1e12, 1),
+                      "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+                      "finite": bool(torch.isfinite(lse).all().item())}
+        del ws
+    return res
+
+
 def bench_merge(H, torch, steps: int, warmup: int):
     """The LSE merge kernel (hcp_ring_lse_merge) on the c3 shapes: per target domain,
     its non-empty ring partials (o [Hq, L, D] + lse [Hq, L] fp32) -> bf16 rows + fp32
@@ -395,6 +426,8 @@ def main():
         log(f"c4 decode {dec['gbs']:.1f} GB/s")
         stg = bench_staged(H, torch, args.steps, args.warmup)
         mrg = bench_merge(H, torch, args.steps, args.warmup)
+        strat = bench_strategies(H, torch, pre["tensors"], args.steps, args.warmup)
+        log(f"c3 strategies {strat}")
         log(f"c3 lse merge {mrg['merge_gbs']:.1f} GB/s")
         log(f"c5 gather {stg['gather_gbs']:.1f} GB/s, prefill {stg.get('prefill_tflops', 0):.1f} TFLOP/s")
         extra = dict(
@@ -414,6 +447,7 @@ def main():
                                    "-> bf16 rows + fp32 LSE, one hcp_ring_lse_merge per domain",
                        "value": round(mrg["merge_gbs"], 1), "unit": "GB/s", "ms_per_step": round(mrg["merge_ms"], 4),
                        "frac_hbm": round(mrg["merge_gbs"] / PEAK_HBM_GBS, 4), "bytes": mrg["merge_bytes"]},
+            strategies=dict(workload="c3 ring prefill with Striped / ZigZag positions (same causal FLOPs)", **strat),
         )
     cpu = None
     if not args.no_cpu:
