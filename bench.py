@@ -195,6 +195,43 @@ def bench_strategies(H, torch, tensors, steps: int, warmup: int):
     return res
 
 
+def bench_wire(H, torch, tensors, steps: int, warmup: int):
+    """Device-side packing of one c3 domain chunk (8192 tokens) into the reference's
+    TCP frame payload (GQA-expanded fp32 K/V + int64 positions, tcp.rs:161-207) and
+    unpacking it back to compact bf16."""
+    c = C3
+    _, k, v = tensors
+    off, n = c["chunks"][0], c["chunks"][1]
+    kh, vh = (x[off:off + n].permute(1, 0, 2) for x in (k, v))
+    pos = torch.arange(off, off + n, dtype=torch.int64, device="cuda")
+    hdr, payload = H.kv_frame_pack(kh, vh, 0, off, off + n, positions=pos, num_heads=c["hq"])
+    desc, _ = H.kv_frame_parse(hdr)
+    desc.num_kv_heads = c["hkv"]
+    ko = torch.empty(c["hkv"], n, c["d"], dtype=torch.bfloat16, device="cuda")
+    vo = torch.empty_like(ko)
+    pack = lambda: H.lib().hcp_kv_frame_pack(H.ctypes.byref(desc), H.view(kh), H.view(vh), H._ptr(pos),
+                                             H._ptr(payload), None)
+    unpack = lambda: H.lib().hcp_kv_frame_unpack(H.ctypes.byref(desc), H._ptr(payload), H.view(ko), H.view(vo),
+                                                 None, None)
+    if pack() != 0 or unpack() != 0:
+        raise RuntimeError(f"wire pack/unpack failed: {H.last_error()}")
+    for _ in range(warmup):
+        pack()
+        unpack()
+    log(f"wire pack/unpack timed x{steps}")
+    t_pack = time_cuda(torch, pack, steps)
+    t_unpack = time_cuda(torch, unpack, steps)
+    ok = bool(torch.equal(ko, kh) and torch.equal(vo, vh))
+    compact = 2 * c["hkv"] * n * c["d"] * 2
+    wire = payload.numel()
+    return {"workload": f"c3 domain-1 chunk ({n} tokens): bf16 [8, L, 128] K/V -> reference TCP payload "
+                        f"(fp32, expanded to 32 heads, + int64 positions) and back",
+            "pack_gbs": round((compact + wire) / (t_pack * 1e-3) / 1e9, 1),
+            "unpack_gbs": round((wire // 4 + compact) / (t_unpack * 1e-3) / 1e9, 1),
+            "unit": "GB/s", "pack_ms": round(t_pack, 4), "unpack_ms": round(t_unpack, 4),
+            "payload_bytes": wire, "round_trip_bit_exact": ok}
+
+
 def bench_merge(H, torch, steps: int, warmup: int):
     """The LSE merge kernel (hcp_ring_lse_merge) on the c3 shapes: per target domain,
     its non-empty ring partials (o [Hq, L, D] + lse [Hq, L] fp32) -> bf16 rows + fp32
@@ -427,6 +464,8 @@ def main():
         stg = bench_staged(H, torch, args.steps, args.warmup)
         mrg = bench_merge(H, torch, args.steps, args.warmup)
         strat = bench_strategies(H, torch, pre["tensors"], args.steps, args.warmup)
+        wire = bench_wire(H, torch, pre["tensors"], args.steps, args.warmup)
+        log(f"wire {wire}")
         log(f"c3 strategies {strat}")
         log(f"c3 lse merge {mrg['merge_gbs']:.1f} GB/s")
         log(f"c5 gather {stg['gather_gbs']:.1f} GB/s, prefill {stg.get('prefill_tflops', 0):.1f} TFLOP/s")
@@ -448,6 +487,7 @@ def main():
                        "value": round(mrg["merge_gbs"], 1), "unit": "GB/s", "ms_per_step": round(mrg["merge_ms"], 4),
                        "frac_hbm": round(mrg["merge_gbs"] / PEAK_HBM_GBS, 4), "bytes": mrg["merge_bytes"]},
             strategies=dict(workload="c3 ring prefill with Striped / ZigZag positions (same causal FLOPs)", **strat),
+            kv_frame=wire,
         )
     cpu = None
     if not args.no_cpu:

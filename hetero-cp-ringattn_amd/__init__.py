@@ -95,6 +95,19 @@ class ReplayDesc(ctypes.Structure):
                 ("strategy", ctypes.c_int32)]
 
 
+class KvFrameDesc(ctypes.Structure):
+    _fields_ = [("layer_idx", ctypes.c_int64), ("global_seq_start", ctypes.c_int64),
+                ("global_seq_end", ctypes.c_int64), ("dtype", ctypes.c_int32), ("num_heads", ctypes.c_int32),
+                ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("len", ctypes.c_int64),
+                ("has_positions", ctypes.c_int32), ("reserved0", ctypes.c_int32)]
+
+
+class PacketFrameDesc(ctypes.Structure):
+    _fields_ = [("layer_idx", ctypes.c_int64), ("q_dtype", ctypes.c_int32), ("o_dtype", ctypes.c_int32),
+                ("batch", ctypes.c_int32), ("num_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("reserved0", ctypes.c_int32), ("scale", ctypes.c_double)]
+
+
 # RingSchedulingStrategy (strategy.rs:14-24) -> HCP_STRATEGY_*
 STRATEGIES = {"vanilla": 0, "striped": 1, "zigzag": 2}
 
@@ -157,6 +170,20 @@ def lib() -> ctypes.CDLL:
         "hcp_ring_prefill_replay_paged": ([ctypes.POINTER(ReplayDesc), View,
                                            ctypes.POINTER(PagedPool), vp, i64, View, vp, vp,
                                            ctypes.c_size_t, vp], ctypes.c_int),
+        "hcp_kv_frame_payload_bytes": ([ctypes.POINTER(KvFrameDesc)], ctypes.c_size_t),
+        "hcp_kv_frame_header": ([ctypes.POINTER(KvFrameDesc), vp, ctypes.c_size_t,
+                                 ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+        "hcp_kv_frame_parse": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(KvFrameDesc),
+                                ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+        "hcp_kv_frame_pack": ([ctypes.POINTER(KvFrameDesc), View, View, vp, vp, vp], ctypes.c_int),
+        "hcp_kv_frame_unpack": ([ctypes.POINTER(KvFrameDesc), vp, View, View, vp, vp], ctypes.c_int),
+        "hcp_packet_frame_payload_bytes": ([ctypes.POINTER(PacketFrameDesc)], ctypes.c_size_t),
+        "hcp_packet_frame_header": ([ctypes.POINTER(PacketFrameDesc), vp, ctypes.c_size_t,
+                                     ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+        "hcp_packet_frame_parse": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(PacketFrameDesc),
+                                    ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+        "hcp_packet_frame_pack": ([ctypes.POINTER(PacketFrameDesc), View, vp, vp, vp, vp], ctypes.c_int),
+        "hcp_packet_frame_unpack": ([ctypes.POINTER(PacketFrameDesc), vp, View, vp, vp, vp], ctypes.c_int),
         "hcp_synth_normals": ([ctypes.c_uint64, i64, i64, i32, vp, vp], ctypes.c_int),
         "hcp_ring_replay_timing": ([i32], ctypes.c_int),
         "hcp_ring_replay_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)],
@@ -519,6 +546,86 @@ def ring_attention_replay_paged(q, pool, block_table, chunks, causal=True, scale
                                                _stream(stream)))
     del arr
     return out, lse_out
+
+
+# ---------------------------------------------------------------------------------
+# (6) wire frames (tcp.rs)
+# ---------------------------------------------------------------------------------
+def _header(fn, desc) -> bytes:
+    n = ctypes.c_size_t(0)
+    getattr(lib(), fn)(ctypes.byref(desc), None, 0, ctypes.byref(n))
+    buf = ctypes.create_string_buffer(n.value)
+    _check(getattr(lib(), fn)(ctypes.byref(desc), buf, n.value, ctypes.byref(n)))
+    return buf.raw[:n.value]
+
+
+def kv_frame_desc(layer_idx, start, end, dtype, num_heads, num_kv_heads, head_dim, length,
+                  has_positions) -> KvFrameDesc:
+    return KvFrameDesc(layer_idx, start, end, dtype_code(dtype) if not isinstance(dtype, int) else dtype,
+                       num_heads, num_kv_heads, head_dim, length, 1 if has_positions else 0, 0)
+
+
+def kv_frame_header(desc: KvFrameDesc) -> bytes:
+    """[meta_len u32 BE][meta_json] of a KV block frame (tcp.rs:161-207)."""
+    return _header("hcp_kv_frame_header", desc)
+
+
+def kv_frame_pack(k, v, layer_idx, start, end, positions=None, num_heads=None, stream=None):
+    """KvBlock -> (header bytes, payload uint8 device tensor).  k / v [Hkv, L, D] views;
+    the wire carries num_heads (default Hkv) heads, head h from view head h / rep."""
+    torch = _torch()
+    hkv, length, d = k.shape
+    desc = kv_frame_desc(layer_idx, start, end, k.dtype, num_heads or hkv, hkv, d, length, positions is not None)
+    n = lib().hcp_kv_frame_payload_bytes(ctypes.byref(desc))
+    if n == 0:
+        raise HcpRingError(-6, "invalid KV frame descriptor")
+    payload = torch.empty(n, dtype=torch.uint8, device=k.device)
+    _check(lib().hcp_kv_frame_pack(ctypes.byref(desc), view(k), view(v), _ptr(positions), _ptr(payload),
+                                   _stream(stream)))
+    return kv_frame_header(desc), payload
+
+
+def kv_frame_parse(frame: bytes):
+    """(KvFrameDesc, header bytes) of a received frame."""
+    desc = KvFrameDesc()
+    hb = ctypes.c_size_t(0)
+    _check(lib().hcp_kv_frame_parse(frame, len(frame), ctypes.byref(desc), ctypes.byref(hb)))
+    return desc, hb.value
+
+
+def kv_frame_unpack(desc: KvFrameDesc, payload, k_out, v_out, positions_out=None, stream=None):
+    _check(lib().hcp_kv_frame_unpack(ctypes.byref(desc), _ptr(payload), view(k_out), view(v_out),
+                                     _ptr(positions_out), _stream(stream)))
+    return k_out, v_out, positions_out
+
+
+def packet_frame_pack(q, o, lse, layer_idx, scale, o_dtype=None, stream=None):
+    """RingPacket -> (header bytes, payload).  q [B, H, D] view, o fp32 [B, H, D], lse fp32 [B, H]."""
+    torch = _torch()
+    b, h, d = q.shape
+    desc = PacketFrameDesc(layer_idx, dtype_code(q.dtype), dtype_code(o_dtype or torch.float32), b, h, d, 0,
+                           float(scale))
+    n = lib().hcp_packet_frame_payload_bytes(ctypes.byref(desc))
+    if n == 0:
+        raise HcpRingError(-6, "invalid packet frame descriptor")
+    payload = torch.empty(n, dtype=torch.uint8, device=q.device)
+    qv = View(q.data_ptr(), q.stride(1), q.stride(0))
+    _check(lib().hcp_packet_frame_pack(ctypes.byref(desc), qv, _ptr(o), _ptr(lse), _ptr(payload), _stream(stream)))
+    return _header("hcp_packet_frame_header", desc), payload
+
+
+def packet_frame_parse(frame: bytes):
+    desc = PacketFrameDesc()
+    hb = ctypes.c_size_t(0)
+    _check(lib().hcp_packet_frame_parse(frame, len(frame), ctypes.byref(desc), ctypes.byref(hb)))
+    return desc, hb.value
+
+
+def packet_frame_unpack(desc: PacketFrameDesc, payload, q_out, o_out, lse_out, stream=None):
+    qv = View(q_out.data_ptr(), q_out.stride(1), q_out.stride(0))
+    _check(lib().hcp_packet_frame_unpack(ctypes.byref(desc), _ptr(payload), qv, _ptr(o_out), _ptr(lse_out),
+                                         _stream(stream)))
+    return q_out, o_out, lse_out
 
 
 # ---------------------------------------------------------------------------------

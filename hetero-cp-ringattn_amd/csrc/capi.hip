@@ -6,6 +6,7 @@
 // (rust_bridge.cc:19-27,614-644).  The C++ ring-replay driver (the single-GPU
 // counterpart of HcpRingAttentionBackend::ring_attention, ring.rs:861-1398) lives here
 // too; it only enqueues kernels.
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -699,6 +700,256 @@ int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_po
     }
     launch_lse_merge(num_domains, os.data(), ls.data(), desc->batch * desc->num_q_heads, 1, desc->head_dim,
                      desc->dtype, out.data, out.head_stride, out.head_stride, lse_out, 1, as_stream(stream));
+  });
+}
+
+namespace {
+
+void check_kv_frame(const hcp_kv_frame_desc* d) {
+  require(d != nullptr, "null descriptor");
+  elem_size(d->dtype);
+  require(d->num_heads > 0 && d->num_kv_heads > 0 && d->num_heads % d->num_kv_heads == 0,
+          "num_heads must be a positive multiple of num_kv_heads");
+  require(d->head_dim > 0, "head_dim must be positive");
+  require(d->len >= 0 && d->layer_idx >= 0 && d->global_seq_start >= 0 && d->global_seq_end >= 0,
+          "negative layer index, range or length");
+  require(d->has_positions == 0 || d->has_positions == 1, "has_positions must be 0 or 1");
+}
+
+size_t kv_plane_bytes(const hcp_kv_frame_desc* d) {
+  return static_cast<size_t>(d->num_heads) * d->len * d->head_dim * 4;
+}
+
+void check_packet_frame(const hcp_packet_frame_desc* d) {
+  require(d != nullptr, "null descriptor");
+  elem_size(d->q_dtype);
+  elem_size(d->o_dtype);
+  require(d->batch > 0 && d->num_heads > 0 && d->head_dim > 0, "bad packet shape");
+  require(d->layer_idx >= 0, "negative layer index");
+}
+
+void write_header(const std::string& meta, void* out, size_t cap, size_t* written) {
+  require(written != nullptr, "null written");
+  const size_t n = 4 + meta.size();
+  *written = n;
+  require(out != nullptr && cap >= n, "header buffer too small: need " + std::to_string(n) + " bytes");
+  unsigned char* o = static_cast<unsigned char*>(out);
+  const uint32_t m = static_cast<uint32_t>(meta.size());
+  o[0] = static_cast<unsigned char>(m >> 24);
+  o[1] = static_cast<unsigned char>(m >> 16);
+  o[2] = static_cast<unsigned char>(m >> 8);
+  o[3] = static_cast<unsigned char>(m);
+  std::memcpy(o + 4, meta.data(), meta.size());
+}
+
+const JVal& field(const JVal& o, const char* key) {
+  auto it = o.obj.find(key);
+  require(it != o.obj.end(), std::string("header: missing ") + key);
+  return it->second;
+}
+
+int64_t field_int(const JVal& o, const char* key) {
+  const JVal& v = field(o, key);
+  require(v.kind == JVal::kNum && v.integral, std::string("header: ") + key + " is not an integer");
+  return v.inum;
+}
+
+std::vector<int64_t> field_shape(const JVal& o, const char* key) {
+  const JVal& v = field(o, key);
+  require(v.kind == JVal::kArr, std::string("header: ") + key + " is not an array");
+  std::vector<int64_t> s;
+  for (const JVal& x : v.arr) {
+    require(x.kind == JVal::kNum && x.integral, std::string("header: bad ") + key);
+    s.push_back(x.inum);
+  }
+  return s;
+}
+
+int field_dtype(const JVal& o, const char* key) {
+  auto it = o.obj.find(key);
+  if (it == o.obj.end() || it->second.kind != JVal::kStr) return kF32;  // tcp.rs:701-704
+  return dtype_from_wire_name(it->second.str);
+}
+
+}  // namespace
+
+size_t hcp_kv_frame_payload_bytes(const hcp_kv_frame_desc* desc) {
+  try {
+    check_kv_frame(desc);
+    return 2 * kv_plane_bytes(desc) + (desc->has_positions ? static_cast<size_t>(desc->len) * 8 : 0);
+  } catch (...) {
+    return 0;
+  }
+}
+
+int hcp_kv_frame_header(const hcp_kv_frame_desc* desc, void* out, size_t capacity, size_t* written) {
+  return guarded(__func__, [&] {
+    check_kv_frame(desc);
+    write_header(kv_frame_meta(desc->layer_idx, desc->global_seq_start, desc->global_seq_end, desc->dtype,
+                               desc->num_heads, desc->len, desc->head_dim, desc->has_positions != 0),
+                 out, capacity, written);
+  });
+}
+
+int hcp_kv_frame_parse(const void* frame, size_t frame_bytes, hcp_kv_frame_desc* desc, size_t* header_bytes) {
+  return guarded(__func__, [&] {
+    require(desc != nullptr && header_bytes != nullptr, "null output");
+    const JVal m = parse_frame_meta(static_cast<const unsigned char*>(frame), frame_bytes, header_bytes);
+    auto t = m.obj.find("type");
+    require(t == m.obj.end() || t->second.kind != JVal::kStr, "header: not a KV block frame");
+    const std::vector<int64_t> ks = field_shape(m, "k_shape"), vs = field_shape(m, "v_shape");
+    require(ks.size() == 4 && ks[0] == 1 && ks == vs, "header: k/v shapes must be equal [1, H, L, D]");
+    hcp_kv_frame_desc d{};
+    d.layer_idx = field_int(m, "layer_idx");
+    d.global_seq_start = field_int(m, "global_seq_start");
+    d.global_seq_end = field_int(m, "global_seq_end");
+    d.dtype = field_dtype(m, "k_dtype");
+    require(field_dtype(m, "v_dtype") == d.dtype, "header: k and v dtypes differ");
+    require(ks[1] > 0 && ks[1] <= INT32_MAX && ks[3] > 0 && ks[3] <= INT32_MAX && ks[2] >= 0, "header: bad shape");
+    d.num_heads = d.num_kv_heads = static_cast<int32_t>(ks[1]);
+    d.len = ks[2];
+    d.head_dim = static_cast<int32_t>(ks[3]);
+    require(field_int(m, "k_bytes") == static_cast<int64_t>(kv_plane_bytes(&d)) &&
+                field_int(m, "v_bytes") == static_cast<int64_t>(kv_plane_bytes(&d)),
+            "header: k_bytes / v_bytes do not match the fp32 shape");
+    auto p = m.obj.find("position_ids");
+    if (p != m.obj.end() && p->second.kind != JVal::kNull) {
+      require(p->second.kind == JVal::kObj, "header: bad position_ids");
+      require(field(p->second, "dtype").str == "int64", "header: position_ids must be int64");
+      const std::vector<int64_t> ps = field_shape(p->second, "shape");
+      require(ps.size() == 1 && ps[0] == d.len && field_int(p->second, "bytes") == d.len * 8,
+              "header: position_ids shape does not match the block");
+      d.has_positions = 1;
+    }
+    check_kv_frame(&d);
+    *desc = d;
+  });
+}
+
+int hcp_kv_frame_pack(const hcp_kv_frame_desc* desc, hcp_ring_view k, hcp_ring_view v, const int64_t* positions,
+                      void* payload, void* stream) {
+  return guarded(__func__, [&] {
+    check_kv_frame(desc);
+    check_view(k, "k", desc->len);
+    check_view(v, "v", desc->len);
+    require(payload != nullptr, "null payload");
+    require(!desc->has_positions || positions != nullptr || desc->len == 0, "null positions");
+    const int64_t rep = desc->num_heads / desc->num_kv_heads;
+    float* wire = static_cast<float*>(payload);
+    const size_t plane = kv_plane_bytes(desc);
+    launch_wire_segment(true, desc->dtype, k.data, wire, desc->num_heads, rep, desc->len, desc->head_dim,
+                        k.head_stride, k.seq_stride, as_stream(stream));
+    launch_wire_segment(true, desc->dtype, v.data, wire + plane / 4, desc->num_heads, rep, desc->len,
+                        desc->head_dim, v.head_stride, v.seq_stride, as_stream(stream));
+    if (desc->has_positions && desc->len > 0)
+      HCP_HIP(hipMemcpyAsync(static_cast<char*>(payload) + 2 * plane, positions, desc->len * 8,
+                             hipMemcpyDeviceToDevice, as_stream(stream)));
+  });
+}
+
+int hcp_kv_frame_unpack(const hcp_kv_frame_desc* desc, const void* payload, hcp_ring_view k, hcp_ring_view v,
+                        int64_t* positions, void* stream) {
+  return guarded(__func__, [&] {
+    check_kv_frame(desc);
+    check_view(k, "k", desc->len);
+    check_view(v, "v", desc->len);
+    require(payload != nullptr, "null payload");
+    const int64_t rep = desc->num_heads / desc->num_kv_heads;
+    float* wire = const_cast<float*>(static_cast<const float*>(payload));
+    const size_t plane = kv_plane_bytes(desc);
+    launch_wire_segment(false, desc->dtype, k.data, wire, desc->num_heads, rep, desc->len, desc->head_dim,
+                        k.head_stride, k.seq_stride, as_stream(stream));
+    launch_wire_segment(false, desc->dtype, v.data, wire + plane / 4, desc->num_heads, rep, desc->len,
+                        desc->head_dim, v.head_stride, v.seq_stride, as_stream(stream));
+    if (desc->has_positions && positions != nullptr && desc->len > 0)
+      HCP_HIP(hipMemcpyAsync(positions, static_cast<const char*>(payload) + 2 * plane, desc->len * 8,
+                             hipMemcpyDeviceToDevice, as_stream(stream)));
+  });
+}
+
+size_t hcp_packet_frame_payload_bytes(const hcp_packet_frame_desc* desc) {
+  try {
+    check_packet_frame(desc);
+    const size_t rows = static_cast<size_t>(desc->batch) * desc->num_heads;
+    return rows * desc->head_dim * 4 * 2 + rows * 4;
+  } catch (...) {
+    return 0;
+  }
+}
+
+int hcp_packet_frame_header(const hcp_packet_frame_desc* desc, void* out, size_t capacity, size_t* written) {
+  return guarded(__func__, [&] {
+    check_packet_frame(desc);
+    write_header(packet_frame_meta(desc->layer_idx, desc->q_dtype, desc->o_dtype, desc->batch, desc->num_heads,
+                                   desc->head_dim, desc->scale),
+                 out, capacity, written);
+  });
+}
+
+int hcp_packet_frame_parse(const void* frame, size_t frame_bytes, hcp_packet_frame_desc* desc,
+                           size_t* header_bytes) {
+  return guarded(__func__, [&] {
+    require(desc != nullptr && header_bytes != nullptr, "null output");
+    const JVal m = parse_frame_meta(static_cast<const unsigned char*>(frame), frame_bytes, header_bytes);
+    const JVal& t = field(m, "type");
+    require(t.kind == JVal::kStr && t.str == "ring_packet", "header: not a ring_packet frame");
+    const std::vector<int64_t> qs = field_shape(m, "q_shape"), os = field_shape(m, "o_shape"),
+                               ls = field_shape(m, "lse_shape");
+    require(qs.size() == 4 && qs[2] == 1 && qs == os, "header: q/o shapes must be equal [B, H, 1, D]");
+    require(ls.size() == 3 && ls[0] == qs[0] && ls[1] == qs[1] && ls[2] == 1, "header: lse shape must be [B, H, 1]");
+    require(qs[0] > 0 && qs[0] <= INT32_MAX && qs[1] > 0 && qs[1] <= INT32_MAX && qs[3] > 0 && qs[3] <= INT32_MAX,
+            "header: bad shape");
+    hcp_packet_frame_desc d{};
+    d.layer_idx = field_int(m, "layer_idx");
+    d.q_dtype = field_dtype(m, "q_dtype");
+    d.o_dtype = field_dtype(m, "o_dtype");
+    d.batch = static_cast<int32_t>(qs[0]);
+    d.num_heads = static_cast<int32_t>(qs[1]);
+    d.head_dim = static_cast<int32_t>(qs[3]);
+    const JVal& sc = field(m, "scale");
+    require(sc.kind == JVal::kNum, "header: scale is not a number");
+    d.scale = sc.num;
+    const int64_t qb = static_cast<int64_t>(d.batch) * d.num_heads * d.head_dim * 4;
+    require(field_int(m, "q_bytes") == qb && field_int(m, "o_bytes") == qb &&
+                field_int(m, "lse_bytes") == static_cast<int64_t>(d.batch) * d.num_heads * 4,
+            "header: byte counts do not match the fp32 shapes");
+    check_packet_frame(&d);
+    *desc = d;
+  });
+}
+
+int hcp_packet_frame_pack(const hcp_packet_frame_desc* desc, hcp_ring_view q, const float* o, const float* lse,
+                          void* payload, void* stream) {
+  return guarded(__func__, [&] {
+    check_packet_frame(desc);
+    check_view(q, "q", 1);
+    require(o != nullptr && lse != nullptr && payload != nullptr, "null o, lse or payload");
+    const int64_t rows = static_cast<int64_t>(desc->batch) * desc->num_heads;
+    float* wire = static_cast<float*>(payload);
+    // q: wire row b = batch b, its [num_heads, head_dim] at (seq_stride, head_stride).
+    launch_wire_segment(true, desc->q_dtype, q.data, wire, desc->batch, 1, desc->num_heads, desc->head_dim,
+                        q.seq_stride, q.head_stride, as_stream(stream));
+    launch_wire_segment(true, kF32, const_cast<float*>(o), wire + rows * desc->head_dim, rows, 1, 1,
+                        desc->head_dim, desc->head_dim, desc->head_dim, as_stream(stream));
+    launch_wire_segment(true, kF32, const_cast<float*>(lse), wire + 2 * rows * desc->head_dim, rows, 1, 1, 1, 1, 1,
+                        as_stream(stream));
+  });
+}
+
+int hcp_packet_frame_unpack(const hcp_packet_frame_desc* desc, const void* payload, hcp_ring_view q, float* o,
+                            float* lse, void* stream) {
+  return guarded(__func__, [&] {
+    check_packet_frame(desc);
+    check_view(q, "q", 1);
+    require(o != nullptr && lse != nullptr && payload != nullptr, "null o, lse or payload");
+    const int64_t rows = static_cast<int64_t>(desc->batch) * desc->num_heads;
+    float* wire = const_cast<float*>(static_cast<const float*>(payload));
+    launch_wire_segment(false, desc->q_dtype, q.data, wire, desc->batch, 1, desc->num_heads, desc->head_dim,
+                        q.seq_stride, q.head_stride, as_stream(stream));
+    launch_wire_segment(false, kF32, o, wire + rows * desc->head_dim, rows, 1, 1, desc->head_dim, desc->head_dim,
+                        desc->head_dim, as_stream(stream));
+    launch_wire_segment(false, kF32, lse, wire + 2 * rows * desc->head_dim, rows, 1, 1, 1, 1, 1,
+                        as_stream(stream));
   });
 }
 

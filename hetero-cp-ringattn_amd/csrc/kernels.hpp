@@ -1,6 +1,10 @@
 // Host-side launchers of the gfx950 kernels (internal to the library).
 #pragma once
 
+#include <map>
+#include <string>
+#include <vector>
+
 #include "hcp_common.hpp"
 
 namespace hcp {
@@ -89,6 +93,29 @@ struct KeyLimitArgs {
   int* err;
 };
 void launch_key_limits(const KeyLimitArgs& a, int n_src, int64_t max_k_len, hipStream_t stream);
+
+// Wire frames (wire.hip): fp32 payload segments <-> strided storage views, the
+// serde_json-compatible headers and a reader for them.
+void launch_wire_segment(bool pack, int dtype, void* tensor, float* wire, int64_t rows, int64_t rep, int64_t len,
+                         int64_t dim, int64_t hs, int64_t ss, hipStream_t stream);
+const char* dtype_wire_name(int dtype);
+int dtype_from_wire_name(const std::string& s);
+std::string json_f64(double x);
+std::string kv_frame_meta(int64_t layer_idx, int64_t start, int64_t end, int dtype, int64_t heads, int64_t len,
+                          int64_t dim, bool positions);
+std::string packet_frame_meta(int64_t layer_idx, int q_dtype, int o_dtype, int64_t batch, int64_t heads,
+                              int64_t dim, double scale);
+// A JSON value restricted to what the frame headers hold.
+struct JVal {
+  enum Kind { kNull, kNum, kStr, kArr, kObj } kind = kNull;
+  double num = 0;
+  bool integral = false;
+  int64_t inum = 0;
+  std::string str;
+  std::vector<JVal> arr;
+  std::map<std::string, JVal> obj;
+};
+JVal parse_frame_meta(const unsigned char* frame, size_t n, size_t* header_bytes);
 
 void launch_synth_normals(uint64_t seed, int64_t offset, int64_t count, int dtype, void* out,
                           hipStream_t stream);

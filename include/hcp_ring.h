@@ -363,6 +363,77 @@ int hcp_ring_prefill_replay_paged(const hcp_ring_replay_desc* desc, hcp_ring_vie
                                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * (6) Wire frames of the ring transport (TcpKvTransport, rust/src/model/transport/
+ * tcp.rs:20-40; serialize_block_to_buffer :161-207; serialize_packet_to_buffer
+ * :209-243; decode_frame_from_reader :604-787).
+ *
+ * A KvBlock frame is [meta_len u32 BE][meta_json][k f32 LE][v f32 LE][positions i64 LE]
+ * and a RingPacket frame [meta_len u32 BE][meta_json][q f32 LE][o f32 LE][lse f32 LE].
+ * The header (length prefix + JSON, byte-identical to the reference's serde_json
+ * output: compact, keys sorted) is built and parsed on the HOST; the payload (the
+ * fp32 tensor bytes, plus the int64 positions) is packed and unpacked on the DEVICE
+ * straight from / into strided views.  A frame on the wire is header then payload.
+ *
+ * KV frames: k / v views hold num_kv_heads heads of [len, head_dim] in `dtype`; the
+ * wire carries num_heads = rep * num_kv_heads heads (the reference sends blocks after
+ * the GQA expand, ring.rs:999-1019: pass num_heads = Hq to interoperate with it, or
+ * num_heads = num_kv_heads for the compact form).  Pack writes wire head h from view
+ * head h / rep; unpack writes view head h from wire head h * rep.  The k/v shape in
+ * the header is [1, num_heads, len, head_dim]; position_ids, when present, is int64 [len].
+ * hcp_kv_frame_parse fills a descriptor from a received header (num_kv_heads =
+ * num_heads; lower it before unpacking to keep one head per group); a header whose
+ * position_ids is null or absent (the legacy frame, tcp.rs:802-813,937-963) gives
+ * has_positions = 0.  The payload pointer must be 16-byte aligned (4-byte when
+ * head_dim is not a multiple of 4); header buffers are HOST memory.
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_kv_frame_desc {
+  int64_t layer_idx;
+  int64_t global_seq_start;
+  int64_t global_seq_end;
+  int32_t dtype;         /* storage dtype, named in k_dtype / v_dtype */
+  int32_t num_heads;     /* heads on the wire */
+  int32_t num_kv_heads;  /* heads of the k / v views (divides num_heads) */
+  int32_t head_dim;
+  int64_t len;           /* tokens in the block */
+  int32_t has_positions;
+  int32_t reserved0;
+} hcp_kv_frame_desc;
+
+size_t hcp_kv_frame_payload_bytes(const hcp_kv_frame_desc* desc);
+int hcp_kv_frame_header(const hcp_kv_frame_desc* desc, void* out, size_t capacity, size_t* written);
+int hcp_kv_frame_parse(const void* frame, size_t frame_bytes, hcp_kv_frame_desc* desc,
+                       size_t* header_bytes);
+int hcp_kv_frame_pack(const hcp_kv_frame_desc* desc, hcp_ring_view k, hcp_ring_view v,
+                      const int64_t* positions, void* payload, void* stream);
+int hcp_kv_frame_unpack(const hcp_kv_frame_desc* desc, const void* payload, hcp_ring_view k,
+                        hcp_ring_view v, int64_t* positions, void* stream);
+
+/* Decode Q-ring packets (RingPacket, block.rs:74-93): q [batch, num_heads, 1, head_dim]
+ * in q_dtype (a view: seq_stride = batch stride, head_stride = head stride), o the fp32
+ * accumulator [batch, num_heads, head_dim] (o_dtype is the name written for it, the
+ * reference keeps o in the query dtype), lse fp32 [batch, num_heads]. */
+typedef struct hcp_packet_frame_desc {
+  int64_t layer_idx;
+  int32_t q_dtype;
+  int32_t o_dtype;
+  int32_t batch;
+  int32_t num_heads;
+  int32_t head_dim;
+  int32_t reserved0;
+  double scale;
+} hcp_packet_frame_desc;
+
+size_t hcp_packet_frame_payload_bytes(const hcp_packet_frame_desc* desc);
+int hcp_packet_frame_header(const hcp_packet_frame_desc* desc, void* out, size_t capacity,
+                            size_t* written);
+int hcp_packet_frame_parse(const void* frame, size_t frame_bytes, hcp_packet_frame_desc* desc,
+                           size_t* header_bytes);
+int hcp_packet_frame_pack(const hcp_packet_frame_desc* desc, hcp_ring_view q, const float* o,
+                          const float* lse, void* payload, void* stream);
+int hcp_packet_frame_unpack(const hcp_packet_frame_desc* desc, const void* payload, hcp_ring_view q,
+                            float* o, float* lse, void* stream);
+
+/* ---------------------------------------------------------------------------------
  * Replay kernel timing (no reference counterpart; benchmark instrumentation; the
  * reference logs wall-clock compute per phase to HCP_PERF_LOG, ring.rs:820-844).
  *

@@ -121,6 +121,46 @@ def kats(name):
         json.dump(data, f, indent=1)
 
 
+def wire_frames(name):
+    """Frames of the reference's own TCP transport tests, restated byte for byte."""
+    from oracle import wire as W
+    ar = lambda n, s, shape: (np.arange(n, dtype=np.float32) * s).reshape(shape)
+    cases = [
+        ("positioned_partial_frame", "rust/src/model/transport/tcp.rs:816-864",
+         dict(layer_idx=7, start=2, end=10, k=ar(4, 1.0, (1, 1, 2, 2)), v=ar(4, 0.25, (1, 1, 2, 2)),
+              positions=[2, 9])),
+        ("positioned_roundtrip", "rust/src/model/transport/tcp.rs:898-935",
+         dict(layer_idx=5, start=0, end=3, k=ar(6, 1.0, (1, 1, 3, 2)), v=ar(6, 0.5, (1, 1, 3, 2)),
+              positions=[0, 9, 16777217])),
+        ("unpositioned", "rust/src/model/transport/tcp.rs:867-896 (KvBlock::single)",
+         dict(layer_idx=3, start=4, end=6, k=ar(4, 1.0, (1, 1, 2, 2)), v=ar(4, 1.0, (1, 1, 2, 2)), positions=None)),
+    ]
+    out = []
+    for cname, src, c in cases:
+        frame = W.kv_block_frame(c["layer_idx"], c["start"], c["end"], c["k"], c["v"], "float32", c["positions"])
+        out.append({"name": cname, "source": src, "kind": "kv_block", "layer_idx": c["layer_idx"],
+                    "start": c["start"], "end": c["end"], "k": c["k"].tolist(), "v": c["v"].tolist(),
+                    "positions": c["positions"], "frame_hex": frame.hex()})
+    # the legacy frame of tcp.rs:937-963: position_ids removed from the meta
+    legacy = W.kv_block_frame(2, 4, 6, ar(4, 1.0, (1, 1, 2, 2)), ar(4, 1.0, (1, 1, 2, 2)), "float32", None)
+    n = int.from_bytes(legacy[:4], "big")
+    meta = json.loads(legacy[4:4 + n])
+    del meta["position_ids"]
+    m = W._dumps(meta).encode()
+    out.append({"name": "legacy_without_position_metadata", "source": "rust/src/model/transport/tcp.rs:802-813,937-963",
+                "kind": "kv_block", "layer_idx": 2, "start": 4, "end": 6, "positions": None,
+                "frame_hex": (len(m).to_bytes(4, "big") + m + legacy[4 + n:]).hex()})
+    q = ar(16, 0.5, (1, 2, 1, 8))
+    o = ar(16, -0.25, (1, 2, 1, 8))
+    lse = ar(2, 1.5, (1, 2, 1))
+    pk = W.ring_packet_frame(4, q, o, lse, 1 / math.sqrt(8), "bfloat16", "bfloat16")
+    out.append({"name": "ring_packet", "source": "rust/src/model/transport/tcp.rs:209-243", "kind": "ring_packet",
+                "layer_idx": 4, "scale": 1 / math.sqrt(8), "q": q.tolist(), "o": o.tolist(), "lse": lse.tolist(),
+                "frame_hex": pk.hex()})
+    with open(os.path.join(HERE, name), "w") as f:
+        json.dump(out, f, indent=1)
+
+
 def main():
     block_case("block_bf16_gqa4.npz", 101, 72, 136, 4, 1, 128, 100, 0, True)
     block_case("block_bf16_future_d64.npz", 102, 64, 64, 2, 2, 64, 0, 50, True)
@@ -129,6 +169,7 @@ def main():
     paged_case("paged_bf16_ragged.npz", 104)
     decode_case("decode_bf16_small.npz", 105)
     kats("reference_kats.json")
+    wire_frames("wire_frames.json")
 
 
 if __name__ == "__main__":

@@ -234,3 +234,57 @@ def test_gpu_paged_decode_on_fixture(gpu):
     torch.cuda.synchronize()
     assert np.abs(o.cpu().numpy() - g["o"]).max() <= 2e-2
     assert np.abs(lse.cpu().numpy() - g["lse"]).max() <= 1e-3
+
+
+def _wire_cases():
+    with open(os.path.join(GOLD, "wire_frames.json")) as f:
+        return json.load(f)
+
+
+def test_wire_frame_oracle_round_trip():
+    # The oracle's parser recovers what the reference's tests assert after a TCP
+    # round trip (layer, range, positions, tensors), from the stored frames.
+    from oracle import wire as W
+    for c in _wire_cases():
+        if c["kind"] != "kv_block":
+            continue
+        meta, k, v, pos = W.parse_kv_block_frame(bytes.fromhex(c["frame_hex"]))
+        assert (meta["layer_idx"], meta["global_seq_start"], meta["global_seq_end"]) == (c["layer_idx"], c["start"],
+                                                                                         c["end"])
+        assert (pos is None and c["positions"] is None) or pos.tolist() == c["positions"]
+        if "k" in c:
+            assert k.tolist() == c["k"] and v.tolist() == c["v"]
+
+
+def test_wire_headers_match_reference_frames():
+    # The library's host-side header writer is byte-identical to the restated
+    # serde_json output of serialize_block_to_buffer / serialize_packet_to_buffer.
+    for c in _wire_cases():
+        frame = bytes.fromhex(c["frame_hex"])
+        n = 4 + int.from_bytes(frame[:4], "big")
+        if c["kind"] == "ring_packet":
+            q = np.array(c["q"])
+            desc = H.PacketFrameDesc(c["layer_idx"], H.DTYPE_BF16, H.DTYPE_BF16, q.shape[0], q.shape[1], q.shape[3], 0,
+                                     c["scale"])
+            assert H._header("hcp_packet_frame_header", desc) == frame[:n]
+            d, hb = H.packet_frame_parse(frame)
+            assert hb == n and (d.batch, d.num_heads, d.head_dim, d.layer_idx) == (1, 2, 8, 4)
+            assert d.scale == c["scale"] and d.q_dtype == H.DTYPE_BF16
+            continue
+        d, hb = H.kv_frame_parse(frame)
+        assert hb == n
+        assert (d.layer_idx, d.global_seq_start, d.global_seq_end) == (c["layer_idx"], c["start"], c["end"])
+        assert d.has_positions == (c["positions"] is not None)
+        if c["name"].startswith("legacy"):
+            continue  # written by the reference's old serializer only
+        assert H.kv_frame_header(d) == frame[:n]
+
+
+def test_wire_parse_rejects_inconsistent_headers():
+    c = _wire_cases()[0]
+    frame = bytearray(bytes.fromhex(c["frame_hex"]))
+    bad = bytes(frame).replace(b'"k_bytes":16', b'"k_bytes":17')
+    with pytest.raises(H.HcpRingError):
+        H.kv_frame_parse(bad)
+    with pytest.raises(H.HcpRingError):
+        H.kv_frame_parse(bytes(frame[:10]))

@@ -534,3 +534,76 @@ def test_ring_replay_paged_strategy_matches_unpaged(gpu):
     o2, l2 = H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, chunks, strategy="zigzag")
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def _wire_cases():
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "wire_frames.json")) as f:
+        return json.load(f)
+
+
+def test_kv_frame_pack_reproduces_reference_frames(gpu):
+    # header + device-packed payload == the stored frames of the reference's TCP tests
+    for c in _wire_cases():
+        if c["kind"] != "kv_block" or "k" not in c:
+            continue
+        k = torch.tensor(c["k"], dtype=torch.float32).cuda()[0]
+        v = torch.tensor(c["v"], dtype=torch.float32).cuda()[0]
+        pos = torch.tensor(c["positions"], dtype=torch.int64).cuda() if c["positions"] is not None else None
+        hdr, payload = H.kv_frame_pack(k, v, c["layer_idx"], c["start"], c["end"], positions=pos)
+        torch.cuda.synchronize()
+        assert hdr + payload.cpu().numpy().tobytes() == bytes.fromhex(c["frame_hex"]), c["name"]
+
+
+@pytest.mark.parametrize("dtype,hkv,rep,length,d", [(torch.bfloat16, 2, 4, 300, 128), (torch.float16, 4, 1, 77, 64),
+                                                    (torch.float32, 1, 8, 33, 128)])
+def test_kv_frame_expand_and_round_trip(gpu, dtype, hkv, rep, length, d):
+    from oracle import wire as W
+    (kb, vb), _ = draw(150 + length, [(length, hkv, d + 8), (length, hkv, d + 8)], dtype)
+    k, v = kb[:, :, :d].permute(1, 0, 2), vb[:, :, :d].permute(1, 0, 2)   # strided [Hkv, L, D] views
+    pos = torch.arange(5, 5 + 3 * length, 3, dtype=torch.int64, device="cuda")
+    hdr, payload = H.kv_frame_pack(k, v, 9, 5, 5 + 3 * length, positions=pos, num_heads=hkv * rep)
+    torch.cuda.synchronize()
+    # the oracle frame of the GQA-expanded fp32 block (ring.rs:999-1019, tcp.rs:161-207)
+    kx = k.float().cpu().repeat_interleave(rep, 0).unsqueeze(0).numpy()
+    vx = v.float().cpu().repeat_interleave(rep, 0).unsqueeze(0).numpy()
+    name = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}[dtype]
+    ref = W.kv_block_frame(9, 5, 5 + 3 * length, kx, vx, name, pos.cpu().numpy())
+    frame = hdr + payload.cpu().numpy().tobytes()
+    assert frame == ref
+    # receive: parse the header, keep one head per group, unpack bit-exactly
+    desc, hb = H.kv_frame_parse(frame)
+    assert hb == len(hdr) and desc.num_heads == hkv * rep and desc.dtype == H.dtype_code(dtype)
+    desc.num_kv_heads = hkv
+    ko = torch.zeros(hkv, length, d, dtype=dtype, device="cuda")
+    vo = torch.zeros_like(ko)
+    po = torch.zeros(length, dtype=torch.int64, device="cuda")
+    H.kv_frame_unpack(desc, payload, ko, vo, po)
+    torch.cuda.synchronize()
+    assert torch.equal(ko.view(torch.uint8 if dtype != torch.float32 else torch.int32),
+                       k.contiguous().view(torch.uint8 if dtype != torch.float32 else torch.int32))
+    assert torch.equal(vo, v) and torch.equal(po, pos)
+
+
+def test_packet_frame_matches_oracle_and_round_trips(gpu):
+    from oracle import wire as W
+    b, h, d = 3, 32, 128
+    (qb,), _ = draw(160, [(b, h, d + 16)], torch.bfloat16)
+    q = qb[:, :, :d]                                   # strided [B, H, D] view
+    o = torch.randn(b, h, d, device="cuda")
+    lse = torch.randn(b, h, device="cuda")
+    scale = 1 / math.sqrt(d)
+    hdr, payload = H.packet_frame_pack(q, o, lse, 12, scale)
+    torch.cuda.synchronize()
+    ref = W.ring_packet_frame(12, q.float().cpu().unsqueeze(2).numpy(), o.cpu().unsqueeze(2).numpy(),
+                              lse.cpu().unsqueeze(2).numpy(), scale, "bfloat16", "float32")
+    frame = hdr + payload.cpu().numpy().tobytes()
+    assert frame == ref
+    desc, hb = H.packet_frame_parse(frame)
+    assert hb == len(hdr) and desc.scale == scale and (desc.batch, desc.num_heads, desc.head_dim) == (b, h, d)
+    qo = torch.zeros(b, h, d, dtype=torch.bfloat16, device="cuda")
+    oo, lo = torch.zeros_like(o), torch.zeros_like(lse)
+    H.packet_frame_unpack(desc, payload, qo, oo, lo)
+    torch.cuda.synchronize()
+    assert torch.equal(qo, q) and torch.equal(oo, o) and torch.equal(lo, lse)
