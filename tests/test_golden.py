@@ -288,3 +288,24 @@ def test_wire_parse_rejects_inconsistent_headers():
         H.kv_frame_parse(bad)
     with pytest.raises(H.HcpRingError):
         H.kv_frame_parse(bytes(frame[:10]))
+
+
+@pytest.mark.parametrize("scale", [0.125, 1.0, 100.0, 1e-5, 1.5e-7, 1e16, 1e17, 123456.789, 0.08838834764831845,
+                                   2.0 ** -20, 0.0001, 3.0e-5])
+def test_packet_header_float_format(scale):
+    # serde_json writes f64 through ryu: the library's writer (std::to_chars digits) and
+    # the oracle's (Python repr digits) must agree on every notation branch.
+    from oracle import wire as W
+    q = np.zeros((1, 2, 1, 4), dtype=np.float32)
+    ref = W.ring_packet_frame(0, q, q, np.zeros((1, 2, 1), np.float32), scale, "float32", "float32")
+    desc = H.PacketFrameDesc(0, H.DTYPE_F32, H.DTYPE_F32, 1, 2, 4, 0, scale)
+    hdr = H._header("hcp_packet_frame_header", desc)
+    assert hdr == ref[:len(hdr)]
+
+
+def test_ryu_notation_examples():
+    from oracle import wire as W
+    cases = {1.0: "1.0", 100.0: "100.0", 1e16: "1e16", 1.5e-7: "1.5e-7", 1e-5: "0.00001", 0.1: "0.1",
+             123456.0: "123456.0", 1e15: "1000000000000000.0", 1.2345e30: "1.2345e30", -2.5: "-2.5"}
+    for x, s in cases.items():
+        assert W.ryu_f64(x) == s, x
