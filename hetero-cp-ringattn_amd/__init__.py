@@ -108,6 +108,12 @@ class PacketFrameDesc(ctypes.Structure):
                 ("reserved0", ctypes.c_int32), ("scale", ctypes.c_double)]
 
 
+class QkvDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int32), ("hidden", ctypes.c_int32), ("num_q_heads", ctypes.c_int32),
+                ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("rope", ctypes.c_int32),
+                ("tokens", ctypes.c_int64), ("rope_rows", ctypes.c_int64)]
+
+
 # RingSchedulingStrategy (strategy.rs:14-24) -> HCP_STRATEGY_*
 STRATEGIES = {"vanilla": 0, "striped": 1, "zigzag": 2}
 
@@ -184,6 +190,11 @@ def lib() -> ctypes.CDLL:
                                     ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
         "hcp_packet_frame_pack": ([ctypes.POINTER(PacketFrameDesc), View, vp, vp, vp, vp], ctypes.c_int),
         "hcp_packet_frame_unpack": ([ctypes.POINTER(PacketFrameDesc), vp, View, vp, vp, vp], ctypes.c_int),
+        "hcp_rope_table": ([i32, i64, ctypes.c_double, vp, vp], ctypes.c_int),
+        "hcp_qkv_rope_project": ([ctypes.POINTER(QkvDesc), vp, i64, vp, vp, vp, vp, vp, vp, vp, vp, View, View,
+                                  View, vp], ctypes.c_int),
+        "hcp_qkv_rope_project_paged": ([ctypes.POINTER(QkvDesc), vp, i64, vp, vp, vp, vp, vp, vp, vp, vp, View,
+                                        ctypes.POINTER(PagedPool), vp, i64, i64, i64, vp], ctypes.c_int),
         "hcp_synth_normals": ([ctypes.c_uint64, i64, i64, i32, vp, vp], ctypes.c_int),
         "hcp_ring_replay_timing": ([i32], ctypes.c_int),
         "hcp_ring_replay_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)],
@@ -626,6 +637,66 @@ def packet_frame_unpack(desc: PacketFrameDesc, payload, q_out, o_out, lse_out, s
     _check(lib().hcp_packet_frame_unpack(ctypes.byref(desc), _ptr(payload), qv, _ptr(o_out), _ptr(lse_out),
                                          _stream(stream)))
     return q_out, o_out, lse_out
+
+
+# ---------------------------------------------------------------------------------
+# (7) fused QKV projection + RoPE + KV append
+# ---------------------------------------------------------------------------------
+def rope_table(head_dim: int, rows: int, base: float = 10000.0, device="cuda", stream=None):
+    """cos / sin caches of RotaryEmbedding::new (rotary.rs:64-97) -> fp32 [2, rows, D/2]."""
+    torch = _torch()
+    t = torch.empty((2, rows, head_dim // 2), dtype=torch.float32, device=device)
+    _check(lib().hcp_rope_table(head_dim, rows, float(base), _ptr(t), _stream(stream)))
+    return t
+
+
+def _qkv_args(x, wq, num_q_heads, num_kv_heads, head_dim, positions, table, rope):
+    torch = _torch()
+    tokens, hidden = x.shape
+    if x.stride(1) != 1:
+        raise ValueError("x rows must be contiguous")
+    desc = QkvDesc(dtype_code(x.dtype), hidden, num_q_heads, num_kv_heads, head_dim, 1 if rope else 0, tokens,
+                   table.shape[1] if table is not None else 0)
+    if rope and (positions is None or positions.dtype != torch.int64 or positions.numel() != tokens):
+        raise ValueError("rope needs int64 positions of one entry per token")
+    return desc
+
+
+def qkv_rope_project(x, wq, wk, wv, num_q_heads, num_kv_heads, head_dim, positions=None, table=None,
+                     bq=None, bk=None, bv=None, rope=True, q_out=None, k_out=None, v_out=None, stream=None):
+    """ring.rs:1865-1908 on the GPU: x [L, hidden] -> q [Hq, L, D], k / v [Hkv, L, D]
+    (q, k rotated at ``positions`` with the ``table`` of :func:`rope_table`)."""
+    torch = _torch()
+    tokens = x.shape[0]
+    desc = _qkv_args(x, wq, num_q_heads, num_kv_heads, head_dim, positions, table, rope)
+    if q_out is None:
+        q_out = torch.empty((num_q_heads, tokens, head_dim), dtype=x.dtype, device=x.device)
+    if k_out is None:
+        k_out = torch.empty((num_kv_heads, tokens, head_dim), dtype=x.dtype, device=x.device)
+    if v_out is None:
+        v_out = torch.empty((num_kv_heads, tokens, head_dim), dtype=x.dtype, device=x.device)
+    _check(lib().hcp_qkv_rope_project(ctypes.byref(desc), _ptr(x), x.stride(0), _ptr(wq), _ptr(wk), _ptr(wv),
+                                      _ptr(bq), _ptr(bk), _ptr(bv), _ptr(positions), _ptr(table), view(q_out),
+                                      view(k_out), view(v_out), _stream(stream)))
+    return q_out, k_out, v_out
+
+
+def qkv_rope_project_paged(x, wq, wk, wv, num_q_heads, num_kv_heads, head_dim, pool, block_table,
+                           table_seq_offset: int, t0: int, positions=None, table=None, bq=None, bk=None, bv=None,
+                           rope=True, q_out=None, stream=None):
+    """As :func:`qkv_rope_project`, k / v appended to the paged pool at sequence
+    positions t0 .. t0 + L (KvCache::update, cache.rs:191-251)."""
+    torch = _torch()
+    tokens = x.shape[0]
+    desc = _qkv_args(x, wq, num_q_heads, num_kv_heads, head_dim, positions, table, rope)
+    if q_out is None:
+        q_out = torch.empty((num_q_heads, tokens, head_dim), dtype=x.dtype, device=x.device)
+    pp = paged_pool(pool)
+    _check(lib().hcp_qkv_rope_project_paged(ctypes.byref(desc), _ptr(x), x.stride(0), _ptr(wq), _ptr(wk),
+                                            _ptr(wv), _ptr(bq), _ptr(bk), _ptr(bv), _ptr(positions), _ptr(table),
+                                            view(q_out), ctypes.byref(pp), _ptr(block_table), block_table.numel(),
+                                            table_seq_offset, t0, _stream(stream)))
+    return q_out
 
 
 # ---------------------------------------------------------------------------------

@@ -953,6 +953,117 @@ int hcp_packet_frame_unpack(const hcp_packet_frame_desc* desc, const void* paylo
   });
 }
 
+namespace {
+
+bool aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+QkvArgs make_qkv(const hcp_qkv_desc* d, const void* x, int64_t x_ss, const void* wq, const void* wk, const void* wv,
+                 const void* bq, const void* bk, const void* bv, const int64_t* positions, const float* table,
+                 hcp_ring_view q_out) {
+  require(d != nullptr, "null descriptor");
+  require(d->dtype == kBF16 || d->dtype == kF16, "dtype must be BF16 or F16");
+  require(d->head_dim == 64 || d->head_dim == 128, "head_dim must be 64 or 128");
+  require(d->hidden > 0 && d->hidden % 32 == 0, "hidden must be a positive multiple of 32");
+  require(d->num_q_heads > 0 && d->num_kv_heads > 0, "head counts must be positive");
+  require((static_cast<int64_t>(d->num_q_heads) * d->head_dim) % 128 == 0 &&
+              (static_cast<int64_t>(d->num_kv_heads) * d->head_dim) % 128 == 0,
+          "Hq*D and Hkv*D must be multiples of 128");
+  require(static_cast<int64_t>(d->num_q_heads + 2 * d->num_kv_heads) * d->head_dim <= INT32_MAX,
+          "too many output features");
+  require(d->tokens >= 0 && d->tokens <= INT32_MAX, "tokens must be in [0, 2^31)");
+  require(d->rope == 0 || d->rope == 1, "rope must be 0 or 1");
+  require(x != nullptr || d->tokens == 0, "null x");
+  require(aligned(x, 16) && x_ss % 8 == 0 && x_ss >= d->hidden, "x must be 16-byte aligned, row stride a multiple of 8 >= hidden");
+  require(wq && wk && wv && aligned(wq, 16) && aligned(wk, 16) && aligned(wv, 16), "weights must be non-null and 16-byte aligned");
+  if (d->rope) require(positions != nullptr && table != nullptr && d->rope_rows > 0, "rope needs positions and a table");
+  require(q_out.data != nullptr && aligned(q_out.data, 8) && q_out.head_stride % 4 == 0 && q_out.seq_stride % 4 == 0,
+          "q_out must be 8-byte aligned with strides multiple of 4");
+  QkvArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_ss = x_ss;
+  a.w[0] = static_cast<const uint16_t*>(wq);
+  a.w[1] = static_cast<const uint16_t*>(wk);
+  a.w[2] = static_cast<const uint16_t*>(wv);
+  a.bias[0] = static_cast<const uint16_t*>(bq);
+  a.bias[1] = static_cast<const uint16_t*>(bk);
+  a.bias[2] = static_cast<const uint16_t*>(bv);
+  a.nq = d->num_q_heads * d->head_dim;
+  a.nkv = d->num_kv_heads * d->head_dim;
+  a.hidden = d->hidden;
+  a.tokens = static_cast<int32_t>(d->tokens);
+  a.rope = d->rope;
+  a.pos = positions;
+  a.rope_cos = table;
+  a.rope_sin = table ? table + d->rope_rows * (d->head_dim / 2) : nullptr;
+  a.rope_rows = d->rope_rows;
+  a.out[0] = static_cast<uint16_t*>(q_out.data);
+  a.out_hs[0] = q_out.head_stride;
+  a.out_ss[0] = q_out.seq_stride;
+  a.err = device_error_flags();
+  return a;
+}
+
+void check_qkv_out(const hcp_ring_view& v, const char* name) {
+  require(v.data != nullptr && aligned(v.data, 8) && v.head_stride % 4 == 0 && v.seq_stride % 4 == 0,
+          std::string(name) + " must be 8-byte aligned with strides multiple of 4");
+}
+
+}  // namespace
+
+int hcp_rope_table(int32_t head_dim, int64_t rows, double base, float* table, void* stream) {
+  return guarded(__func__, [&] {
+    require(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 256, "head_dim must be even and <= 256");
+    require(rows >= 0 && rows <= (int64_t(1) << 24), "rows must be in [0, 2^24] (fp32-exact positions)");
+    require(base > 0, "base must be positive");
+    require(table != nullptr || rows == 0, "null table");
+    launch_rope_table(head_dim, rows, base, table, table + rows * (head_dim / 2), as_stream(stream));
+  });
+}
+
+int hcp_qkv_rope_project(const hcp_qkv_desc* desc, const void* x, int64_t x_row_stride, const void* wq,
+                         const void* wk, const void* wv, const void* bq, const void* bk, const void* bv,
+                         const int64_t* positions, const float* rope_table, hcp_ring_view q_out, hcp_ring_view k_out,
+                         hcp_ring_view v_out, void* stream) {
+  return guarded(__func__, [&] {
+    QkvArgs a = make_qkv(desc, x, x_row_stride, wq, wk, wv, bq, bk, bv, positions, rope_table, q_out);
+    check_qkv_out(k_out, "k_out");
+    check_qkv_out(v_out, "v_out");
+    a.out[1] = static_cast<uint16_t*>(k_out.data);
+    a.out_hs[1] = k_out.head_stride;
+    a.out_ss[1] = k_out.seq_stride;
+    a.out[2] = static_cast<uint16_t*>(v_out.data);
+    a.out_hs[2] = v_out.head_stride;
+    a.out_ss[2] = v_out.seq_stride;
+    launch_qkv_rope(desc->dtype, desc->head_dim, a, as_stream(stream));
+  });
+}
+
+int hcp_qkv_rope_project_paged(const hcp_qkv_desc* desc, const void* x, int64_t x_row_stride, const void* wq,
+                               const void* wk, const void* wv, const void* bq, const void* bk, const void* bv,
+                               const int64_t* positions, const float* rope_table, hcp_ring_view q_out,
+                               const hcp_paged_pool* pool, const int32_t* block_table, int64_t table_len,
+                               int64_t table_seq_offset, int64_t t0, void* stream) {
+  return guarded(__func__, [&] {
+    QkvArgs a = make_qkv(desc, x, x_row_stride, wq, wk, wv, bq, bk, bv, positions, rope_table, q_out);
+    check_pool(pool);
+    require(pool->elem_bytes == 2 && pool->num_kv_heads == desc->num_kv_heads && pool->head_dim == desc->head_dim,
+            "pool does not match the descriptor");
+    require(aligned(pool->data, 8), "pool must be 8-byte aligned");
+    require(block_table != nullptr && table_len >= 1, "null or empty block table");
+    require(t0 >= table_seq_offset, "t0 must be >= table_seq_offset");
+    a.pool = static_cast<uint16_t*>(pool->data);
+    a.plane_elems = pool->num_blocks * pool->block_size * static_cast<int64_t>(pool->num_kv_heads) * pool->head_dim;
+    a.num_blocks = pool->num_blocks;
+    a.bs = pool->block_size;
+    a.hkv = pool->num_kv_heads;
+    a.table = block_table;
+    a.table_len = table_len;
+    a.table_off = table_seq_offset;
+    a.t0 = t0;
+    launch_qkv_rope(desc->dtype, desc->head_dim, a, as_stream(stream));
+  });
+}
+
 size_t hcp_ring_replay_workspace_size(const hcp_ring_replay_desc* desc, int32_t paged) {
   try {
     return plan_replay(desc, paged != 0).total;

@@ -117,6 +117,34 @@ struct JVal {
 };
 JVal parse_frame_meta(const unsigned char* frame, size_t n, size_t* header_bytes);
 
+// Fused QKV projection + RoPE + KV append (qkv_rope.hip).
+struct QkvArgs {
+  const uint16_t* x;
+  int64_t x_ss;                 // elements between token rows
+  const uint16_t* w[3];         // q, k, v weights [out, hidden], rows contiguous
+  const uint16_t* bias[3];      // or null
+  int32_t nq, nkv;              // Hq * D, Hkv * D
+  int32_t hidden;
+  int32_t tokens;
+  int32_t rope;
+  const int64_t* pos;           // [tokens] global positions (RoPE rows)
+  const float* rope_cos;        // [rope_rows, D/2]
+  const float* rope_sin;
+  int64_t rope_rows;
+  uint16_t* out[3];             // views (k / v null when paged)
+  int64_t out_hs[3], out_ss[3];
+  uint16_t* pool;               // paged append of k / v
+  int64_t plane_elems, num_blocks;
+  int32_t bs, hkv;
+  const int32_t* table;
+  int64_t table_len, table_off, t0;
+  int* err;
+  int32_t n_tiles_n, n_tiles_m;
+};
+void launch_qkv_rope(int dtype, int d, QkvArgs& a, hipStream_t stream);
+// cos / sin tables [rows, d/2] of RotaryEmbedding (rotary.rs:64-97).
+void launch_rope_table(int d, int64_t rows, double base, float* cos, float* sin, hipStream_t stream);
+
 void launch_synth_normals(uint64_t seed, int64_t offset, int64_t count, int dtype, void* out,
                           hipStream_t stream);
 

@@ -83,7 +83,8 @@ int hcp_ring_device_count(int* count);
 /*
  * Reads and clears the sticky device-side error flags of the current device
  * (bit 0: a paged block id outside [0, num_blocks) was met and that row skipped;
- * bit 1: a list of key positions given to the positions mode was not non-decreasing).
+ * bit 1: a list of key positions given to the positions mode was not non-decreasing;
+ * bit 2: a RoPE position outside the cos / sin table).
  * Synchronises `stream`.
  */
 int hcp_ring_fetch_device_errors(void* stream, int* flags);
@@ -432,6 +433,58 @@ int hcp_packet_frame_pack(const hcp_packet_frame_desc* desc, hcp_ring_view q, co
                           const float* lse, void* payload, void* stream);
 int hcp_packet_frame_unpack(const hcp_packet_frame_desc* desc, const void* payload, hcp_ring_view q,
                             float* o, float* lse, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * (7) Fused QKV projection + RoPE + KV append (the head of HcpRingAttentionBackend::
+ * forward, ring.rs:1865-1936: q/k/v = x W^T + b, head split, RotaryEmbedding::apply at
+ * the tokens' global positions (rust/src/model/layers/rotary.rs:64-158), and the
+ * KV-cache append (KvCache::update, cache.rs:191-251; the positioned slab of
+ * self_driving.rs:180-228)).
+ *
+ * hcp_rope_table writes the reference's cos / sin caches for positions [0, rows):
+ * table[0 : rows*D/2] = cos(m * inv_freq[j]), table[rows*D/2 : rows*D] = sin(...),
+ * row-major [rows, D/2], with inv_freq[j] = (float)(1 / base^(2j/D)) and the angle
+ * formed in fp32 (rotary.rs:72-97).  DEVICE memory of rows*D floats.
+ *
+ * hcp_qkv_rope_project: x [tokens, hidden] (row stride x_row_stride elements), weights
+ * in the HF layout [out_features, hidden] (rows contiguous: wq [Hq*D, hidden], wk / wv
+ * [Hkv*D, hidden]), optional biases (NULL = none).  Outputs in the input dtype:
+ * q_out [Hq, tokens, D] and k_out / v_out [Hkv, tokens, D] as views, q and k rotated
+ * with positions[t] (DEVICE int64 [tokens]) when desc->rope is set (rotate_pairs:
+ * halves d and d + D/2).  Accumulation and the epilogue run in fp32 and round once.
+ * The _paged form appends k / v to the paged pool instead: token t goes to sequence
+ * position t0 + t through block_table (as hcp_paged_kv_scatter, without the tail
+ * fill); bad block ids set device error bit 0, positions outside the RoPE table bit 2.
+ * dtype BF16 or F16; head_dim 64 or 128; hidden a multiple of 32; Hq*D and Hkv*D
+ * multiples of 128; x, weights 16-byte aligned, x_row_stride a multiple of 8 and
+ * >= hidden; output views 8-byte aligned with strides multiple of 4.
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_qkv_desc {
+  int32_t dtype;
+  int32_t hidden;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t rope;          /* 1: rotate q and k */
+  int64_t tokens;
+  int64_t rope_rows;     /* rows of the cos / sin tables */
+} hcp_qkv_desc;
+
+int hcp_rope_table(int32_t head_dim, int64_t rows, double base, float* table, void* stream);
+
+int hcp_qkv_rope_project(const hcp_qkv_desc* desc, const void* x, int64_t x_row_stride,
+                         const void* wq, const void* wk, const void* wv, const void* bq,
+                         const void* bk, const void* bv, const int64_t* positions,
+                         const float* rope_table, hcp_ring_view q_out, hcp_ring_view k_out,
+                         hcp_ring_view v_out, void* stream);
+
+int hcp_qkv_rope_project_paged(const hcp_qkv_desc* desc, const void* x, int64_t x_row_stride,
+                               const void* wq, const void* wk, const void* wv, const void* bq,
+                               const void* bk, const void* bv, const int64_t* positions,
+                               const float* rope_table, hcp_ring_view q_out,
+                               const hcp_paged_pool* pool, const int32_t* block_table,
+                               int64_t table_len, int64_t table_seq_offset, int64_t t0,
+                               void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Replay kernel timing (no reference counterpart; benchmark instrumentation; the

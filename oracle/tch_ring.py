@@ -16,6 +16,8 @@ this module replays the same ATen op sequence through PyTorch's CPU backend:
 * :func:`decode_merge_packet`         ring.rs:647-663 (+ compact variant :525-536)
 * :func:`ring_decode_attention`       ring.rs:665-818 (the decode Q-ring, one packet's journey)
 * :func:`ring_attention`              ring.rs:861-1398 (tiling, order, early exit, output)
+* :func:`rope_caches`, :func:`rope_apply`  rust/src/model/layers/rotary.rs:56-158
+* :func:`qkv_rope_forward`            ring.rs:1865-1908 (projection, bias, head split, RoPE)
 * :func:`ring_attention_replay`       CS2 of the reference tests (ring.rs:3014-3165,
                                       3230-3364): every domain driven in one process,
                                       peers delivered by a mock transport
@@ -170,6 +172,53 @@ def decode_merge_compact_partial(scale, q, o, lse, k, v):
     num_rep = q.shape[1] // k.shape[1]
     return decode_merge_packet(scale, q, o, lse, repeat_kv_heads(k, num_rep),
                                repeat_kv_heads(v, num_rep))
+
+
+def rope_caches(dim: int, max_seq_len: int, base: float):
+    """RotaryEmbedding::new (rotary.rs:56-97): inv_freq[i] = 1 / base^(2i/dim) in f64
+    cast to f32; angles = positions (f32) x inv_freq (f32); cos / sin in f32."""
+    half = dim // 2
+    inv = torch.tensor([1.0 / base ** ((2.0 * i) / dim) for i in range(half)], dtype=torch.float32)
+    ang = torch.arange(max_seq_len, dtype=torch.float32).unsqueeze(1) * inv.unsqueeze(0)
+    return ang.cos(), ang.sin()
+
+
+def rope_apply(q, k, position_ids, cos_cache, sin_cache):
+    """RotaryEmbedding::apply + rotate_pairs (rotary.rs:103-158): halves (d, d + D/2)
+    rotated by the cached angle of each token's position, cos / sin cast to q's dtype."""
+    b, s = position_ids.shape
+    half = cos_cache.shape[1]
+    flat = position_ids.reshape(-1)
+    cos = cos_cache.index_select(0, flat).view(b, s, half).unsqueeze(1).to(q.dtype)
+    sin = sin_cache.index_select(0, flat).view(b, s, half).unsqueeze(1).to(q.dtype)
+
+    def rot(x):
+        x1, x2 = x[..., :half], x[..., half:]
+        return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=3)
+
+    return rot(q), rot(k)
+
+
+def qkv_rope_forward(x, wq, wk, wv, bq, bk, bv, num_heads: int, num_kv_heads: int, head_dim: int,
+                     position_ids, cos_cache, sin_cache, rope: bool = True):
+    """The head of forward (ring.rs:1865-1908): x [B, L, hidden] -> q [B, Hq, L, D],
+    k / v [B, Hkv, L, D] (projection, bias, head split, RoPE)."""
+    b, l, _ = x.shape
+    q = x.matmul(wq.transpose(0, 1))
+    if bq is not None:
+        q = q + bq
+    k = x.matmul(wk.transpose(0, 1))
+    if bk is not None:
+        k = k + bk
+    v = x.matmul(wv.transpose(0, 1))
+    if bv is not None:
+        v = v + bv
+    q = q.view(b, l, num_heads, head_dim).transpose(1, 2)
+    k = k.view(b, l, num_kv_heads, head_dim).transpose(1, 2)
+    v = v.view(b, l, num_kv_heads, head_dim).transpose(1, 2)
+    if rope:
+        q, k = rope_apply(q, k, position_ids, cos_cache, sin_cache)
+    return q, k, v
 
 
 def chunk_sizes(seq_len: int, num_domains: int, micro_override: int = 0):

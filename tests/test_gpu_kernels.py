@@ -607,3 +607,91 @@ def test_packet_frame_matches_oracle_and_round_trips(gpu):
     H.packet_frame_unpack(desc, payload, qo, oo, lo)
     torch.cuda.synchronize()
     assert torch.equal(qo, q) and torch.equal(oo, o) and torch.equal(lo, lse)
+
+
+def test_rope_table_matches_oracle(gpu):
+    for d, rows, base in ((128, 4096, 500000.0), (64, 131072, 10000.0)):
+        t = H.rope_table(d, rows, base)
+        torch.cuda.synchronize()
+        cos, sin = T.rope_caches(d, rows, base)
+        assert np.abs(t[0].cpu().numpy() - cos.numpy()).max() <= 2e-6, (d, rows)
+        assert np.abs(t[1].cpu().numpy() - sin.numpy()).max() <= 2e-6, (d, rows)
+
+
+QKV_CASES = [
+    # name, tokens, hidden, Hq, Hkv, D, dtype, bias, rope, positions
+    ("llama_like_bf16", 300, 512, 8, 2, 128, torch.bfloat16, False, True, "contiguous"),
+    ("qwen_like_bias_f16_d64", 200, 256, 14, 2, 64, torch.float16, True, True, "striped"),
+    ("no_rope_bf16", 64, 128, 4, 4, 128, torch.bfloat16, False, False, None),
+    ("many_stages_bias_bf16", 513, 1024, 8, 2, 128, torch.bfloat16, True, True, "offset"),
+]
+
+
+def _qkv_inputs(tokens, hidden, hq, hkv, d, dtype, bias, seed):
+    rng_parts = clib.draw_normals(seed, [(tokens, hidden), (hq * d, hidden), (hkv * d, hidden), (hkv * d, hidden),
+                                         ((hq + 2 * hkv) * d,)], "fp32")
+    x = torch.from_numpy(rng_parts[0]).to(dtype)
+    ws = [torch.from_numpy(w / math.sqrt(hidden)).to(dtype) for w in rng_parts[1:4]]
+    b = torch.from_numpy(rng_parts[4] * 0.5).to(dtype)
+    bs = [b[: hq * d], b[hq * d: (hq + hkv) * d], b[(hq + hkv) * d:]] if bias else [None] * 3
+    return x, ws, bs
+
+
+@pytest.mark.parametrize("case", QKV_CASES, ids=[c[0] for c in QKV_CASES])
+def test_qkv_rope_project_matches_closed_form(gpu, case):
+    name, tokens, hidden, hq, hkv, d, dtype, bias, rope, pat = case
+    x, ws, bs = _qkv_inputs(tokens, hidden, hq, hkv, d, dtype, bias, 200 + tokens)
+    if pat == "striped":
+        pos_np = np.array(_strategy_rows([tokens, tokens + 17], "striped")[0][0])
+    elif pat == "offset":
+        pos_np = np.arange(1000, 1000 + tokens)
+    else:
+        pos_np = np.arange(tokens)
+    rows = 4096
+    table = H.rope_table(d, rows, 10000.0)
+    pos = torch.from_numpy(pos_np.astype(np.int64)).cuda()
+    dev = lambda t: t.cuda() if t is not None else None
+    q, k, v = H.qkv_rope_project(dev(x), *(dev(w) for w in ws), hq, hkv, d, positions=pos, table=table,
+                                 bq=dev(bs[0]), bk=dev(bs[1]), bv=dev(bs[2]), rope=rope)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    # closed form in f64 on the stored inputs, rotated with the library's own table
+    x64 = x.double().numpy()
+    tab = table.cpu().double().numpy()
+    outs = []
+    for i, (w, b, heads) in enumerate(zip(ws, bs, (hq, hkv, hkv))):
+        y = x64 @ w.double().numpy().T + (b.double().numpy() if b is not None else 0.0)
+        y = y.reshape(tokens, heads, d).transpose(1, 0, 2)
+        if rope and i < 2:
+            c, s = tab[0][pos_np][None], tab[1][pos_np][None]
+            y1, y2 = y[..., : d // 2], y[..., d // 2:]
+            y = np.concatenate([y1 * c - y2 * s, y1 * s + y2 * c], axis=-1)
+        outs.append(y)
+    for got, ref in zip((q, k, v), outs):
+        g = got.double().cpu().numpy()
+        bound = np.abs(ref) / 128 + 1e-3 * np.abs(ref).max()
+        assert np.all(np.abs(g - ref) <= bound), (name, float(np.abs(g - ref).max()))
+    # the reference's own op sequence in fp32 (ring.rs:1865-1908, rotary.rs:103-158)
+    cos, sin = T.rope_caches(d, rows, 10000.0)
+    f32 = lambda t: t.float() if t is not None else None
+    tq, tk, tv = T.qkv_rope_forward(f32(x)[None], *(f32(w) for w in ws), *(f32(b) for b in bs), hq, hkv, d,
+                                    torch.from_numpy(pos_np.astype(np.int64))[None], cos, sin, rope=rope)
+    for got, ref in zip((q, k, v), (tq[0], tk[0], tv[0])):
+        assert (got.float().cpu() - ref).abs().max() <= 1e-2 * ref.abs().max() + 1e-3, name
+
+
+def test_qkv_rope_project_paged_append_matches_views(gpu):
+    tokens, hidden, hq, hkv, d, bs_ = 150, 256, 8, 2, 128, 16
+    x, ws, _ = _qkv_inputs(tokens, hidden, hq, hkv, d, torch.bfloat16, False, 310)
+    x, ws = x.cuda(), [w.cuda() for w in ws]
+    table = H.rope_table(d, 1024, 10000.0)
+    pos = torch.arange(37, 37 + tokens, dtype=torch.int64, device="cuda")
+    q1, k1, v1 = H.qkv_rope_project(x, *ws, hq, hkv, d, positions=pos, table=table)
+    nb = 24
+    pool = torch.zeros(2, nb, bs_, hkv, d, dtype=torch.bfloat16, device="cuda")
+    blocks = torch.from_numpy(I.permuted_block_table(311, nb)[:14].astype(np.int32)).cuda()
+    q2 = H.qkv_rope_project_paged(x, *ws, hq, hkv, d, pool, blocks, 16, 16 + 37, positions=pos, table=table)
+    k2, v2 = H.paged_kv_gather(pool, blocks, 16, 16 + 37, 16 + 37 + tokens)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)

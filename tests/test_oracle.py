@@ -439,3 +439,76 @@ def test_block_table_matches_contiguous():
     k, v = clib.paged_gather(pool, table, 0, 0, 77)
     np.testing.assert_array_equal(k, kv[0].transpose(1, 0, 2))
     np.testing.assert_array_equal(v, kv[1].transpose(1, 0, 2))
+
+
+# ------------------------------------------------------------------ QKV + RoPE ----
+def _rope_f64(x, pos, dim, base):
+    """Closed form: pair (d, d + D/2) rotated by pos * base^(-2d/D), all in f64."""
+    half = dim // 2
+    inv = 1.0 / base ** (2.0 * np.arange(half) / dim)
+    ang = pos[:, None] * inv[None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], axis=-1)
+
+
+def test_rope_oracle_matches_closed_form_and_invariants():
+    dim, base = 64, 10000.0
+    cos, sin = T.rope_caches(dim, 256, base)
+    pos = np.array([0, 1, 7, 100, 255])
+    q = _rand(50, (1, 2, 5, dim)).astype(np.float32)
+    k = _rand(51, (1, 1, 5, dim)).astype(np.float32)
+    rq, rk = T.rope_apply(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(pos)[None], cos, sin)
+    assert np.abs(rq.numpy() - _rope_f64(q.astype(np.float64), pos.astype(np.float64), dim, base)).max() < 1e-4
+    # position 0 is the identity; every (d, d + D/2) pair keeps its norm
+    assert np.array_equal(rq.numpy()[:, :, 0], q[:, :, 0])
+    h = dim // 2
+    n0 = q[..., :h] ** 2 + q[..., h:] ** 2
+    n1 = rq.numpy()[..., :h] ** 2 + rq.numpy()[..., h:] ** 2
+    assert np.abs(n0 - n1).max() < 1e-4
+
+
+def test_rope_scores_depend_on_relative_position_only():
+    dim = 128
+    cos, sin = T.rope_caches(dim, 512, 10000.0)
+    q = torch.from_numpy(_rand(52, (1, 1, 1, dim)).astype(np.float32))
+    k = torch.from_numpy(_rand(53, (1, 1, 1, dim)).astype(np.float32))
+    def score(m, n):
+        rq, _ = T.rope_apply(q, q, torch.tensor([[m]]), cos, sin)
+        rk, _ = T.rope_apply(k, k, torch.tensor([[n]]), cos, sin)
+        return float((rq * rk).sum())
+    assert abs(score(40, 10) - score(130, 100)) < 1e-3
+    assert abs(score(40, 10) - score(40, 11)) > 1e-3
+
+
+def test_rope_interleaved_pairing_is_caught():
+    # Planted mistake: rotate adjacent pairs (2i, 2i+1) instead of the halves.
+    dim = 32
+    x = _rand(54, (1, 1, 3, dim))
+    pos = np.array([3.0, 9.0, 20.0])
+    good = _rope_f64(x, pos, dim, 10000.0)
+    inv = 1.0 / 10000.0 ** (2.0 * np.arange(dim // 2) / dim)
+    ang = pos[:, None] * inv[None]
+    xe, xo = x[..., 0::2], x[..., 1::2]
+    bad = np.empty_like(x)
+    bad[..., 0::2] = xe * np.cos(ang) - xo * np.sin(ang)
+    bad[..., 1::2] = xe * np.sin(ang) + xo * np.cos(ang)
+    assert np.abs(good - bad).max() > 1e-2
+
+
+def test_qkv_forward_oracle_matches_closed_form():
+    l, hidden, hq, hkv, d = 5, 48, 4, 2, 16
+    x = _rand(55, (1, l, hidden))
+    wq, wk, wv = _rand(56, (hq * d, hidden)), _rand(57, (hkv * d, hidden)), _rand(58, (hkv * d, hidden))
+    bq, bk, bv = _rand(59, (hq * d,)), _rand(60, (hkv * d,)), _rand(61, (hkv * d,))
+    pos = np.array([4, 9, 10, 33, 60])
+    cos, sin = T.rope_caches(d, 64, 10000.0)
+    f = lambda a: torch.from_numpy(a.astype(np.float32))
+    q, k, v = T.qkv_rope_forward(f(x), f(wq), f(wk), f(wv), f(bq), f(bk), f(bv), hq, hkv, d,
+                                 torch.from_numpy(pos)[None], cos, sin)
+    rq = (x[0] @ wq.T + bq).reshape(l, hq, d).transpose(1, 0, 2)
+    rk = (x[0] @ wk.T + bk).reshape(l, hkv, d).transpose(1, 0, 2)
+    rv = (x[0] @ wv.T + bv).reshape(l, hkv, d).transpose(1, 0, 2)
+    assert np.abs(q[0].numpy() - _rope_f64(rq, pos.astype(np.float64), d, 10000.0)).max() < 1e-3
+    assert np.abs(k[0].numpy() - _rope_f64(rk, pos.astype(np.float64), d, 10000.0)).max() < 1e-3
+    assert np.abs(v[0].numpy() - rv).max() < 1e-4
