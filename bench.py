@@ -10,7 +10,8 @@ algorithmic FLOPs of causal pairs only: 2 GEMMs x 2 x D x Hq x S(S+1)/2.
 
 Also reported on the same line: paged decode GB/s (config c4), KV staging gather GB/s
 and the staged 128k prefill (config c5), the LSE merge GB/s, the c3 prefill with Striped
-and ZigZag positions, a roofline object for the
+and ZigZag positions, the KV wire-frame pack, the fused QKV + RoPE + KV append,
+a roofline object for the
 dominant kernel (the flash block kernel, from HIP events recorded by the replay
 driver on its launch stream over the timed region) and the CPU baseline (the oracle's
 op-for-op libtorch restatement of ring.rs timed on this host on a bounded sample).
@@ -230,6 +231,47 @@ def bench_wire(H, torch, tensors, steps: int, warmup: int):
             "unpack_gbs": round((wire // 4 + compact) / (t_unpack * 1e-3) / 1e9, 1),
             "unit": "GB/s", "pack_ms": round(t_pack, 4), "unpack_ms": round(t_unpack, 4),
             "payload_bytes": wire, "round_trip_bit_exact": ok}
+
+
+def bench_qkv(H, torch, steps: int, warmup: int):
+    """Fused QKV projection + RoPE + paged KV append for the Llama-3-8B layer shape
+    (hidden 4096, 32 q / 8 kv heads, D = 128) over one c3 domain chunk of 12288 tokens,
+    beside torch.matmul (the vendor GEMM) of the same concatenated projection alone."""
+    c = C3
+    tokens, hidden = c["chunks"][0], 4096
+    hq, hkv, d = c["hq"], c["hkv"], c["d"]
+    n_feat = (hq + 2 * hkv) * d
+    x = torch.empty(tokens, hidden, dtype=torch.bfloat16, device="cuda")
+    w = torch.empty(n_feat, hidden, dtype=torch.bfloat16, device="cuda")
+    H.synth_normals(47, 0, x.numel(), x)
+    H.synth_normals(47, x.numel(), w.numel(), w)
+    w.mul_(1.0 / math.sqrt(hidden))
+    wq, wk, wv = w[: hq * d], w[hq * d: (hq + hkv) * d], w[(hq + hkv) * d:]
+    table = H.rope_table(d, 32768, 500000.0)
+    pos = torch.arange(tokens, dtype=torch.int64, device="cuda")
+    bs = 16
+    nb = tokens // bs + 8
+    pool = torch.empty(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    blocks = torch.arange(tokens // bs, dtype=torch.int32, device="cuda")
+    q = torch.empty(hq, tokens, d, dtype=torch.bfloat16, device="cuda")
+    run = lambda: H.qkv_rope_project_paged(x, wq, wk, wv, hq, hkv, d, pool, blocks, 0, 0, positions=pos,
+                                           table=table, q_out=q)
+    for _ in range(warmup):
+        run()
+    log(f"qkv+rope timed x{steps}")
+    ms = time_cuda(torch, run, steps)
+    y = torch.empty(tokens, n_feat, dtype=torch.bfloat16, device="cuda")
+    gemm = lambda: torch.matmul(x, w.t(), out=y)
+    for _ in range(warmup):
+        gemm()
+    ms_gemm = time_cuda(torch, gemm, steps)
+    flops = 2.0 * tokens * hidden * n_feat
+    return {"workload": f"Llama-3-8B QKV: {tokens} tokens x hidden {hidden} -> {hq}q/{hkv}kv heads x {d}, "
+                        "bias-free, RoPE (theta 5e5), k/v appended to a bs=16 paged pool",
+            "value": round(flops / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s", "ms": round(ms, 4),
+            "frac_mfma": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "vendor_gemm_only_tflops": round(flops / (ms_gemm * 1e-3) / 1e12, 1),
+            "finite": bool(torch.isfinite(q.float()).all().item())}
 
 
 def bench_merge(H, torch, steps: int, warmup: int):
@@ -466,6 +508,8 @@ def main():
         strat = bench_strategies(H, torch, pre["tensors"], args.steps, args.warmup)
         wire = bench_wire(H, torch, pre["tensors"], args.steps, args.warmup)
         log(f"wire {wire}")
+        qkv = bench_qkv(H, torch, args.steps, args.warmup)
+        log(f"qkv {qkv}")
         log(f"c3 strategies {strat}")
         log(f"c3 lse merge {mrg['merge_gbs']:.1f} GB/s")
         log(f"c5 gather {stg['gather_gbs']:.1f} GB/s, prefill {stg.get('prefill_tflops', 0):.1f} TFLOP/s")
@@ -488,6 +532,7 @@ def main():
                        "frac_hbm": round(mrg["merge_gbs"] / PEAK_HBM_GBS, 4), "bytes": mrg["merge_bytes"]},
             strategies=dict(workload="c3 ring prefill with Striped / ZigZag positions (same causal FLOPs)", **strat),
             kv_frame=wire,
+            qkv_rope=qkv,
         )
     cpu = None
     if not args.no_cpu:
