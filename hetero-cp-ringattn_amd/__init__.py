@@ -28,7 +28,9 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libhcp_ring_amd.so")
+# HCP_RING_AMD_LIB selects another build of the library (e.g. one built with other
+# compile-time options); the default is the in-tree build.
+LIB_PATH = os.environ.get("HCP_RING_AMD_LIB") or os.path.join(HERE, "lib", "libhcp_ring_amd.so")
 HEADER = os.path.join(HERE, "..", "include", "hcp_ring.h")
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 1, 2, 3
