@@ -197,6 +197,14 @@ def lib() -> ctypes.CDLL:
                                   View, vp], ctypes.c_int),
         "hcp_qkv_rope_project_paged": ([ctypes.POINTER(QkvDesc), vp, i64, vp, vp, vp, vp, vp, vp, vp, vp, View,
                                         ctypes.POINTER(PagedPool), vp, i64, i64, i64, vp], ctypes.c_int),
+        "hcp_ringattn_runtime_create": ([ctypes.c_char_p, ctypes.POINTER(vp)], ctypes.c_int),
+        "hcp_ringattn_runtime_destroy": ([vp], None),
+        "hcp_ringattn_runtime_init": ([vp, i32, i32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(i64),
+                                       ctypes.POINTER(i64), ctypes.c_char_p, i64, i64, i64, i32], ctypes.c_int),
+        "hcp_ringattn_runtime_bind_layer": ([vp, i32, i32, View, View, View, f32, vp], ctypes.c_int),
+        "hcp_ringattn_runtime_run_layer": ([vp, i32, i64, vp, vp, vp, vp, vp, vp], ctypes.c_int),
+        "hcp_ringattn_runtime_shutdown": ([vp], ctypes.c_int),
+        "hcp_ringattn_cxx_smoke_domain_count": ([], ctypes.c_int),
         "hcp_synth_normals": ([ctypes.c_uint64, i64, i64, i32, vp, vp], ctypes.c_int),
         "hcp_ring_replay_timing": ([i32], ctypes.c_int),
         "hcp_ring_replay_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)],
@@ -699,6 +707,68 @@ def qkv_rope_project_paged(x, wq, wk, wv, num_q_heads, num_kv_heads, head_dim, p
                                             view(q_out), ctypes.byref(pp), _ptr(block_table), block_table.numel(),
                                             table_seq_offset, t0, _stream(stream)))
     return q_out
+
+
+# ---------------------------------------------------------------------------------
+# (8) domain runtime (RingAttnRuntime)
+# ---------------------------------------------------------------------------------
+class RingAttnRuntime:
+    """The reference's per-domain runtime (include/hcp_ringattn/core/ringattn_runtime.h)
+    on the GPU: Init / BindLayer / RunRingAttentionLayer / Shutdown."""
+
+    def __init__(self, device_type: str = "hip"):
+        h = ctypes.c_void_p()
+        _check(lib().hcp_ringattn_runtime_create(device_type.encode(), ctypes.byref(h)))
+        self._h = h
+        self._shape = None
+
+    def init(self, domain_index: int, domain_ids, seq_chunk_lens, num_heads: int, head_dim: int, dtype,
+             block_sizes=None, device: str = "hip", global_seq_len: int | None = None):
+        n = len(domain_ids)
+        ids = (ctypes.c_char_p * n)(*[d.encode() for d in domain_ids])
+        lens = (ctypes.c_int64 * n)(*seq_chunk_lens)
+        bss = (ctypes.c_int64 * n)(*(block_sizes or [16] * n))
+        total = sum(seq_chunk_lens) if global_seq_len is None else global_seq_len
+        code = dtype if isinstance(dtype, int) else dtype_code(dtype)
+        _check(lib().hcp_ringattn_runtime_init(self._h, domain_index, n, ids, lens, bss, device.encode(), total,
+                                               num_heads, head_dim, code))
+        self._shape = (num_heads, seq_chunk_lens[domain_index], head_dim)
+
+    def bind_layer(self, layer: int, q, k, v, scale: float | None = None, stream=None):
+        """q [Hq, L, D], k / v [Hkv, L, D] device views of this domain's chunk."""
+        sc = scale if scale is not None else 1.0 / math.sqrt(q.shape[2])
+        _check(lib().hcp_ringattn_runtime_bind_layer(self._h, layer, k.shape[0], view(q), view(k), view(v), sc,
+                                                     _stream(stream)))
+
+    def run_ring_attention_layer(self, layer: int, initial_state=None):
+        """-> (running_max [H, L], running_sum [H, L], output [H, L, D]) numpy fp32."""
+        import numpy as np
+        h, l, d = self._shape or (0, 0, 0)  # before Init the library reports the error
+        mx, sm, out = (np.empty((max(h, 1), max(l, 1)), np.float32), np.empty((max(h, 1), max(l, 1)), np.float32),
+                       np.empty((max(h, 1), max(l, 1), max(d, 1)), np.float32))
+        mx, sm, out = mx[:h, :l], sm[:h, :l], out[:h, :l, :d]
+        ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+        if initial_state is None:
+            args = (0, None, None, None)
+        else:
+            im, isum, io = (np.ascontiguousarray(a, dtype=np.float32) for a in initial_state)
+            args = (l, ptr(im), ptr(isum), ptr(io))
+        _check(lib().hcp_ringattn_runtime_run_layer(self._h, layer, *args, ptr(mx), ptr(sm), ptr(out)))
+        return mx, sm, out
+
+    def shutdown(self):
+        _check(lib().hcp_ringattn_runtime_shutdown(self._h))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.hcp_ringattn_runtime_destroy(h)
+            self._h = None
+
+
+def cxx_smoke_domain_count() -> int:
+    """The reference's three-domain runtime smoke (rust_bridge.cc:646-681) on "hip" runtimes."""
+    return lib().hcp_ringattn_cxx_smoke_domain_count()
 
 
 # ---------------------------------------------------------------------------------

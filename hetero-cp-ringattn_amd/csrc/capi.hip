@@ -13,6 +13,7 @@
 
 #include "kernels.hpp"
 #include "../../include/hcp_ring.h"
+#include "../../include/hcp_ringattn/core/ringattn_runtime.h"
 
 namespace hcp {
 
@@ -1062,6 +1063,151 @@ int hcp_qkv_rope_project_paged(const hcp_qkv_desc* desc, const void* x, int64_t 
     a.t0 = t0;
     launch_qkv_rope(desc->dtype, desc->head_dim, a, as_stream(stream));
   });
+}
+
+namespace {
+
+int status_code(const hcp_ringattn::Status& st, const char* fn) {
+  using C = hcp_ringattn::Status::Code;
+  if (st.ok()) return HCP_RING_OK;
+  const int code = st.code() == C::kInvalidArgument ? -6 : (st.code() == C::kUnimplemented ? -5 : -2);
+  return fail(code, std::string(fn) + ": " + st.message());
+}
+
+hcp_ringattn::TensorDType runtime_dtype(int32_t d) {
+  switch (d) {
+    case kF16: return hcp_ringattn::TensorDType::kFloat16;
+    case kBF16: return hcp_ringattn::TensorDType::kBFloat16;
+    case kF32: return hcp_ringattn::TensorDType::kFloat32;
+    default: return hcp_ringattn::TensorDType::kUnknown;
+  }
+}
+
+hcp_ringattn::BoundaryTensor host_f32(const char* name, std::vector<int64_t> shape, const float* data, size_t n) {
+  hcp_ringattn::BoundaryTensor t;
+  t.name = name;
+  t.dtype = hcp_ringattn::TensorDType::kFloat32;
+  t.shape = std::move(shape);
+  t.payload.resize(n * 4);
+  std::memcpy(t.payload.data(), data, n * 4);
+  return t;
+}
+
+}  // namespace
+
+struct hcp_ringattn_runtime {
+  std::unique_ptr<hcp_ringattn::RingAttnRuntime> impl;
+  int64_t num_heads = 0, head_dim = 0, len = 0;
+};
+
+int hcp_ringattn_runtime_create(const char* device_type, hcp_ringattn_runtime** out) {
+  return guarded(__func__, [&] {
+    require(device_type != nullptr && out != nullptr, "null argument");
+    auto* rt = new hcp_ringattn_runtime;
+    rt->impl = hcp_ringattn::CreateRingAttnRuntime(device_type);
+    *out = rt;
+  });
+}
+
+void hcp_ringattn_runtime_destroy(hcp_ringattn_runtime* rt) { delete rt; }
+
+int hcp_ringattn_runtime_init(hcp_ringattn_runtime* rt, int32_t domain_index, int32_t num_domains,
+                              const char* const* domain_ids, const int64_t* seq_chunk_lens,
+                              const int64_t* block_sizes, const char* device, int64_t global_seq_len,
+                              int64_t num_heads, int64_t head_dim, int32_t dtype) {
+  g_last_error.clear();
+  if (rt == nullptr || domain_ids == nullptr || seq_chunk_lens == nullptr || block_sizes == nullptr ||
+      device == nullptr || num_domains <= 0 || domain_index < 0 || domain_index >= num_domains)
+    return fail(-6, std::string(__func__) + ": null argument or domain_index out of range");
+  hcp_ringattn::RingAttnConfig g;
+  g.global_seq_len = global_seq_len;
+  g.num_heads = num_heads;
+  g.head_dim = head_dim;
+  g.dtype = runtime_dtype(dtype);
+  for (int i = 0; i < num_domains; ++i) {
+    if (domain_ids[i] == nullptr) return fail(-6, std::string(__func__) + ": null domain id");
+    g.domains.push_back({domain_ids[i], "", 0, seq_chunk_lens[i], block_sizes[i], device});
+  }
+  const int rc = status_code(rt->impl->Init(g.domains[domain_index], g), __func__);
+  if (rc == 0) {
+    rt->num_heads = num_heads;
+    rt->head_dim = head_dim;
+    rt->len = seq_chunk_lens[domain_index];
+  }
+  return rc;
+}
+
+int hcp_ringattn_runtime_bind_layer(hcp_ringattn_runtime* rt, int32_t layer_index, int32_t num_kv_heads,
+                                    hcp_ring_view q, hcp_ring_view k, hcp_ring_view v, float scale, void* stream) {
+  g_last_error.clear();
+  if (rt == nullptr) return fail(-6, std::string(__func__) + ": null runtime");
+  auto* hip = dynamic_cast<hcp_ringattn::HipRingAttnRuntime*>(rt->impl.get());
+  if (hip == nullptr) return fail(-5, std::string(__func__) + ": runtime cannot bind device inputs");
+  return status_code(hip->BindLayer(layer_index, num_kv_heads, q, k, v, scale, stream), __func__);
+}
+
+int hcp_ringattn_runtime_run_layer(hcp_ringattn_runtime* rt, int32_t layer_index, int64_t in_seq_len,
+                                   const float* in_max, const float* in_sum, const float* in_output,
+                                   float* out_max, float* out_sum, float* out_output) {
+  g_last_error.clear();
+  if (rt == nullptr || out_max == nullptr || out_sum == nullptr || out_output == nullptr)
+    return fail(-6, std::string(__func__) + ": null runtime or output array");
+  const int64_t h = rt->num_heads, d = rt->head_dim, l = rt->len;
+  const size_t rows = static_cast<size_t>(h) * l;
+  hcp_ringattn::RingAttnSoftmaxState in, out;
+  if (in_seq_len > 0) {
+    if (in_seq_len != l || in_max == nullptr || in_sum == nullptr || in_output == nullptr)
+      return fail(-6, std::string(__func__) + ": initial state must cover the domain's chunk");
+    in.seq_len = l;
+    in.num_heads = h;
+    in.head_dim = d;
+    in.running_max = host_f32("running_max", {h, l}, in_max, rows);
+    in.running_sum = host_f32("running_sum", {h, l}, in_sum, rows);
+    in.output = host_f32("output", {h, l, d}, in_output, rows * d);
+  }
+  const int rc = status_code(rt->impl->RunRingAttentionLayer(layer_index, in, &out), __func__);
+  if (rc != 0) return rc;
+  if (out.seq_len == 0) {  // nothing bound and no initial state: an empty state
+    for (size_t i = 0; i < rows; ++i) out_max[i] = -INFINITY, out_sum[i] = 0.f;
+    std::memset(out_output, 0, rows * d * 4);
+    return 0;
+  }
+  std::memcpy(out_max, out.running_max.payload.data(), rows * 4);
+  std::memcpy(out_sum, out.running_sum.payload.data(), rows * 4);
+  std::memcpy(out_output, out.output.payload.data(), rows * d * 4);
+  return 0;
+}
+
+int hcp_ringattn_runtime_shutdown(hcp_ringattn_runtime* rt) {
+  g_last_error.clear();
+  if (rt == nullptr) return fail(-6, std::string(__func__) + ": null runtime");
+  return status_code(rt->impl->Shutdown(), __func__);
+}
+
+int hcp_ringattn_cxx_smoke_domain_count(void) {
+  try {
+    hcp_ringattn::RingAttnConfig g;
+    g.global_seq_len = 1024;
+    g.num_heads = 8;
+    g.head_dim = 64;
+    g.domains = {{"domain-0", "127.0.0.1", 26001, 512, 128, "hip"},
+                 {"domain-1", "127.0.0.1", 26002, 256, 64, "hip"},
+                 {"domain-2", "127.0.0.1", 26003, 256, 64, "hip"}};
+    int ok = 0;
+    for (const auto& dom : g.domains) {
+      auto rt = hcp_ringattn::CreateRingAttnRuntime(dom.device);
+      hcp_ringattn::RingAttnSoftmaxState init_state, out_state;
+      if (!rt->Init(dom, g).ok()) return -1;
+      if (!rt->RunRingAttentionLayer(0, init_state, &out_state).ok()) return -2;
+      if (!rt->Shutdown().ok()) return -3;
+      ++ok;
+    }
+    return ok;
+  } catch (const std::exception&) {
+    return -10;
+  } catch (...) {
+    return -11;
+  }
 }
 
 size_t hcp_ring_replay_workspace_size(const hcp_ring_replay_desc* desc, int32_t paged) {

@@ -487,6 +487,40 @@ int hcp_qkv_rope_project_paged(const hcp_qkv_desc* desc, const void* x, int64_t 
                                void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * (8) Domain runtime (RingAttnRuntime, the reference's include/hcp_ringattn/core/
+ * ringattn_runtime.h:10-29 and its smoke, src/rust_bridge.cc:646-681) through plain C.
+ *
+ * The C++ interface is include/hcp_ringattn/core/ringattn_runtime.h
+ * (hcp_ringattn::CreateRingAttnRuntime); these entries wrap it for FFI callers.
+ * init: this runtime is domain `domain_index` of num_domains domains, with their ids
+ * and seq_chunk_lens / block_sizes in ring order, global_seq_len = the sum of the
+ * chunk lengths, num_heads / head_dim / dtype (HCP_DTYPE_*) of the layer, device
+ * "hip".  bind_layer: the domain's q [Hq, L, D], k / v [Hkv, L, D] device views for a
+ * layer.  run_layer: HOST fp32 arrays, initial state (in_seq_len = 0 for none) and the
+ * resulting state: max [Hq, L] (= LSE), sum [Hq, L] (= 1), output [Hq, L, D].
+ * Status: 0 ok, -6 invalid argument, -5 unimplemented, -2 internal.
+ * hcp_ringattn_cxx_smoke_domain_count runs the reference's three-domain
+ * Init / Run / Shutdown smoke on "hip" runtimes: returns 3, or -1 / -2 / -3 when Init /
+ * Run / Shutdown fails and -10 / -11 on an exception (the reference's codes).
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_ringattn_runtime hcp_ringattn_runtime;
+
+int hcp_ringattn_runtime_create(const char* device_type, hcp_ringattn_runtime** out);
+void hcp_ringattn_runtime_destroy(hcp_ringattn_runtime* rt);
+int hcp_ringattn_runtime_init(hcp_ringattn_runtime* rt, int32_t domain_index, int32_t num_domains,
+                              const char* const* domain_ids, const int64_t* seq_chunk_lens,
+                              const int64_t* block_sizes, const char* device, int64_t global_seq_len,
+                              int64_t num_heads, int64_t head_dim, int32_t dtype);
+int hcp_ringattn_runtime_bind_layer(hcp_ringattn_runtime* rt, int32_t layer_index, int32_t num_kv_heads,
+                                    hcp_ring_view q, hcp_ring_view k, hcp_ring_view v, float scale,
+                                    void* stream);
+int hcp_ringattn_runtime_run_layer(hcp_ringattn_runtime* rt, int32_t layer_index, int64_t in_seq_len,
+                                   const float* in_max, const float* in_sum, const float* in_output,
+                                   float* out_max, float* out_sum, float* out_output);
+int hcp_ringattn_runtime_shutdown(hcp_ringattn_runtime* rt);
+int hcp_ringattn_cxx_smoke_domain_count(void);
+
+/* ---------------------------------------------------------------------------------
  * Replay kernel timing (no reference counterpart; benchmark instrumentation; the
  * reference logs wall-clock compute per phase to HCP_PERF_LOG, ring.rs:820-844).
  *

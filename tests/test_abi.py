@@ -101,3 +101,33 @@ def test_strategy_helpers_reject_bad_arguments():
         H.build_assignment([3, 1], 7)
     with pytest.raises(H.HcpRingError):
         H.build_assignment([3, -1], "striped")
+
+
+def test_runtime_smoke_and_init_validation():
+    # The reference's Init checks (src/ringattn_runtime.cc:17-37) and its three-domain
+    # Init / Run / Shutdown smoke (rust_bridge.cc:646-681); no GPU work is involved.
+    assert H.cxx_smoke_domain_count() == 3
+    ids, lens = ["d0", "d1"], [6, 4]
+    rt = H.RingAttnRuntime("hip")
+    with pytest.raises(H.HcpRingError):          # chunk lengths must sum to the sequence
+        rt.init(0, ids, lens, 2, 8, torch.float32, global_seq_len=11)
+    with pytest.raises(H.HcpRingError):
+        rt.init(0, ["", "d1"], lens, 2, 8, torch.float32)
+    with pytest.raises(H.HcpRingError):
+        rt.init(0, ids, lens, 2, 8, torch.float32, block_sizes=[0, 16])
+    with pytest.raises(H.HcpRingError):
+        rt.init(0, ids, lens, 0, 8, torch.float32)
+    with pytest.raises(H.HcpRingError):          # no CPU path in this library
+        rt.init(0, ids, lens, 2, 8, torch.float32, device="cpu")
+    with pytest.raises(H.HcpRingError):          # run before a successful Init
+        H.RingAttnRuntime("hip").run_ring_attention_layer(0)
+    rt.init(1, ids, lens, 2, 8, torch.float32)
+    mx, sm, out = rt.run_ring_attention_layer(0)  # nothing bound: the empty state passes through
+    assert np.isneginf(mx).all() and (sm == 0).all() and (out == 0).all()
+    state = (np.full((2, 4), 0.5, np.float32), np.full((2, 4), 2.0, np.float32), np.ones((2, 4, 8), np.float32))
+    mx, sm, out = rt.run_ring_attention_layer(0, state)
+    assert np.array_equal(mx, state[0]) and np.array_equal(sm, state[1]) and np.array_equal(out, state[2])
+    rt.shutdown()
+    bad = H.RingAttnRuntime("cpu")
+    with pytest.raises(H.HcpRingError):
+        bad.init(0, ids, lens, 2, 8, torch.float32)

@@ -695,3 +695,46 @@ def test_qkv_rope_project_paged_append_matches_views(gpu):
     torch.cuda.synchronize()
     assert H.fetch_device_errors() == 0
     assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
+@pytest.mark.parametrize("dtype,chunks,hq,hkv,d", [(torch.float32, [40, 24, 36], 4, 2, 64),
+                                                   (torch.bfloat16, [128, 96, 200], 8, 2, 128)])
+def test_ring_runtime_domains_match_full_attention(gpu, dtype, chunks, hq, hkv, d):
+    # One HipRingAttnRuntime per domain (the reference's RingAttnRuntime contract):
+    # each binds its chunk, runs its ring, and returns its rows of causal attention.
+    s = sum(chunks)
+    (q, k, v), (q32, k32, v32) = draw(170 + d, [(s, hq, d), (s, hkv, d), (s, hkv, d)], dtype)
+    ids = [f"domain-{i}" for i in range(len(chunks))]
+    offs = np.concatenate([[0], np.cumsum(chunks)])
+    rts = []
+    for i in range(len(chunks)):
+        rt = H.RingAttnRuntime("hip")
+        rt.init(i, ids, chunks, hq, d, dtype)
+        a, b = offs[i], offs[i + 1]
+        rt.bind_layer(3, q[a:b].permute(1, 0, 2), k[a:b].permute(1, 0, 2), v[a:b].permute(1, 0, 2))
+        rts.append(rt)
+    p = np.arange(s)
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, p, p, 1 / math.sqrt(d))
+    tol_o = 1e-4 if dtype == torch.float32 else OUT_TOL
+    tol_l = 1e-4 if dtype == torch.float32 else LSE_TOL
+    for i, rt in enumerate(rts):
+        mx, sm, out = rt.run_ring_attention_layer(3)
+        a, b = offs[i], offs[i + 1]
+        assert np.all(sm == 1.0)
+        assert np.abs(out - ref_o[a:b].transpose(1, 0, 2)).max() <= tol_o, i
+        assert np.abs(mx - ref_l[a:b].T).max() <= tol_l, i
+    # an initial state is merged in first: extra keys at positions before the sequence
+    e = 8
+    (ek, ev), (ek32, ev32) = draw(180 + d, [(e, hkv, d), (e, hkv, d)], dtype)
+    i = 1
+    a, b = offs[i], offs[i + 1]
+    eo, el = C.attention_f64(q32[a:b], ek32, ev32, np.arange(a, b), np.arange(-e, 0), 1 / math.sqrt(d))
+    init = (el.T.astype(np.float32) - 1.0, np.full(el.T.shape, math.e, np.float32),
+            eo.transpose(1, 0, 2).astype(np.float32))             # m + ln(l) = lse
+    mx, sm, out = rts[i].run_ring_attention_layer(3, init)
+    kk, vv = np.concatenate([ek32, k32]), np.concatenate([ev32, v32])
+    ro, rl = C.attention_f64(q32[a:b], kk, vv, np.arange(a, b), np.concatenate([np.arange(-e, 0), p]), 1 / math.sqrt(d))
+    assert np.abs(out - ro.transpose(1, 0, 2)).max() <= tol_o
+    assert np.abs(mx - rl.T).max() <= tol_l
+    for rt in rts:
+        rt.shutdown()
