@@ -1,0 +1,130 @@
+"""Parity at the full BASELINE sizes (c3 32k ring prefill, c4 paged decode, c5 128k
+staging), through properties that do not need the whole closed form: sampled query rows
+against the f64 closed form, order invariance between strategies, bit-exactness against
+an independent GPU gather (torch advanced indexing) and scatter/gather round trips.
+Inputs come from the device LCG generator with the bench's seeds."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import hcp_ring_amd as H
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 2e-2
+LSE_TOL = 1e-3
+
+
+def synth(seed, shapes):
+    out, off = [], 0
+    for shp in shapes:
+        t = torch.empty(*shp, dtype=torch.bfloat16, device="cuda")
+        H.synth_normals(seed, off, t.numel(), t)
+        off += t.numel()
+        out.append(t)
+    return out
+
+
+def rows_closed_form(q32, k32, v32, rows, scale, key_end):
+    """f64 attention of query rows `rows` (q32 [S, Hq, D]) over keys [0, key_end(r))."""
+    hq, hkv = q32.shape[1], k32.shape[1]
+    rep = hq // hkv
+    o = np.zeros((len(rows), hq, q32.shape[2]))
+    lse = np.zeros((len(rows), hq))
+    for i, r in enumerate(rows):
+        e = key_end(r)
+        for g in range(hkv):
+            qg = q32[r, g * rep:(g + 1) * rep].astype(np.float64)          # [rep, D]
+            kg = k32[:e, g].astype(np.float64)                              # [e, D]
+            s = qg @ kg.T * scale
+            m = s.max(axis=1, keepdims=True)
+            w = np.exp(s - m)
+            den = w.sum(axis=1, keepdims=True)
+            o[i, g * rep:(g + 1) * rep] = (w @ v32[:e, g].astype(np.float64)) / den
+            lse[i, g * rep:(g + 1) * rep] = (m + np.log(den))[:, 0]
+    return o, lse
+
+
+def test_c3_full_ring_prefill_sampled_rows_and_strategy_invariance(gpu):
+    chunks, hq, hkv, d = [12288, 8192, 8192, 4096], 32, 8, 128
+    s = sum(chunks)
+    q, k, v = synth(44, [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    out, lse = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    rows = [0, 1, 777, 12287, 12288, 20479, 20480, 28671, 28672, 31000, 32767]
+    q32, k32, v32 = (x.float().cpu().numpy() for x in (q, k, v))
+    ref_o, ref_l = rows_closed_form(q32, k32, v32, rows, 1 / math.sqrt(d), lambda r: r + 1)
+    got_o = out.float().cpu().numpy()[:, rows].transpose(1, 0, 2)
+    got_l = lse.cpu().numpy()[:, rows].T
+    assert np.abs(got_o - ref_o).max() <= OUT_TOL
+    assert np.abs(got_l - ref_l).max() <= LSE_TOL
+    # the same sequence under ZigZag positions (rows in domain-major order) agrees
+    from oracle import strategy as SP
+    a = SP.build_assignment(chunks, "zigzag")
+    order = torch.tensor(sum(SP.build_domain_positions(a), []), device="cuda")
+    inv = torch.tensor(SP.build_inverse_perm(a), device="cuda")
+    qz, kz, vz = (x.index_select(0, order).permute(1, 0, 2) for x in (q, k, v))
+    oz, lz = H.ring_attention_replay(qz, kz, vz, chunks, strategy="zigzag")
+    oz, lz = oz.index_select(1, inv), lz.index_select(1, inv)
+    torch.cuda.synchronize()
+    assert (oz.float() - out.float()).abs().max().item() <= 2 * OUT_TOL
+    assert (lz - lse).abs().max().item() <= 2 * LSE_TOL
+
+
+def test_c4_full_paged_decode_sampled_sequences(gpu):
+    batch, hq, hkv, d, bs, ctx, nb = 64, 32, 8, 128, 16, 16384, 65536
+    chunks = [8192, 5120, 3072]
+    q = torch.empty(batch, hq, d, dtype=torch.bfloat16, device="cuda")
+    pool = torch.empty(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.synth_normals(45, 0, q.numel(), q)
+    H.synth_normals(45, q.numel(), pool.numel(), pool)
+    rng = np.random.default_rng(45)
+    tables_np = rng.permutation(nb)[: batch * (ctx // bs)].astype(np.int32).reshape(batch, ctx // bs)
+    tables = torch.from_numpy(tables_np).cuda()
+    parts, t0 = [], 0
+    for L in chunks:
+        parts.append(H.decode_local_compact_partial(q, pool, tables, t0, t0 + L))
+        t0 += L
+    out, lse = H.lse_merge([o.view(-1, 1, d) for o, _ in parts], [l.view(-1, 1) for _, l in parts],
+                           out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    out = out.view(batch, hq, d).float().cpu().numpy()
+    lse = lse.view(batch, hq).cpu().numpy()
+    for b in (0, 31, 63):
+        blocks = torch.from_numpy(tables_np[b].astype(np.int64)).cuda()
+        k = pool[0].index_select(0, blocks).reshape(ctx, hkv, d).float().cpu().numpy()
+        v = pool[1].index_select(0, blocks).reshape(ctx, hkv, d).float().cpu().numpy()
+        ro, rl = rows_closed_form(q[b:b + 1].float().cpu().numpy(), k, v, [0], 1 / math.sqrt(d), lambda r: ctx)
+        assert np.abs(out[b] - ro[0]).max() <= OUT_TOL, b
+        assert np.abs(lse[b] - rl[0]).max() <= LSE_TOL, b
+
+
+def test_c5_full_staging_bit_exact_against_torch_indexing(gpu):
+    chunks = [21504, 13312, 18432, 23552, 24576, 9216, 8192, 12288]
+    hkv, d, bs = 8, 128, 16
+    s = sum(chunks)
+    k, v = synth(46, [(s, hkv, d), (s, hkv, d)])
+    nb = s // bs
+    perm = torch.from_numpy(np.random.default_rng(46).permutation(nb).astype(np.int32)).cuda()
+    pool = torch.zeros(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.paged_kv_scatter(pool, perm, 0, 0, s, k.permute(1, 0, 2), v.permute(1, 0, 2))
+    # independent placement check: pool[plane, perm[t // bs], t % bs] == source token t
+    t = torch.arange(s, device="cuda")
+    blk, slot = perm.long()[t // bs], t % bs
+    assert torch.equal(pool[0][blk, slot].view(torch.int16), k.view(torch.int16))
+    assert torch.equal(pool[1][blk, slot].view(torch.int16), v.view(torch.int16))
+    ranges, off = [], 0
+    for L in chunks:
+        ko = torch.empty(hkv, L, d, dtype=torch.bfloat16, device="cuda")
+        ranges.append((perm, 0, off, off + L, ko, torch.empty_like(ko)))
+        off += L
+    H.paged_kv_gather_batch(pool, ranges)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    for (_, _, a, b, ko, vo) in ranges:
+        assert torch.equal(ko.view(torch.int16), k[a:b].permute(1, 0, 2).view(torch.int16))
+        assert torch.equal(vo.view(torch.int16), v[a:b].permute(1, 0, 2).view(torch.int16))
