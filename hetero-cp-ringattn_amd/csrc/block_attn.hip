@@ -143,11 +143,12 @@ struct RowLimits {
   int n_kv;
   int64_t lane, wave_first, wave_last;
 };
+template <bool POS>
 __device__ __forceinline__ RowLimits row_limits(const BlockArgs& a, int q_end, int wq0, int my_q, int wave,
                                                 int lane, int* red) {
   RowLimits r;
   r.n_kv = a.lk;
-  if (a.q_lim == nullptr) {
+  if constexpr (!POS) {
     r.lane = a.q_off + my_q - a.k_off;
     r.wave_first = a.q_off + wq0 - a.k_off;
     r.wave_last = a.q_off + min(wq0 + 31, a.lq - 1) - a.k_off;
@@ -245,7 +246,7 @@ __device__ __forceinline__ void write_row(const BlockArgs& a, int head, int my_q
   }
 }
 
-template <int D, int DT, int G>
+template <int D, int DT, int G, bool POS>
 __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
@@ -285,7 +286,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 
   // Keys visible to some row of this workgroup.
   __shared__ int lim_red[kWaves];
-  const RowLimits rl = row_limits(a, q_end, wq0, my_q, wave, lane, lim_red);
+  const RowLimits rl = row_limits<POS>(a, q_end, wq0, my_q, wave, lane, lim_red);
   const int n_kv = rl.n_kv;
   const int n_tiles = (n_kv + kBK - 1) / kBK;
 
@@ -505,7 +506,7 @@ constexpr int kD3 = 128;
 constexpr int kTile3 = kBK * kD3 * 2;  // bytes of one K or V tile (16 KiB)
 
 
-template <int DT, int G>
+template <int DT, int G, bool POS>
 __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs a) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
@@ -537,7 +538,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
   const int q_end = min(a.lq, tq0 + TQ);
 
   __shared__ int lim_red[kWaves];
-  const RowLimits rl = row_limits(a, q_end, wq0, my_q, wave, lane, lim_red);
+  const RowLimits rl = row_limits<POS>(a, q_end, wq0, my_q, wave, lane, lim_red);
   const int n_kv = rl.n_kv;
   const int n_tiles = (n_kv + kBK - 1) / kBK;
 
@@ -872,19 +873,37 @@ static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   a.n_groups = L.hq / g;
   const dim3 grid(static_cast<unsigned>(a.n_qtiles * a.n_groups));
   if (D == kD3) {
-    switch (g) {
-      case 8: flash_block_dma_kernel<DT, 8><<<grid, kThreads, 0, stream>>>(a); break;
-      case 4: flash_block_dma_kernel<DT, 4><<<grid, kThreads, 0, stream>>>(a); break;
-      case 2: flash_block_dma_kernel<DT, 2><<<grid, kThreads, 0, stream>>>(a); break;
-      default: flash_block_dma_kernel<DT, 1><<<grid, kThreads, 0, stream>>>(a); break;
+    if (a.q_lim != nullptr) {
+      switch (g) {
+        case 8: flash_block_dma_kernel<DT, 8, true><<<grid, kThreads, 0, stream>>>(a); break;
+        case 4: flash_block_dma_kernel<DT, 4, true><<<grid, kThreads, 0, stream>>>(a); break;
+        case 2: flash_block_dma_kernel<DT, 2, true><<<grid, kThreads, 0, stream>>>(a); break;
+        default: flash_block_dma_kernel<DT, 1, true><<<grid, kThreads, 0, stream>>>(a); break;
+      }
+    } else {
+      switch (g) {
+        case 8: flash_block_dma_kernel<DT, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
+        case 4: flash_block_dma_kernel<DT, 4, false><<<grid, kThreads, 0, stream>>>(a); break;
+        case 2: flash_block_dma_kernel<DT, 2, false><<<grid, kThreads, 0, stream>>>(a); break;
+        default: flash_block_dma_kernel<DT, 1, false><<<grid, kThreads, 0, stream>>>(a); break;
+      }
     }
     return;
   }
-  switch (g) {
-    case 8: flash_block_kernel<D, DT, 8><<<grid, kThreads, 0, stream>>>(a); break;
-    case 4: flash_block_kernel<D, DT, 4><<<grid, kThreads, 0, stream>>>(a); break;
-    case 2: flash_block_kernel<D, DT, 2><<<grid, kThreads, 0, stream>>>(a); break;
-    default: flash_block_kernel<D, DT, 1><<<grid, kThreads, 0, stream>>>(a); break;
+  if (a.q_lim != nullptr) {
+    switch (g) {
+      case 8: flash_block_kernel<D, DT, 8, true><<<grid, kThreads, 0, stream>>>(a); break;
+      case 4: flash_block_kernel<D, DT, 4, true><<<grid, kThreads, 0, stream>>>(a); break;
+      case 2: flash_block_kernel<D, DT, 2, true><<<grid, kThreads, 0, stream>>>(a); break;
+      default: flash_block_kernel<D, DT, 1, true><<<grid, kThreads, 0, stream>>>(a); break;
+    }
+  } else {
+    switch (g) {
+      case 8: flash_block_kernel<D, DT, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
+      case 4: flash_block_kernel<D, DT, 4, false><<<grid, kThreads, 0, stream>>>(a); break;
+      case 2: flash_block_kernel<D, DT, 2, false><<<grid, kThreads, 0, stream>>>(a); break;
+      default: flash_block_kernel<D, DT, 1, false><<<grid, kThreads, 0, stream>>>(a); break;
+    }
   }
 }
 
