@@ -20,8 +20,10 @@
 //   * Online softmax in the log2 domain with the scale folded in; the running max is
 //     only moved (and O rescaled) when a row's max grows by more than 8 (2^8 bound on
 //     P), which keeps the result exact and skips most rescales.
-//   * K/V tiles of 64 keys are double-buffered in LDS; global loads of tile t+1 are in
-//     flight while tile t is computed.  One barrier per tile.
+//   * K/V tiles of 64 keys.  head_dim 64: double-buffered in LDS, register-staged
+//     global loads of tile t+1 in flight while tile t is computed, one barrier per
+//     tile.  head_dim 128 (flash_block_pingpong_kernel): asynchronous global->LDS
+//     loads and two wave groups that alternate MFMA and softmax phases.
 //   * Causal: tiles wholly in a wave's future are skipped, tiles wholly visible are
 //     unmasked, only tiles straddling the diagonal (or the kv tail) are masked.  The
 //     visible keys of a row are a prefix of the chunk: j <= q_off + i - k_off for
@@ -482,32 +484,58 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 }
 
 // ----------------------------------------------------------------------------------
-// Head-dim-128 kernel with asynchronous global->LDS loads.
+// Head-dim-128 kernel: asynchronous global->LDS tiles, two wave groups in ping-pong.
 //
 // Same wave layout and math as flash_block_kernel (8 waves, one query head and 32
 // query tokens per wave, S^T = K Q^T with K rows in kperm order, P^T straight from the
-// S^T accumulators), but the K and V tiles reach LDS without passing through
-// registers:
-//   * buffer_load_dwordx4 ... lds writes 1 KiB per wave instruction (4 rows of 64 keys
-//     x 128 dims); three tiles in flight (triple-buffered LDS, loads of tile t+2 issued
-//     while tile t is computed), so there are no staging registers, no VALU transpose
-//     and no LDS stores on the compute waves' path.
-//   * For LDS chunk p of row r the DMA fetches global chunk p ^ swz(r): K rows use
-//     swz = r & 15, V rows 4 * (r & 3), which makes the fragment reads below
-//     bank-conflict free.
-//   * K fragments (A of S^T) are ds_read_b128; V^T fragments (A of O^T = V^T P^T) come
-//     from row-major V through ds_read_b64_tr_b16: two reads give one lane the 8 keys
-//     of its head-dim column.
-//   * The loop is unrolled by the buffer count so each LDS address is a per-lane
-//     register set up once plus an immediate offset.
+// S^T accumulators), with two changes:
+//
+// Tiles.  The K and V tiles of 64 keys reach LDS without passing through registers:
+// buffer_load_dwordx4 ... lds writes 1 KiB per wave instruction (4 rows of 64 keys x
+// 128 dims).  For LDS chunk p of row r the DMA fetches global chunk p ^ swz(r): K rows
+// use swz = r & 15, V rows 4 * (r & 3), which makes the fragment reads bank-conflict
+// free.  K fragments (A of S^T) are ds_read_b128; V^T fragments (A of O^T = V^T P^T)
+// come from row-major V through ds_read_b64_tr_b16, two reads giving one lane the 8
+// keys of its head-dim column.  K and V have rings of three buffers each.
+//
+// Ping-pong.  The work of a tile is split in two phases per wave -- M: the MFMA phase
+// (O^T += V^T P^T of the previous tile, then S^T = K Q^T of this tile: 32 MFMAs fed by
+// 48 LDS reads) and X: the softmax phase of that tile on the VALU -- and the two waves
+// that share a SIMD (waves w and w + 4; the pairing is read from HW_ID) run them out of
+// phase: while one issues its M phase the other runs its X phase.  Every wave passes
+// one barrier per phase, the lead group in the order M(u) | X(u), the other group in
+// the order X(u-1) | M(u), so each barrier keeps every SIMD's matrix core fed by one
+// wave while the other wave's exponentials run beside it.  The M phase runs at wave
+// priority 1, so its MFMAs issue first and the VALU stream fills the gaps.
+//
+// Tile t's K is read in super-step t, its V in super-step t + 1 (by the PV product of
+// M(t + 1)).  In super-step u each wave issues its DMA share of K_{u+2} and V_{u+1}
+// (into buffers freed by the previous super-step's closing barrier; the lead group
+// issues after its first barrier, so its MFMA phase starts at once), and at its end
+// waits for K_{u+1} and V_u.
 // ----------------------------------------------------------------------------------
-constexpr int kNBuf3 = 3;
 constexpr int kD3 = 128;
 constexpr int kTile3 = kBK * kD3 * 2;  // bytes of one K or V tile (16 KiB)
 
+// Empty asm that uses x: keeps the code producing x on this side of the next barrier
+// (the compiler may otherwise move register-only work across s_barrier).
+template <typename T>
+__device__ __forceinline__ void pin(const T& x) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only parses device code; its asm has no "v" registers
+  asm volatile("" : : "v"(x));
+#else
+  (void)x;
+#endif
+}
+
+__device__ __forceinline__ int simd_id() {
+  int r;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID, 4, 2)" : "=s"(r));
+  return r;
+}
 
 template <int DT, int G, bool POS>
-__global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockArgs a) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
   constexpr int D = kD3;
@@ -517,8 +545,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
   constexpr int DB = D / 32;
   constexpr int kDmaPerWave = kBK / 4 / kWaves;  // 1 KiB DMA instructions per wave per tile (K or V)
 
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kNBuf3 * kBK * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[kNBuf3 * kBK * D];
+  constexpr int NB = 3;  // LDS buffers per ring
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[NB * kBK * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[NB * kBK * D];
+  __shared__ int lim_red[kWaves];
+  __shared__ int simd_of[kWaves];
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
   const int hg = logical / a.n_qtiles;
@@ -537,7 +568,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
   const int my_q = wq0 + lcol;
   const int q_end = min(a.lq, tq0 + TQ);
 
-  __shared__ int lim_red[kWaves];
+  if (lane == 0) simd_of[wave] = simd_id();
   const RowLimits rl = row_limits<POS>(a, q_end, wq0, my_q, wave, lane, lim_red);
   const int n_kv = rl.n_kv;
   const int n_tiles = (n_kv + kBK - 1) / kBK;
@@ -550,23 +581,31 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
   uint32_t k_voff[kDmaPerWave], v_voff[kDmaPerWave];
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
-    const int r = (wave * kDmaPerWave + j) * 4 + (lane >> 4);  // tile row this lane loads
-    const int p = lane & 15;                                     // LDS chunk of the row
+    const int r = (wave * kDmaPerWave + j) * 4 + (lane >> 4);
+    const int p = lane & 15;
     k_voff[j] = static_cast<uint32_t>(r * a.k_ss * 2 + ((p ^ (r & 15)) << 4));
     v_voff[j] = static_cast<uint32_t>(r * a.v_ss * 2 + ((p ^ (4 * (r & 3))) << 4));
   }
-  auto issue_tile = [&](int t, int buf) __attribute__((always_inline)) {
+  auto issue_k = [&](int t, int buf) __attribute__((always_inline)) {
     const int kv0 = t * kBK;
-    const u32x4 ks = make_srd(kbase + static_cast<int64_t>(kv0) * a.k_ss, static_cast<int64_t>(a.lk - kv0) * a.k_ss * 2);
-    const u32x4 vs = make_srd(vbase + static_cast<int64_t>(kv0) * a.v_ss, static_cast<int64_t>(a.lk - kv0) * a.v_ss * 2);
+    const u32x4 s = make_srd(kbase + static_cast<int64_t>(kv0) * a.k_ss, static_cast<int64_t>(a.lk - kv0) * a.k_ss * 2);
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) dma16(ks, k_voff[j], k_lds0 + buf * kTile3 + j * 1024);
+    for (int j = 0; j < kDmaPerWave; ++j) dma16(s, k_voff[j], k_lds0 + buf * kTile3 + j * 1024);
+  };
+  auto issue_v = [&](int t, int buf) __attribute__((always_inline)) {
+    const int kv0 = t * kBK;
+    const u32x4 s = make_srd(vbase + static_cast<int64_t>(kv0) * a.v_ss, static_cast<int64_t>(a.lk - kv0) * a.v_ss * 2);
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) dma16(vs, v_voff[j], v_lds0 + buf * kTile3 + j * 1024);
+    for (int j = 0; j < kDmaPerWave; ++j) dma16(s, v_voff[j], v_lds0 + buf * kTile3 + j * 1024);
   };
 
-  if (n_tiles > 0) issue_tile(0, 0);
-  if (n_tiles > 1) issue_tile(1, 1);
+  // prologue: K_0 .. K_{NB-2}, V_0 .. V_{NB-3}
+#pragma unroll
+  for (int t = 0; t < NB - 1; ++t)
+    if (t < n_tiles) issue_k(t, t);
+#pragma unroll
+  for (int t = 0; t < NB - 2; ++t)
+    if (t < n_tiles) issue_v(t, t);
 
   frag qf[KS];
   {
@@ -577,14 +616,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
     for (int s = 0; s < KS; ++s) qf[s] = as_frag<frag>(buf_load16(qr, qoff + 32 * s));
   }
 
-  // ---- per-lane LDS read addresses (byte offsets within buffer 0) ----
-  // K: row 32b + kperm(lcol), chunk (lhalf + 2s) ^ swz, swz = row & 15 = kperm(lcol) & 15.
   const int krow = kperm(lcol);
   uint32_t k_rd[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) k_rd[s] = krow * (D * 2) + (((lhalf + 2 * s) ^ (krow & 15)) << 4);
-  // V (transposing reads): lane group g = lane / 16 and sub-lane sl = lane % 16 read row
-  // 16s + 8(g/2) + 4h + sl/4 (h = 0, 1 for the two reads), dims 32b + 16(g%2) + 4(sl%4).
   const int g16 = lane >> 4, sl = lane & 15;
   uint32_t v_rd[DB];
 #pragma unroll
@@ -599,6 +634,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
   for (int b = 0; b < DB; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
+  f32x16 sacc[2];
+  frag pf[4];
   float m_run = kInitMax;
   float l_run = 0.f;
 
@@ -607,18 +644,41 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
   const int64_t wave_lim_first = rl.wave_first;
   const int64_t wave_lim_last = rl.wave_last;
 
-  __builtin_amdgcn_s_waitcnt(0);  // Q fragments and tiles 0, 1 resident
+  __builtin_amdgcn_s_waitcnt(0);  // Q fragments and the first tiles resident
   __syncthreads();
+  bool lead = true;
+  {
+    const int mine = simd_of[wave];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) lead = lead && !(w < wave && simd_of[w] == mine);
+  }
+  lead = __builtin_amdgcn_readfirstlane(static_cast<int>(lead)) != 0;
 
-  auto compute = [&](int t, auto bufc) __attribute__((always_inline)) {
-    constexpr int bf = decltype(bufc)::value;
-    const int kv0 = t * kBK;
-    const bool wave_live = !a.causal || kv0 <= wave_lim_last;
-    if (!(wave_live && wq0 < a.lq)) return;
-    const bool need_mask = (kv0 + kBK > a.lk) || (a.causal && kv0 + kBK - 1 > wave_lim_first);
+  // Last tile with a key visible to some row of this wave (-1: none); the tiles a wave
+  // computes are 0 .. last_live, so both phases of the steady-state loop below run
+  // unconditionally.
+  int last_live = n_tiles - 1;
+  if (wq0 >= a.lq) last_live = -1;
+  else if (a.causal) last_live = wave_lim_last < 0 ? -1 : static_cast<int>(min(static_cast<int64_t>(last_live), wave_lim_last / kBK));
+  auto live = [&](int t) __attribute__((always_inline)) { return t >= 0 && t <= last_live; };
 
-    // ---- S^T = K Q^T for two 32-key blocks ----
-    f32x16 sacc[2];
+  // ---- M phase pieces: O^T += V^T P^T of the previous tile (V buffer vb), S^T = K Q^T of this tile (K buffer kb) ----
+  auto pv_part = [&](int vb) __attribute__((always_inline)) {
+    const char* vl = v_lds_c + vb * kTile3;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int b = 0; b < DB; ++b) {
+        const char* p0 = vl + v_rd[b] + s * 16 * D * 2;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0 + 4 * D * 2));
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+        oacc[b] = Ops::mma(as_frag<frag>(u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}), pf[s], oacc[b]);
+      }
+    }
+  };
+  auto s_part = [&](int kb) __attribute__((always_inline)) {
+    const char* kl = k_lds_c + kb * kTile3;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -627,21 +687,41 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        const frag kf = as_frag<frag>(
-            *reinterpret_cast<const u32x4*>(k_lds_c + k_rd[s] + (bf * kTile3 + b * 32 * D * 2)));
+        const frag kf = as_frag<frag>(*reinterpret_cast<const u32x4*>(kl + k_rd[s] + b * 32 * D * 2));
         sacc[b] = Ops::mma(kf, qf[s], sacc[b]);
       }
     }
-    // Keep four K fragment reads in flight ahead of the MFMAs that consume them.
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // 4 LDS reads
+  };
+  // Steady state: both products in one block, LDS reads running ahead of the MFMAs that
+  // consume them (8 Vt reads, then 2 per PV MFMA, then the K reads one per MFMA).
+  auto m_full = [&](int kb, int vb) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);  // the MFMA stream first; the other wave's VALU fills in
+    pv_part(vb);
+    s_part(kb);
+    constexpr int A = 8;  // Vt reads issued before the first MFMA (4 KiB per wave in flight)
+    __builtin_amdgcn_sched_group_barrier(0x100, A, 0);
 #pragma unroll
-    for (int i = 0; i < 2 * KS - 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+    for (int i = 0; i < (32 - A) / 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // last 4 MFMAs
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 32 - 16 - (32 - A) / 2, 0);
+    __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+    for (int b = 0; b < DB; ++b) pin(oacc[b]);
+    pin(sacc[0]);
+    pin(sacc[1]);
+  };
 
-    // ---- mask (boundary tiles only), tile max, lazy rescale ----
+  // ---- X phase: mask, tile max, lazy rescale, P = 2^(s*c - m) of tile t ----
+  auto xphase = [&](int t) __attribute__((always_inline)) {
+    const int kv0 = t * kBK;
+    const bool need_mask = (kv0 + kBK > a.lk) || (a.causal && kv0 + kBK - 1 > wave_lim_first);
     if (need_mask) {
       int64_t lim64 = a.lk - 1 - kv0;
       if (a.causal) lim64 = min(lim64, qlim64 - kv0);
@@ -672,9 +752,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
         for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
       m_run = m_new;
     }
-
-    // ---- P = 2^(s*c - m) as 16-bit B operands, row-sum partial ----
-    frag pf[4];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       float p[16];
@@ -686,38 +763,78 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_dma_kernel(BlockArgs 
       pf[2 * b] = Ops::pack(p);
       pf[2 * b + 1] = Ops::pack(p + 8);
     }
-
-    // ---- O^T += V^T P^T, V^T fragments by transposing reads of row-major V ----
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int b = 0; b < DB; ++b) {
-        const char* p0 = v_lds_c + v_rd[b] + (bf * kTile3 + s * 16 * D * 2);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0 + 4 * D * 2));
-        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
-        oacc[b] = Ops::mma(as_frag<frag>(u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}), pf[s], oacc[b]);
-      }
-    }
+    for (int s = 0; s < 4; ++s) pin(pf[s]);
+    pin(l_run);
   };
 
-  // One step per buffer: issue tile t+2, compute tile t, wait for this wave's loads of
-  // tile t+1 (the newer t+2 loads may stay in flight), barrier.
-  auto step = [&](int t, auto bufc) __attribute__((always_inline)) {
-    constexpr int bf = decltype(bufc)::value;
-    const bool ahead = t + 2 < n_tiles;
-    if (ahead) issue_tile(t + 2, (bf + 2) % kNBuf3);
-    compute(t, bufc);
-    if (t + 1 < n_tiles) {
-      if (ahead) wait_vmcnt<2 * kDmaPerWave>();
+  // Super-step u (u = 0 .. n_tiles): issue K_{u+NB-1} and V_{u+NB-2}; two phases
+  // separated by a barrier; wait for this wave's share of K_{u+1} and V_u (issued NB-2
+  // super-steps earlier); barrier.  Buffers rotate with r = u mod NB: K_u in K buffer
+  // r, V_{u-1} in V buffer r - 1.  Every wave passes the same barriers.
+  auto dma_count = [&](int w) __attribute__((always_inline)) {
+    return (w + NB - 1 < n_tiles ? kDmaPerWave : 0) + (w + NB - 2 < n_tiles ? kDmaPerWave : 0);
+  };
+  auto issue = [&](int u, int r) __attribute__((always_inline)) {
+    if (u + NB - 1 < n_tiles) issue_k(u + NB - 1, r == 0 ? NB - 1 : r - 1);
+    if (u + NB - 2 < n_tiles) issue_v(u + NB - 2, r < 2 ? r + NB - 2 : r - 2);
+  };
+  auto settle = [&](int u) __attribute__((always_inline)) {
+    if (u < n_tiles) {
+      int allow = 0;
+      for (int w = max(0, u + 3 - NB); w <= u; ++w) allow += dma_count(w);
+      static_assert(NB <= 4, "wait table covers NB <= 4");
+      if (allow >= 8) wait_vmcnt<8>();
+      else if (allow >= 6) wait_vmcnt<6>();
+      else if (allow >= 4) wait_vmcnt<4>();
+      else if (allow >= 2) wait_vmcnt<2>();
       else wait_vmcnt<0>();
       __syncthreads();
     }
   };
-  for (int t = 0; t < n_tiles; t += kNBuf3) {
-    step(t, IntC<0>{});
-    if (t + 1 < n_tiles) step(t + 1, IntC<1>{});
-    if (t + 2 < n_tiles) step(t + 2, IntC<2>{});
+  const int hot = max(last_live, 0);  // super-steps 1 .. hot have both products live
+  // The lead group issues its DMA share after the first barrier, at the start of its
+  // softmax phase, so its MFMA phase starts right after the barrier that opens it.
+  if (lead) {
+    if (live(0)) s_part(0);
+    __syncthreads();
+    issue(0, 0);
+    if (live(0)) xphase(0);
+    settle(0);
+    int u = 1, r = 1;
+    for (; u <= hot; ++u, r = r == NB - 1 ? 0 : r + 1) {
+      m_full(r, r == 0 ? NB - 1 : r - 1);
+      __syncthreads();
+      issue(u, r);
+      xphase(u);
+      settle(u);
+    }
+    for (; u <= n_tiles; ++u, r = r == NB - 1 ? 0 : r + 1) {
+      if (live(u - 1)) pv_part(r == 0 ? NB - 1 : r - 1);
+      __syncthreads();
+      issue(u, r);
+      settle(u);
+    }
+  } else {
+    issue(0, 0);
+    __syncthreads();
+    if (live(0)) s_part(0);
+    settle(0);
+    int u = 1, r = 1;
+    for (; u <= hot; ++u, r = r == NB - 1 ? 0 : r + 1) {
+      issue(u, r);
+      xphase(u - 1);
+      __syncthreads();
+      m_full(r, r == 0 ? NB - 1 : r - 1);
+      settle(u);
+    }
+    for (; u <= n_tiles; ++u, r = r == NB - 1 ? 0 : r + 1) {
+      issue(u, r);
+      if (live(u - 1)) xphase(u - 1);
+      __syncthreads();
+      if (live(u - 1)) pv_part(r == 0 ? NB - 1 : r - 1);
+      settle(u);
+    }
   }
 
   if (my_q >= a.lq) return;
@@ -875,17 +992,17 @@ static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   if (D == kD3) {
     if (a.q_lim != nullptr) {
       switch (g) {
-        case 8: flash_block_dma_kernel<DT, 8, true><<<grid, kThreads, 0, stream>>>(a); break;
-        case 4: flash_block_dma_kernel<DT, 4, true><<<grid, kThreads, 0, stream>>>(a); break;
-        case 2: flash_block_dma_kernel<DT, 2, true><<<grid, kThreads, 0, stream>>>(a); break;
-        default: flash_block_dma_kernel<DT, 1, true><<<grid, kThreads, 0, stream>>>(a); break;
+        case 8: flash_block_pingpong_kernel<DT, 8, true><<<grid, kThreads, 0, stream>>>(a); break;
+        case 4: flash_block_pingpong_kernel<DT, 4, true><<<grid, kThreads, 0, stream>>>(a); break;
+        case 2: flash_block_pingpong_kernel<DT, 2, true><<<grid, kThreads, 0, stream>>>(a); break;
+        default: flash_block_pingpong_kernel<DT, 1, true><<<grid, kThreads, 0, stream>>>(a); break;
       }
     } else {
       switch (g) {
-        case 8: flash_block_dma_kernel<DT, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
-        case 4: flash_block_dma_kernel<DT, 4, false><<<grid, kThreads, 0, stream>>>(a); break;
-        case 2: flash_block_dma_kernel<DT, 2, false><<<grid, kThreads, 0, stream>>>(a); break;
-        default: flash_block_dma_kernel<DT, 1, false><<<grid, kThreads, 0, stream>>>(a); break;
+        case 8: flash_block_pingpong_kernel<DT, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
+        case 4: flash_block_pingpong_kernel<DT, 4, false><<<grid, kThreads, 0, stream>>>(a); break;
+        case 2: flash_block_pingpong_kernel<DT, 2, false><<<grid, kThreads, 0, stream>>>(a); break;
+        default: flash_block_pingpong_kernel<DT, 1, false><<<grid, kThreads, 0, stream>>>(a); break;
       }
     }
     return;
