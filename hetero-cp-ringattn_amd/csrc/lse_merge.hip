@@ -5,11 +5,13 @@
 //
 // Layout: each partial is o [H, L, D] fp32 and lse [H, L] fp32 (as the block kernel
 // writes them).  One row (h, t) = D fp32 is handled by D/4 lanes with 16-byte loads,
-// so a wavefront covers 64*4/D rows per instruction; the per-row max/sum over the n
-// partials runs in every lane of the row (n is small), the row's lse is loaded once
-// per lane group.  HBM-bound: algorithmic bytes per row = n*(4D + 4) read +
-// (D*out_bytes + 4) written.
+// so a wavefront covers 64*4/D rows per instruction.  The partials are folded in one
+// pass, in groups of up to 8 whose loads are all in flight together, with the running
+// max, sum and accumulator rescaled when a group raises the max (the same closed form,
+// grouped).  HBM-bound: algorithmic bytes per row = n*(4D + 4) read + (D*out_bytes + 4)
+// written.
 #include "kernels.hpp"
+#include "lds_dma.hpp"
 
 namespace hcp {
 
@@ -29,7 +31,14 @@ struct MergeArgs {
   int64_t lse_out_hs;      // elements between heads of lse_out
 };
 
-template <int OUT_DT>
+// 16-byte streaming load: each partial is read once.
+__device__ __forceinline__ float4 nt_load4(const float* p) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 x = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+  return make_float4(x[0], x[1], x[2], x[3]);
+}
+
+template <int OUT_DT, int NP>
 __global__ __launch_bounds__(256) void lse_merge_kernel(MergeArgs a) {
   const int lpr = a.lanes_per_row;
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / lpr;
@@ -39,48 +48,48 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(MergeArgs a) {
   const int64_t h = row / a.q_len;
   const int64_t t = row - h * a.q_len;
   const int n = a.n;
-
-  float m = -INFINITY;
-  for (int i = 0; i < n; ++i) m = fmaxf(m, a.lse[i][row]);
-  const bool any = m != -INFINITY;
-  const float m_safe = any ? m : 0.f;
-
   const int c = lane_in_row * 4;
   const bool active = c < a.d;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+
+  // One pass over the partials in groups of NP: every load of a group (NP lse values
+  // and NP 16-byte slices of o) is issued before any is used, and the running
+  // (max, sum, acc) is rescaled when a group raises the max.
+  float m = -INFINITY;
   float den = 0.f;
-  int i = 0;
-  // Four partials in flight per step.
-  for (; i + 4 <= n; i += 4) {
-    float l4[4];
-    float4 v4[4];
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int base = 0; base < n; base += NP) {
+    float l[NP];
+    float4 v[NP];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      l4[u] = a.lse[i + u][row];
-      v4[u] = active ? *reinterpret_cast<const float4*>(a.o[i + u] + row * a.d + c)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float w = __expf(l4[u] - m_safe);  // exp(-inf) = 0 for empty partials
-      den += w;
-      acc.x += w * v4[u].x;
-      acc.y += w * v4[u].y;
-      acc.z += w * v4[u].z;
-      acc.w += w * v4[u].w;
-    }
-  }
-  for (; i < n; ++i) {
-    const float l = a.lse[i][row];
-    const float4 v = active ? *reinterpret_cast<const float4*>(a.o[i] + row * a.d + c)
+    for (int u = 0; u < NP; ++u) {
+      const bool in = base + u < n;
+      l[u] = in ? a.lse[base + u][row] : -INFINITY;
+      v[u] = (in && active) ? nt_load4(a.o[base + u] + row * a.d + c)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float w = __expf(l - m_safe);
-    den += w;
-    acc.x += w * v.x;
-    acc.y += w * v.y;
-    acc.z += w * v.z;
-    acc.w += w * v.w;
+    }
+    float mg = l[0];
+#pragma unroll
+    for (int u = 1; u < NP; ++u) mg = fmaxf(mg, l[u]);
+    const float mn = fmaxf(m, mg);
+    if (mn == -INFINITY) continue;  // every partial so far is empty
+    const float sc = __expf(m - mn);  // 0 while m = -inf
+    den *= sc;
+    acc.x *= sc;
+    acc.y *= sc;
+    acc.z *= sc;
+    acc.w *= sc;
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+      const float w = __expf(l[u] - mn);  // exp(-inf) = 0 for empty partials
+      den += w;
+      acc.x += w * v[u].x;
+      acc.y += w * v[u].y;
+      acc.z += w * v[u].z;
+      acc.w += w * v[u].w;
+    }
+    m = mn;
   }
+  const bool any = m != -INFINITY;
   const float inv = (any && den > 0.f) ? 1.f / den : 0.f;
   if (active) {
     const int64_t base = h * a.out_hs + t * a.out_ss + c;
@@ -136,12 +145,20 @@ void launch_lse_merge(int n, const float* const* o_parts, const float* const* ls
   a.lse_out_hs = lse_out_hs;
   const int64_t threads = static_cast<int64_t>(heads) * q_len * lpr;
   const dim3 grid(static_cast<unsigned>(ceil_div(threads, 256)));
-  switch (out_dtype) {
-    case kBF16: lse_merge_kernel<kBF16><<<grid, 256, 0, stream>>>(a); break;
-    case kF16: lse_merge_kernel<kF16><<<grid, 256, 0, stream>>>(a); break;
-    case kF32: lse_merge_kernel<kF32><<<grid, 256, 0, stream>>>(a); break;
-    default: throw Error(-6, "lse_merge: out_dtype must be BF16, F16 or F32");
-  }
+  // Group size: all partials in one group up to 4, else groups of 8.
+  auto go = [&](auto np) {
+    constexpr int NP = decltype(np)::value;
+    switch (out_dtype) {
+      case kBF16: lse_merge_kernel<kBF16, NP><<<grid, 256, 0, stream>>>(a); break;
+      case kF16: lse_merge_kernel<kF16, NP><<<grid, 256, 0, stream>>>(a); break;
+      case kF32: lse_merge_kernel<kF32, NP><<<grid, 256, 0, stream>>>(a); break;
+      default: throw Error(-6, "lse_merge: out_dtype must be BF16, F16 or F32");
+    }
+  };
+  if (n == 1) go(IntC<1>{});
+  else if (n == 2) go(IntC<2>{});
+  else if (n <= 4) go(IntC<4>{});
+  else go(IntC<8>{});
   HCP_HIP(hipGetLastError());
 }
 
