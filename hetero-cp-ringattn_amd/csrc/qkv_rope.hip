@@ -9,10 +9,11 @@
 //
 //   * C^T = W X^T on v_mfma_f32_32x32x16 (A = weight rows, B = token rows, both
 //     hidden-contiguous), so a lane owns one token and 16 features of each 32-feature
-//     block.  A workgroup computes 256 features x 256 tokens with 8 waves of
-//     128 features x 64 tokens: a wave's 128 features are one head (D = 128) or two
-//     (D = 64), so the RoPE partners d and d + D/2 sit in the same lane and register
-//     slot of blocks b and b + D/64 -- the rotation needs no data exchange.
+//     block.  A workgroup computes 256 features x TN tokens (TN = 128, 256 or 384,
+//     chosen per launch) with 8 waves of 64 features x TN/2 tokens: a wave's 64
+//     features are the 32-feature blocks at d and d + D/2 of one head, so each RoPE
+//     partner pair sits in the same lane and register slot of the wave's two blocks --
+//     the rotation needs no data exchange.
 //   * Weight and token tiles of 32 hidden values reach LDS through buffer_load ... lds
 //     (four buffers, three stages in flight, one barrier per stage); chunk p of tile row
 //     r holds global chunk p ^ ((r >> 2) & 3), which keeps the fragment reads free of
@@ -33,11 +34,10 @@ namespace {
 
 constexpr int kQWaves = 8;
 constexpr int kQThreads = kQWaves * 64;
-constexpr int kQTile = 256;                  // features and tokens per workgroup
+constexpr int kQTileF = 256;                 // features per workgroup
 constexpr int kQK = 32;                      // hidden values per stage
 constexpr int kQRow = kQK * 2;               // bytes per tile row in LDS
-constexpr int kQOperand = kQTile * kQRow;    // 16 KiB
-constexpr int kQStage = 2 * kQOperand;       // weights then tokens
+constexpr int kQOperandW = kQTileF * kQRow;  // 16 KiB
 constexpr int kQBufs = 4;
 constexpr int kQGroupM = 4;                  // token tiles per placement group
 
@@ -71,11 +71,20 @@ __device__ __forceinline__ float ld16(const uint16_t* p) {
   return DT == kBF16 ? bf16_bits_to_f32(*p) : f16_bits_to_f32(*p);
 }
 
-template <int DT, int D>
+// TN = tokens per workgroup (256 or 128).  Wave w owns feature group wf = w & 3 and
+// token half wt = w >> 2: 64 features -- the 32-feature blocks at fbase and
+// fbase + D/2 of one head, i.e. RoPE partners -- times TN/2 tokens.
+template <int DT, int D, int TN>
 __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
   using Ops = QkvMfma<DT>;
   using frag = typename Ops::frag;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kQBufs * kQStage];
+  constexpr int TB = TN / 64;                   // 32-token blocks per wave
+  constexpr int XJ = TN / 128;                  // token-row DMA instructions per wave per stage
+  constexpr int kOperandX = TN * kQRow;
+  constexpr int kStage = kQOperandW + kOperandX;
+  constexpr int kPerStage = 2 + XJ;             // DMA instructions per wave per stage
+  constexpr int kPair = D / 64;                 // waves per head
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kQBufs * kStage];
 
   // ---- placement: groups of kQGroupM token tiles x every feature tile ----
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -83,18 +92,20 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
   const int first_m = (logical / per_group) * kQGroupM;
   const int gsize = min(a.n_tiles_m - first_m, kQGroupM);
   const int in_group = logical % per_group;
-  const int tok0 = (first_m + in_group % gsize) * kQTile;
-  const int feat0 = (in_group / gsize) * kQTile;
+  const int tok0 = (first_m + in_group % gsize) * TN;
+  const int feat0 = (in_group / gsize) * kQTileF;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int lcol = lane & 31, lhalf = lane >> 5;
-  const int wf = wave & 1;   // 128-feature half of the tile
-  const int wt = wave >> 1;  // 64-token quarter of the tile
+  const int wf = wave & 3;   // feature group
+  const int wt = wave >> 2;  // token half
+  const int fbase = D * (wf / kPair) + 32 * (wf % kPair);  // first feature of the group in the tile
   const int n_feat = a.nq + 2 * a.nkv;
 
-  // ---- DMA roles: wave w copies weight rows and token rows 32w .. 32w + 31 ----
+  // ---- DMA roles: wave w copies weight rows 32w .. 32w + 31 and token rows
+  // (TN / 8) w .. (TN / 8) (w + 1) - 1 ----
   const int frow = feat0 + 32 * wave;  // never straddles q/k/v (boundaries are multiples of 128)
   int which = 0, local = frow;
   if (frow >= a.nq + a.nkv) {
@@ -107,52 +118,57 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
   const int64_t rows_left = frow >= n_feat ? 0 : (which == 0 ? a.nq : a.nkv) - local;
   const u32x4 srd_w = make_srd(a.w[which] + static_cast<int64_t>(local) * a.hidden,
                                rows_left * a.hidden * 2);
-  const int trow = tok0 + 32 * wave;
+  const int trow = tok0 + (TN / 8) * wave;
   const u32x4 srd_x = make_srd(a.x + static_cast<int64_t>(trow) * a.x_ss,
                                trow >= a.tokens ? 0 : (static_cast<int64_t>(a.tokens - trow) * a.x_ss * 2));
-  uint32_t w_voff[2], x_voff[2];
+  uint32_t w_voff[2], x_voff[XJ];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int r = 16 * j + (lane >> 2);        // row within the wave's 32
+    const int r = 16 * j + (lane >> 2);        // row within the wave's 32 weight rows
     const int tr = 32 * wave + r;              // row within the tile (swizzle key)
-    const uint32_t ch = ((lane & 3) ^ qswz(tr)) << 4;
-    w_voff[j] = static_cast<uint32_t>(r * a.hidden * 2) + ch;
-    x_voff[j] = static_cast<uint32_t>(r * a.x_ss * 2) + ch;
+    w_voff[j] = static_cast<uint32_t>(r * a.hidden * 2) + (((lane & 3) ^ qswz(tr)) << 4);
+  }
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int r = 16 * j + (lane >> 2);        // row within the wave's token rows
+    const int tr = (TN / 8) * wave + r;
+    x_voff[j] = static_cast<uint32_t>(r * a.x_ss * 2) + (((lane & 3) ^ qswz(tr)) << 4);
   }
   const uint32_t lds0 = lds_offset(lds);
   auto issue = [&](int st, int buf) __attribute__((always_inline)) {
     const uint32_t kb = static_cast<uint32_t>(st) * kQRow;
-    const uint32_t base = lds0 + buf * kQStage + wave * (32 * kQRow);
+    const uint32_t wbase = lds0 + buf * kStage + wave * (32 * kQRow);
+    const uint32_t xbase = lds0 + buf * kStage + kQOperandW + wave * ((TN / 8) * kQRow);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(srd_w, w_voff[j] + kb, base + j * 1024);
+    for (int j = 0; j < 2; ++j) dma16(srd_w, w_voff[j] + kb, wbase + j * 1024);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(srd_x, x_voff[j] + kb, base + kQOperand + j * 1024);
+    for (int j = 0; j < XJ; ++j) dma16(srd_x, x_voff[j] + kb, xbase + j * 1024);
   };
 
   // ---- fragment read offsets (bytes within a stage buffer) ----
-  uint32_t w_rd[4][2], x_rd[2][2];
+  uint32_t w_rd[2][2], x_rd[TB][2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const int c = 2 * s + lhalf;
 #pragma unroll
-    for (int fb = 0; fb < 4; ++fb) {
-      const int r = 128 * wf + 32 * fb + lcol;
-      w_rd[fb][s] = r * kQRow + ((c ^ qswz(r)) << 4);
+    for (int i = 0; i < 2; ++i) {
+      const int r = fbase + (D / 2) * i + lcol;
+      w_rd[i][s] = r * kQRow + ((c ^ qswz(r)) << 4);
     }
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      const int r = 64 * wt + 32 * tb + lcol;
-      x_rd[tb][s] = kQOperand + r * kQRow + ((c ^ qswz(r)) << 4);
+    for (int tb = 0; tb < TB; ++tb) {
+      const int r = (TN / 2) * wt + 32 * tb + lcol;
+      x_rd[tb][s] = kQOperandW + r * kQRow + ((c ^ qswz(r)) << 4);
     }
   }
 
-  f32x16 acc[4][2];
+  f32x16 acc[2][TB];
 #pragma unroll
-  for (int fb = 0; fb < 4; ++fb)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
+    for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[fb][tb][r] = 0.f;
+      for (int r = 0; r < 16; ++r) acc[i][tb][r] = 0.f;
 
   const int n_st = a.hidden / kQK;
   if (n_st > 0) issue(0, 0);
@@ -161,26 +177,26 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
 
   auto compute = [&](auto bufc) __attribute__((always_inline)) {
     constexpr int bf = decltype(bufc)::value;
-    const uint8_t* L = lds + bf * kQStage;
+    const uint8_t* L = lds + bf * kStage;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      frag wfr[4], xfr[2];
+      frag wfr[2], xfr[TB];
 #pragma unroll
-      for (int fb = 0; fb < 4; ++fb) wfr[fb] = __builtin_bit_cast(frag, *reinterpret_cast<const u32x4*>(L + w_rd[fb][s]));
+      for (int i = 0; i < 2; ++i) wfr[i] = __builtin_bit_cast(frag, *reinterpret_cast<const u32x4*>(L + w_rd[i][s]));
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb) xfr[tb] = __builtin_bit_cast(frag, *reinterpret_cast<const u32x4*>(L + x_rd[tb][s]));
+      for (int tb = 0; tb < TB; ++tb) xfr[tb] = __builtin_bit_cast(frag, *reinterpret_cast<const u32x4*>(L + x_rd[tb][s]));
 #pragma unroll
-      for (int fb = 0; fb < 4; ++fb)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) acc[fb][tb] = Ops::mma(wfr[fb], xfr[tb], acc[fb][tb]);
+        for (int tb = 0; tb < TB; ++tb) acc[i][tb] = Ops::mma(wfr[i], xfr[tb], acc[i][tb]);
     }
   };
   auto step = [&](int st, auto bufc) __attribute__((always_inline)) {
     constexpr int bf = decltype(bufc)::value;
     // Stage st is resident once at most the stages issued after it are in flight.
     const int after = min(2, n_st - 1 - st);
-    if (after >= 2) wait_vmcnt<8>();
-    else if (after == 1) wait_vmcnt<4>();
+    if (after >= 2) wait_vmcnt<2 * kPerStage>();
+    else if (after == 1) wait_vmcnt<kPerStage>();
     else wait_vmcnt<0>();
     __syncthreads();  // stage st visible; every wave is done with stage st - 1's buffer
     if (st + 3 < n_st) issue(st + 3, (bf + 3) & 3);
@@ -194,7 +210,7 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
   }
 
   // ---- epilogue ----
-  const int fw0 = feat0 + 128 * wf;  // first feature of this wave
+  const int fw0 = feat0 + fbase;     // first feature of this wave
   if (fw0 >= n_feat) return;
   int ow = 0, of = fw0;              // output tensor and its feature offset
   if (fw0 >= a.nq + a.nkv) {
@@ -206,18 +222,19 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
   }
   const uint16_t* bias = a.bias[ow];
   const bool rot = a.rope && ow < 2;
-  constexpr int kPair = D / 64;  // block distance of the RoPE partner
+  const int head = of / D;
+  const int dh = of % D;             // head dim of block 0 (block 1 is dh + D/2)
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const int t = tok0 + 64 * wt + 32 * tb + lcol;
+  for (int tb = 0; tb < TB; ++tb) {
+    const int t = tok0 + (TN / 2) * wt + 32 * tb + lcol;
     if (t >= a.tokens) continue;
-    float v[4][16];
+    float v[2][16];
 #pragma unroll
-    for (int fb = 0; fb < 4; ++fb)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int lf = 32 * fb + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-        v[fb][r] = acc[fb][tb][r] + (bias ? ld16<DT>(bias + of + lf) : 0.f);
+        const int lf = (D / 2) * i + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        v[i][r] = acc[i][tb][r] + (bias ? ld16<DT>(bias + of + lf) : 0.f);
       }
     if (rot) {
       const int64_t p = a.pos[t];
@@ -227,47 +244,47 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
         const float* crow = a.rope_cos + p * (D / 2);
         const float* srow = a.rope_sin + p * (D / 2);
 #pragma unroll
-        for (int fb = 0; fb < 4; ++fb) {
-          if ((fb / kPair) % 2 != 0) continue;  // first half of a head
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = dh + 8 * g + 4 * lhalf;
+          const float4 cs = *reinterpret_cast<const float4*>(crow + d0);
+          const float4 sn = *reinterpret_cast<const float4*>(srow + d0);
+          const float cc[4] = {cs.x, cs.y, cs.z, cs.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int d0 = (32 * fb + 8 * g + 4 * lhalf) % D;
-            const float4 cs = *reinterpret_cast<const float4*>(crow + d0);
-            const float4 sn = *reinterpret_cast<const float4*>(srow + d0);
-            const float cc[4] = {cs.x, cs.y, cs.z, cs.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float x1 = v[fb][4 * g + i], x2 = v[fb + kPair][4 * g + i];
-              v[fb][4 * g + i] = x1 * cc[i] - x2 * ss[i];
-              v[fb + kPair][4 * g + i] = x1 * ss[i] + x2 * cc[i];
-            }
+          for (int i = 0; i < 4; ++i) {
+            const float x1 = v[0][4 * g + i], x2 = v[1][4 * g + i];
+            v[0][4 * g + i] = x1 * cc[i] - x2 * ss[i];
+            v[1][4 * g + i] = x1 * ss[i] + x2 * cc[i];
           }
         }
       }
     }
     // store 4 consecutive head dims per (block, group)
+    int32_t blk = 0;
+    int64_t slot = 0;
+    if (ow != 0 && a.pool != nullptr) {
+      const int64_t sp = a.t0 + t - a.table_off;  // position of this token in the table
+      const int64_t entry = sp / a.bs;
+      blk = (sp >= 0 && entry < a.table_len) ? a.table[entry] : -1;
+      if (blk < 0 || blk >= a.num_blocks) {
+        if (lhalf == 0) atomicOr(a.err, 1);
+        continue;
+      }
+      slot = sp - entry * a.bs;
+    }
 #pragma unroll
-    for (int fb = 0; fb < 4; ++fb)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int f = of + 32 * fb + 8 * g + 4 * lhalf;
-        const int head = f / D, d0 = f % D;
+        const int d0 = dh + (D / 2) * i + 8 * g + 4 * lhalf;
         u32x2 pk;
-        pk[0] = pack2<DT>(v[fb][4 * g], v[fb][4 * g + 1]);
-        pk[1] = pack2<DT>(v[fb][4 * g + 2], v[fb][4 * g + 3]);
+        pk[0] = pack2<DT>(v[i][4 * g], v[i][4 * g + 1]);
+        pk[1] = pack2<DT>(v[i][4 * g + 2], v[i][4 * g + 3]);
         uint16_t* dst;
         if (ow == 0 || a.pool == nullptr) {
           dst = a.out[ow] + head * a.out_hs[ow] + static_cast<int64_t>(t) * a.out_ss[ow] + d0;
         } else {
-          const int64_t sp = a.t0 + t - a.table_off;  // position of this token in the table
-          const int64_t entry = sp / a.bs;
-          const int32_t blk = (sp >= 0 && entry < a.table_len) ? a.table[entry] : -1;
-          if (blk < 0 || blk >= a.num_blocks) {
-            if (lhalf == 0 && g == 0 && fb == 0) atomicOr(a.err, 1);
-            continue;
-          }
           dst = a.pool + (ow == 2 ? a.plane_elems : 0) +
-                ((static_cast<int64_t>(blk) * a.bs + (sp - entry * a.bs)) * a.hkv + head) * D + d0;
+                ((static_cast<int64_t>(blk) * a.bs + slot) * a.hkv + head) * D + d0;
         }
         *reinterpret_cast<u32x2*>(dst) = pk;
       }
@@ -311,19 +328,51 @@ void launch_rope_table(int d, int64_t rows, double base, float* cos, float* sin,
   HCP_HIP(hipGetLastError());
 }
 
+// Token tile TN in {128, 256, 384}: the one with the fewest rounds of workgroups over
+// the device's compute units, each round weighted by the time one tile of that size
+// takes relative to TN = 256 (0.62 and 1.57, measured on MI355X: bigger tiles reuse
+// each LDS fragment more, smaller ones fill the last round better).  Llama-3-8B at
+// 12288 tokens: 768 tiles of 384 are 3 rounds of 256 CUs, 1152 of 256 are 4.5.
+static int qkv_token_tile(int64_t tiles_f, int64_t tokens) {
+  int dev = 0, cus = 0;
+  HCP_HIP(hipGetDevice(&dev));
+  HCP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  if (cus <= 0) return 256;
+  const int tn[3] = {128, 256, 384};
+  const double cost[3] = {0.62, 1.0, 1.57};
+  int best = 1;
+  double best_t = 0.0;
+  for (int i = 0; i < 3; ++i) {
+    const int64_t rounds = ceil_div(tiles_f * ceil_div(tokens, tn[i]), cus);
+    const double t = static_cast<double>(rounds) * cost[i];
+    if (i == 0 || t < best_t - 1e-9 || (i == 1 && t <= best_t + 1e-9)) {
+      best = i;
+      best_t = t;
+    }
+  }
+  return tn[best];
+}
+
 void launch_qkv_rope(int dtype, int d, QkvArgs& a, hipStream_t stream) {
   const int n_feat = a.nq + 2 * a.nkv;
-  a.n_tiles_n = static_cast<int32_t>(ceil_div(n_feat, kQTile));
-  a.n_tiles_m = static_cast<int32_t>(ceil_div(a.tokens, kQTile));
+  a.n_tiles_n = static_cast<int32_t>(ceil_div(n_feat, kQTileF));
+  const int tn = qkv_token_tile(a.n_tiles_n, a.tokens);
+  a.n_tiles_m = static_cast<int32_t>(ceil_div(a.tokens, tn));
   const unsigned grid = static_cast<unsigned>(a.n_tiles_n * a.n_tiles_m);
   if (grid == 0) return;
-  if (dtype == kBF16) {
-    if (d == 128) qkv_rope_kernel<kBF16, 128><<<grid, kQThreads, 0, stream>>>(a);
-    else qkv_rope_kernel<kBF16, 64><<<grid, kQThreads, 0, stream>>>(a);
-  } else {
-    if (d == 128) qkv_rope_kernel<kF16, 128><<<grid, kQThreads, 0, stream>>>(a);
-    else qkv_rope_kernel<kF16, 64><<<grid, kQThreads, 0, stream>>>(a);
-  }
+  auto go = [&](auto tnc) {
+    constexpr int TN = decltype(tnc)::value;
+    if (dtype == kBF16) {
+      if (d == 128) qkv_rope_kernel<kBF16, 128, TN><<<grid, kQThreads, 0, stream>>>(a);
+      else qkv_rope_kernel<kBF16, 64, TN><<<grid, kQThreads, 0, stream>>>(a);
+    } else {
+      if (d == 128) qkv_rope_kernel<kF16, 128, TN><<<grid, kQThreads, 0, stream>>>(a);
+      else qkv_rope_kernel<kF16, 64, TN><<<grid, kQThreads, 0, stream>>>(a);
+    }
+  };
+  if (tn == 128) go(IntC<128>{});
+  else if (tn == 384) go(IntC<384>{});
+  else go(IntC<256>{});
   HCP_HIP(hipGetLastError());
 }
 
