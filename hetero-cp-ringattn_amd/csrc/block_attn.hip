@@ -20,10 +20,11 @@
 //   * Online softmax in the log2 domain with the scale folded in; the running max is
 //     only moved (and O rescaled) when a row's max grows by more than 8 (2^8 bound on
 //     P), which keeps the result exact and skips most rescales.
-//   * K/V tiles of 64 keys.  head_dim 64: double-buffered in LDS, register-staged
+//   * head_dim 64: K/V tiles of 64 keys, double-buffered in LDS, register-staged
 //     global loads of tile t+1 in flight while tile t is computed, one barrier per
-//     tile.  head_dim 128 (flash_block_pingpong_kernel): asynchronous global->LDS
-//     loads and two wave groups that alternate MFMA and softmax phases.
+//     tile.  head_dim 128 (flash_block_pingpong_kernel): tiles of 128 keys,
+//     asynchronous global->LDS loads and two wave groups that alternate MFMA and
+//     softmax phases.
 //   * Causal: tiles wholly in a wave's future are skipped, tiles wholly visible are
 //     unmasked, only tiles straddling the diagonal (or the kv tail) are masked.  The
 //     visible keys of a row are a prefix of the chunk: j <= q_off + i - k_off for
@@ -490,17 +491,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 // query tokens per wave, S^T = K Q^T with K rows in kperm order, P^T straight from the
 // S^T accumulators), with two changes:
 //
-// Tiles.  The K and V tiles of 64 keys reach LDS without passing through registers:
-// buffer_load_dwordx4 ... lds writes 1 KiB per wave instruction (4 rows of 64 keys x
-// 128 dims).  For LDS chunk p of row r the DMA fetches global chunk p ^ swz(r): K rows
+// Tiles.  The K and V tiles of 128 keys reach LDS without passing through registers:
+// buffer_load_dwordx4 ... lds writes 1 KiB per wave instruction (4 rows of 128
+// dims).  For LDS chunk p of row r the DMA fetches global chunk p ^ swz(r): K rows
 // use swz = r & 15, V rows 4 * (r & 3), which makes the fragment reads bank-conflict
 // free.  K fragments (A of S^T) are ds_read_b128; V^T fragments (A of O^T = V^T P^T)
 // come from row-major V through ds_read_b64_tr_b16, two reads giving one lane the 8
-// keys of its head-dim column.  K and V have rings of three buffers each.
+// keys of its head-dim column.  K and V have rings of two 32 KiB buffers each (the
+// kernel also compiles for 64-key tiles with rings of three; 128 keys halve the
+// per-tile barriers, DMA issue and softmax bookkeeping and measured 5% faster).
 //
 // Ping-pong.  The work of a tile is split in two phases per wave -- M: the MFMA phase
-// (O^T += V^T P^T of the previous tile, then S^T = K Q^T of this tile: 32 MFMAs fed by
-// 48 LDS reads) and X: the softmax phase of that tile on the VALU -- and the two waves
+// (O^T += V^T P^T of the previous tile, then S^T = K Q^T of this tile: 64 MFMAs fed by
+// 96 LDS reads) and X: the softmax phase of that tile on the VALU -- and the two waves
 // that share a SIMD (waves w and w + 4; the pairing is read from HW_ID) run them out of
 // phase: while one issues its M phase the other runs its X phase.  Every wave passes
 // one barrier per phase, the lead group in the order M(u) | X(u), the other group in
@@ -509,13 +512,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 // priority 1, so its MFMAs issue first and the VALU stream fills the gaps.
 //
 // Tile t's K is read in super-step t, its V in super-step t + 1 (by the PV product of
-// M(t + 1)).  In super-step u each wave issues its DMA share of K_{u+2} and V_{u+1}
-// (into buffers freed by the previous super-step's closing barrier; the lead group
-// issues after its first barrier, so its MFMA phase starts at once), and at its end
-// waits for K_{u+1} and V_u.
+// M(t + 1)).  With NB buffers per ring, in super-step u each wave issues its DMA share
+// of K_{u+NB-1} and V_{u+NB-2} (into buffers freed by the previous super-step's closing
+// barrier; the lead group issues after its first barrier, so its MFMA phase starts at
+// once), and at its end waits for K_{u+1} and V_u.
 // ----------------------------------------------------------------------------------
+constexpr int kBK3 = 128;  // keys per K/V tile of the head-dim-128 kernel
 constexpr int kD3 = 128;
-constexpr int kTile3 = kBK * kD3 * 2;  // bytes of one K or V tile (16 KiB)
 
 // Empty asm that uses x: keeps the code producing x on this side of the next barrier
 // (the compiler may otherwise move register-only work across s_barrier).
@@ -534,7 +537,7 @@ __device__ __forceinline__ int simd_id() {
   return r;
 }
 
-template <int DT, int G, bool POS>
+template <int DT, int G, bool POS, int BK>
 __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockArgs a) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
@@ -543,11 +546,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   constexpr int TQ = 32 * TB;
   constexpr int KS = D / 16;
   constexpr int DB = D / 32;
-  constexpr int kDmaPerWave = kBK / 4 / kWaves;  // 1 KiB DMA instructions per wave per tile (K or V)
-
-  constexpr int NB = 3;  // LDS buffers per ring
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[NB * kBK * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[NB * kBK * D];
+  constexpr int kDmaPerWave = BK / 4 / kWaves;  // 1 KiB DMA instructions per wave per tile (K or V)
+  constexpr int kTile = BK * D * 2;              // bytes of one K or V tile
+  constexpr int NKB = BK / 32;                   // 32-key blocks of S^T per tile
+  constexpr int NPS = BK / 16;                   // 16-key steps of the PV product per tile
+  constexpr int NB = BK == 64 ? 3 : 2;           // LDS buffers per ring (96 or 128 KiB in all)
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[NB * BK * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[NB * BK * D];
   __shared__ int lim_red[kWaves];
   __shared__ int simd_of[kWaves];
 
@@ -571,7 +576,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   if (lane == 0) simd_of[wave] = simd_id();
   const RowLimits rl = row_limits<POS>(a, q_end, wq0, my_q, wave, lane, lim_red);
   const int n_kv = rl.n_kv;
-  const int n_tiles = (n_kv + kBK - 1) / kBK;
+  const int n_tiles = (n_kv + BK - 1) / BK;
 
   // ---- DMA set-up: wave w fills rows 8w .. 8w+7 of every K and V tile ----
   const uint16_t* kbase = a.k + kvh * a.k_hs;
@@ -587,16 +592,16 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     v_voff[j] = static_cast<uint32_t>(r * a.v_ss * 2 + ((p ^ (4 * (r & 3))) << 4));
   }
   auto issue_k = [&](int t, int buf) __attribute__((always_inline)) {
-    const int kv0 = t * kBK;
+    const int kv0 = t * BK;
     const u32x4 s = make_srd(kbase + static_cast<int64_t>(kv0) * a.k_ss, static_cast<int64_t>(a.lk - kv0) * a.k_ss * 2);
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) dma16(s, k_voff[j], k_lds0 + buf * kTile3 + j * 1024);
+    for (int j = 0; j < kDmaPerWave; ++j) dma16(s, k_voff[j], k_lds0 + buf * kTile + j * 1024);
   };
   auto issue_v = [&](int t, int buf) __attribute__((always_inline)) {
-    const int kv0 = t * kBK;
+    const int kv0 = t * BK;
     const u32x4 s = make_srd(vbase + static_cast<int64_t>(kv0) * a.v_ss, static_cast<int64_t>(a.lk - kv0) * a.v_ss * 2);
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) dma16(s, v_voff[j], v_lds0 + buf * kTile3 + j * 1024);
+    for (int j = 0; j < kDmaPerWave; ++j) dma16(s, v_voff[j], v_lds0 + buf * kTile + j * 1024);
   };
 
   // prologue: K_0 .. K_{NB-2}, V_0 .. V_{NB-3}
@@ -634,8 +639,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   for (int b = 0; b < DB; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
-  f32x16 sacc[2];
-  frag pf[4];
+  f32x16 sacc[NKB];
+  frag pf[NPS];
   float m_run = kInitMax;
   float l_run = 0.f;
 
@@ -659,14 +664,14 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   // unconditionally.
   int last_live = n_tiles - 1;
   if (wq0 >= a.lq) last_live = -1;
-  else if (a.causal) last_live = wave_lim_last < 0 ? -1 : static_cast<int>(min(static_cast<int64_t>(last_live), wave_lim_last / kBK));
+  else if (a.causal) last_live = wave_lim_last < 0 ? -1 : static_cast<int>(min(static_cast<int64_t>(last_live), wave_lim_last / BK));
   auto live = [&](int t) __attribute__((always_inline)) { return t >= 0 && t <= last_live; };
 
   // ---- M phase pieces: O^T += V^T P^T of the previous tile (V buffer vb), S^T = K Q^T of this tile (K buffer kb) ----
   auto pv_part = [&](int vb) __attribute__((always_inline)) {
-    const char* vl = v_lds_c + vb * kTile3;
+    const char* vl = v_lds_c + vb * kTile;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < NPS; ++s) {
 #pragma unroll
       for (int b = 0; b < DB; ++b) {
         const char* p0 = vl + v_rd[b] + s * 16 * D * 2;
@@ -678,15 +683,15 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     }
   };
   auto s_part = [&](int kb) __attribute__((always_inline)) {
-    const char* kl = k_lds_c + kb * kTile3;
+    const char* kl = k_lds_c + kb * kTile;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < NKB; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[b][r] = 0.f;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < NKB; ++b) {
         const frag kf = as_frag<frag>(*reinterpret_cast<const u32x4*>(kl + k_rd[s] + b * 32 * D * 2));
         sacc[b] = Ops::mma(kf, qf[s], sacc[b]);
       }
@@ -698,36 +703,38 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     __builtin_amdgcn_s_setprio(1);  // the MFMA stream first; the other wave's VALU fills in
     pv_part(vb);
     s_part(kb);
-    constexpr int A = 8;  // Vt reads issued before the first MFMA (4 KiB per wave in flight)
+    constexpr int A = 8;            // Vt reads issued before the first MFMA (4 KiB per wave in flight)
+    constexpr int NPV = NPS * DB;   // PV MFMAs (2 Vt reads each)
+    constexpr int NS = NKB * KS;    // S MFMAs (1 K read each)
     __builtin_amdgcn_sched_group_barrier(0x100, A, 0);
 #pragma unroll
-    for (int i = 0; i < (32 - A) / 2; ++i) {
+    for (int i = 0; i < NPV - A / 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < NS; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 32 - 16 - (32 - A) / 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, A / 2, 0);
     __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int b = 0; b < DB; ++b) pin(oacc[b]);
-    pin(sacc[0]);
-    pin(sacc[1]);
+#pragma unroll
+    for (int b = 0; b < NKB; ++b) pin(sacc[b]);
   };
 
   // ---- X phase: mask, tile max, lazy rescale, P = 2^(s*c - m) of tile t ----
   auto xphase = [&](int t) __attribute__((always_inline)) {
-    const int kv0 = t * kBK;
-    const bool need_mask = (kv0 + kBK > a.lk) || (a.causal && kv0 + kBK - 1 > wave_lim_first);
+    const int kv0 = t * BK;
+    const bool need_mask = (kv0 + BK > a.lk) || (a.causal && kv0 + BK - 1 > wave_lim_first);
     if (need_mask) {
       int64_t lim64 = a.lk - 1 - kv0;
       if (a.causal) lim64 = min(lim64, qlim64 - kv0);
-      const int lim = static_cast<int>(max(min(lim64, static_cast<int64_t>(kBK)), static_cast<int64_t>(-1))) - 8 * lhalf;
+      const int lim = static_cast<int>(max(min(lim64, static_cast<int64_t>(BK)), static_cast<int64_t>(-1))) - 8 * lhalf;
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < NKB; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int j = r >> 2, i = r & 3;
@@ -737,7 +744,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     }
     float tmax = -INFINITY;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < NKB; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[b][r]);
     tmax = max_xor32(tmax) * c;
@@ -753,7 +760,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
       m_run = m_new;
     }
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < NKB; ++b) {
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -764,7 +771,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
       pf[2 * b + 1] = Ops::pack(p + 8);
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) pin(pf[s]);
+    for (int s = 0; s < NPS; ++s) pin(pf[s]);
     pin(l_run);
   };
 
@@ -992,17 +999,17 @@ static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   if (D == kD3) {
     if (a.q_lim != nullptr) {
       switch (g) {
-        case 8: flash_block_pingpong_kernel<DT, 8, true><<<grid, kThreads, 0, stream>>>(a); break;
-        case 4: flash_block_pingpong_kernel<DT, 4, true><<<grid, kThreads, 0, stream>>>(a); break;
-        case 2: flash_block_pingpong_kernel<DT, 2, true><<<grid, kThreads, 0, stream>>>(a); break;
-        default: flash_block_pingpong_kernel<DT, 1, true><<<grid, kThreads, 0, stream>>>(a); break;
+        case 8: flash_block_pingpong_kernel<DT, 8, true, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
+        case 4: flash_block_pingpong_kernel<DT, 4, true, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
+        case 2: flash_block_pingpong_kernel<DT, 2, true, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
+        default: flash_block_pingpong_kernel<DT, 1, true, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
       }
     } else {
       switch (g) {
-        case 8: flash_block_pingpong_kernel<DT, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
-        case 4: flash_block_pingpong_kernel<DT, 4, false><<<grid, kThreads, 0, stream>>>(a); break;
-        case 2: flash_block_pingpong_kernel<DT, 2, false><<<grid, kThreads, 0, stream>>>(a); break;
-        default: flash_block_pingpong_kernel<DT, 1, false><<<grid, kThreads, 0, stream>>>(a); break;
+        case 8: flash_block_pingpong_kernel<DT, 8, false, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
+        case 4: flash_block_pingpong_kernel<DT, 4, false, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
+        case 2: flash_block_pingpong_kernel<DT, 2, false, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
+        default: flash_block_pingpong_kernel<DT, 1, false, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
       }
     }
     return;

@@ -128,3 +128,31 @@ def test_c5_full_staging_bit_exact_against_torch_indexing(gpu):
     for (_, _, a, b, ko, vo) in ranges:
         assert torch.equal(ko.view(torch.int16), k[a:b].permute(1, 0, 2).view(torch.int16))
         assert torch.equal(vo.view(torch.int16), v[a:b].permute(1, 0, 2).view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens", [4096, 2048, 12288])
+def test_llama3_8b_qkv_rope_sampled_tokens(gpu, tokens):
+    # The Llama-3-8B projection (hidden 4096 -> 32 q / 8 kv heads of 128, RoPE theta 5e5)
+    # at token counts whose launches take 128-, 256- and 384-token tiles; sampled tokens of
+    # q, k and v against the f64 closed form rotated with the library's own table.
+    hidden, hq, hkv, d = 4096, 32, 8, 128
+    x, wq, wk, wv = synth(47, [(tokens, hidden), (hq * d, hidden), (hkv * d, hidden), (hkv * d, hidden)])
+    for w in (wq, wk, wv):
+        w.mul_(1.0 / math.sqrt(hidden))
+    table = H.rope_table(d, tokens + 64, 500000.0)
+    pos = torch.arange(64, 64 + tokens, dtype=torch.int64, device="cuda")
+    q, k, v = H.qkv_rope_project(x, wq, wk, wv, hq, hkv, d, positions=pos, table=table)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    rows = np.unique(np.array([0, 1, 127, 128, 255, 383, 384, tokens // 2, tokens - 2, tokens - 1]))
+    xs = x[torch.from_numpy(rows).cuda()].double().cpu().numpy()
+    tab = table.cpu().double().numpy()
+    c, s = tab[0][rows + 64], tab[1][rows + 64]
+    for got, w, heads, rot in ((q, wq, hq, True), (k, wk, hkv, True), (v, wv, hkv, False)):
+        y = (xs @ w.double().cpu().numpy().T).reshape(len(rows), heads, d)
+        if rot:
+            y1, y2 = y[..., : d // 2], y[..., d // 2:]
+            y = np.concatenate([y1 * c[:, None] - y2 * s[:, None], y1 * s[:, None] + y2 * c[:, None]], axis=-1)
+        g = got[:, torch.from_numpy(rows).cuda()].transpose(0, 1).double().cpu().numpy()
+        bound = np.abs(y) / 128 + 1e-3 * np.abs(y).max()
+        assert np.all(np.abs(g - y) <= bound), (tokens, float(np.abs(g - y).max()))
