@@ -53,6 +53,8 @@ BLOCK_CASES = [
     ("mha_d64_f16", 300, 300, 4, 4, 64, 77, 77, True, torch.float16),
     ("diag_unaligned_offsets", 257, 260, 8, 8, 128, 1003, 1000, True, torch.bfloat16),
     ("fp32_general_d64", 150, 150, 8, 8, 64, 0, 0, True, torch.float32),
+    ("gqa2_long_noncausal", 160, 1000, 8, 4, 128, 0, 0, False, torch.bfloat16),
+    ("gqa2_causal_long_past", 300, 1500, 4, 2, 128, 1200, 0, True, torch.bfloat16),
 ]
 
 
