@@ -554,7 +554,7 @@ def main():
         "config": {"workload": "c3_llama3_8b_ring_prefill_32k", "chunks": C3["chunks"], "num_q_heads": C3["hq"],
                    "num_kv_heads": C3["hkv"], "head_dim": C3["d"], "causal": True,
                    "flops_per_step": pre["flops"], "frac_mfma_peak": round(pre["tflops"] / PEAK_BF16_TFLOPS, 4)},
-        "roofline": {"bound": "mfma", "kernel": "flash_block_kernel",
+        "roofline": {"bound": "mfma", "kernel": "flash_block_pingpong_kernel",
                      "achieved": round(pre["achieved"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(pre["achieved"] / PEAK_BF16_TFLOPS, 4),
                      "traffic": profiled_traffic("flash_block_kernel_c3_prefill.md"),
