@@ -130,11 +130,13 @@ def test_c5_full_staging_bit_exact_against_torch_indexing(gpu):
         assert torch.equal(vo.view(torch.int16), v[a:b].permute(1, 0, 2).view(torch.int16))
 
 
-@pytest.mark.parametrize("tokens", [4096, 2048, 12288])
+@pytest.mark.parametrize("tokens", [4096, 2048, 12288, 12200])
 def test_llama3_8b_qkv_rope_sampled_tokens(gpu, tokens):
     # The Llama-3-8B projection (hidden 4096 -> 32 q / 8 kv heads of 128, RoPE theta 5e5)
-    # at token counts whose launches take 128-, 256- and 384-token tiles; sampled tokens of
-    # q, k and v against the f64 closed form rotated with the library's own table.
+    # at token counts whose launches take 128-, 256- and 384-token tiles (12200: 384 with
+    # a partial last tile); sampled tokens of q, k and v against the f64 closed form
+    # rotated with the library's own table, and for 12200 the paged append against the
+    # plain views, bit for bit.
     hidden, hq, hkv, d = 4096, 32, 8, 128
     x, wq, wk, wv = synth(47, [(tokens, hidden), (hq * d, hidden), (hkv * d, hidden), (hkv * d, hidden)])
     for w in (wq, wk, wv):
@@ -156,3 +158,15 @@ def test_llama3_8b_qkv_rope_sampled_tokens(gpu, tokens):
         g = got[:, torch.from_numpy(rows).cuda()].transpose(0, 1).double().cpu().numpy()
         bound = np.abs(y) / 128 + 1e-3 * np.abs(y).max()
         assert np.all(np.abs(g - y) <= bound), (tokens, float(np.abs(g - y).max()))
+    if tokens == 12200:
+        bs_, off = 16, 5
+        nb = (tokens + off + bs_ - 1) // bs_ + 3
+        pool = torch.zeros(2, nb, bs_, hkv, d, dtype=torch.bfloat16, device="cuda")
+        blocks = torch.from_numpy(np.random.default_rng(48).permutation(nb).astype(np.int32)).cuda()
+        q2 = H.qkv_rope_project_paged(x, wq, wk, wv, hq, hkv, d, pool, blocks, 0, off, positions=pos, table=table)
+        k2, v2 = H.paged_kv_gather(pool, blocks, 0, off, off + tokens)
+        torch.cuda.synchronize()
+        assert H.fetch_device_errors() == 0
+        assert torch.equal(q.view(torch.int16), q2.view(torch.int16))
+        assert torch.equal(k.view(torch.int16), k2.view(torch.int16))
+        assert torch.equal(v.view(torch.int16), v2.view(torch.int16))
