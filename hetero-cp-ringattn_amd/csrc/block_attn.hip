@@ -33,6 +33,9 @@
 //
 // General path (fp32, or any head_dim <= 256): one thread per (query row, head), K/V
 // tiles staged in LDS as fp32.  Used for the fp32 CPU-smoke config.
+#include <algorithm>
+#include <vector>
+
 #include "kernels.hpp"
 #include "lds_dma.hpp"
 
@@ -58,6 +61,18 @@ struct BlockArgs {
   int64_t fin_lse_hs;
   const int32_t* q_lim;    // positions mode when non-null (causal): row i sees keys [0, q_lim[i])
 };
+
+// Up to kMaxGroup independent (query chunk, KV chunk) pairs with the same head layout in
+// one launch of the head-dim-128 kernel (one ring step of a replay).  Workgroups are
+// numbered head group first, then pair, then query tile (heaviest first): logical id
+// hg * qt_begin[n] + qt_begin[p] + j is query tile n_qtiles_p - 1 - j of pair p.
+constexpr int kMaxGroup = 8;
+struct BlockGroup {
+  BlockArgs a[kMaxGroup];
+  int32_t n;
+  int32_t qt_begin[kMaxGroup + 1];
+};
+static_assert(sizeof(BlockGroup) <= 4096, "kernel arguments are limited to 4 KiB");
 
 namespace {
 
@@ -538,7 +553,7 @@ __device__ __forceinline__ int simd_id() {
 }
 
 template <int DT, int G, bool POS, int BK>
-__global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockGroup grp) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
   constexpr int D = kD3;
@@ -557,8 +572,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   __shared__ int simd_of[kWaves];
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int hg = logical / a.n_qtiles;
-  const int qt = a.n_qtiles - 1 - logical % a.n_qtiles;
+  const int per_hg = grp.qt_begin[grp.n];
+  const int hg = logical / per_hg;
+  const int rem = logical - hg * per_hg;
+  int pi = 0;
+  while (pi + 1 < grp.n && rem >= grp.qt_begin[pi + 1]) ++pi;
+  const BlockArgs& a = grp.a[pi];
+  const int qt = a.n_qtiles - 1 - (rem - grp.qt_begin[pi]);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -966,8 +986,15 @@ __global__ __launch_bounds__(kGenRows) void general_block_kernel(GenArgs a) {
 // Host launcher
 // ----------------------------------------------------------------------------------
 
-template <int D, int DT>
-static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
+// Heads per workgroup of the matrix-core kernels: the largest of 8, 4, 2 dividing
+// Hq / Hkv (query heads that share a KV head), else 1.
+static int heads_per_group(int rep) {
+  for (int cand : {8, 4, 2})
+    if (rep % cand == 0) return cand;
+  return 1;
+}
+
+static BlockArgs make_args(const BlockLaunch& L) {
   BlockArgs a;
   a.q = static_cast<const uint16_t*>(L.q);
   a.k = static_cast<const uint16_t*>(L.k);
@@ -988,41 +1015,61 @@ static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   a.fin_out = L.fin_out; a.fin_dtype = L.fin_dtype; a.fin_hs = L.fin_hs; a.fin_ss = L.fin_ss;
   a.fin_lse = L.fin_lse; a.fin_lse_hs = L.fin_lse_hs;
   a.q_lim = L.causal ? L.q_lim : nullptr;
-  int g = 1;
-  for (int cand : {8, 4, 2}) {
-    if (a.rep % cand == 0) { g = cand; break; }
-  }
-  const int tq = 32 * (kWaves / g);
-  a.n_qtiles = static_cast<int32_t>(ceil_div(L.lq, tq));
+  const int g = heads_per_group(a.rep);
+  a.n_qtiles = static_cast<int32_t>(ceil_div(L.lq, 32 * (kWaves / g)));
   a.n_groups = L.hq / g;
-  const dim3 grid(static_cast<unsigned>(a.n_qtiles * a.n_groups));
+  return a;
+}
+
+// One launch of the head-dim-128 kernel over grp.a[0 .. grp.n) (same dtype, heads, and
+// positions mode; every pair has at least one query tile).
+template <int DT>
+static void launch_pingpong(BlockGroup& grp, hipStream_t stream) {
+  const BlockArgs& a0 = grp.a[0];
+  grp.qt_begin[0] = 0;
+  for (int i = 0; i < grp.n; ++i) grp.qt_begin[i + 1] = grp.qt_begin[i] + grp.a[i].n_qtiles;
+  const dim3 grid(static_cast<unsigned>(grp.qt_begin[grp.n] * a0.n_groups));
+  const bool pos = a0.q_lim != nullptr;
+  switch (heads_per_group(a0.rep)) {
+    case 8:
+      if (pos) flash_block_pingpong_kernel<DT, 8, true, kBK3><<<grid, kThreads, 0, stream>>>(grp);
+      else flash_block_pingpong_kernel<DT, 8, false, kBK3><<<grid, kThreads, 0, stream>>>(grp);
+      break;
+    case 4:
+      if (pos) flash_block_pingpong_kernel<DT, 4, true, kBK3><<<grid, kThreads, 0, stream>>>(grp);
+      else flash_block_pingpong_kernel<DT, 4, false, kBK3><<<grid, kThreads, 0, stream>>>(grp);
+      break;
+    case 2:
+      if (pos) flash_block_pingpong_kernel<DT, 2, true, kBK3><<<grid, kThreads, 0, stream>>>(grp);
+      else flash_block_pingpong_kernel<DT, 2, false, kBK3><<<grid, kThreads, 0, stream>>>(grp);
+      break;
+    default:
+      if (pos) flash_block_pingpong_kernel<DT, 1, true, kBK3><<<grid, kThreads, 0, stream>>>(grp);
+      else flash_block_pingpong_kernel<DT, 1, false, kBK3><<<grid, kThreads, 0, stream>>>(grp);
+      break;
+  }
+}
+
+template <int D, int DT>
+static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
+  BlockArgs a = make_args(L);
   if (D == kD3) {
-    if (a.q_lim != nullptr) {
-      switch (g) {
-        case 8: flash_block_pingpong_kernel<DT, 8, true, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
-        case 4: flash_block_pingpong_kernel<DT, 4, true, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
-        case 2: flash_block_pingpong_kernel<DT, 2, true, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
-        default: flash_block_pingpong_kernel<DT, 1, true, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
-      }
-    } else {
-      switch (g) {
-        case 8: flash_block_pingpong_kernel<DT, 8, false, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
-        case 4: flash_block_pingpong_kernel<DT, 4, false, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
-        case 2: flash_block_pingpong_kernel<DT, 2, false, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
-        default: flash_block_pingpong_kernel<DT, 1, false, kBK3><<<grid, kThreads, 0, stream>>>(a); break;
-      }
-    }
+    BlockGroup grp;
+    grp.n = 1;
+    grp.a[0] = a;
+    launch_pingpong<DT>(grp, stream);
     return;
   }
+  const dim3 grid(static_cast<unsigned>(a.n_qtiles * a.n_groups));
   if (a.q_lim != nullptr) {
-    switch (g) {
+    switch (heads_per_group(a.rep)) {
       case 8: flash_block_kernel<D, DT, 8, true><<<grid, kThreads, 0, stream>>>(a); break;
       case 4: flash_block_kernel<D, DT, 4, true><<<grid, kThreads, 0, stream>>>(a); break;
       case 2: flash_block_kernel<D, DT, 2, true><<<grid, kThreads, 0, stream>>>(a); break;
       default: flash_block_kernel<D, DT, 1, true><<<grid, kThreads, 0, stream>>>(a); break;
     }
   } else {
-    switch (g) {
+    switch (heads_per_group(a.rep)) {
       case 8: flash_block_kernel<D, DT, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
       case 4: flash_block_kernel<D, DT, 4, false><<<grid, kThreads, 0, stream>>>(a); break;
       case 2: flash_block_kernel<D, DT, 2, false><<<grid, kThreads, 0, stream>>>(a); break;
@@ -1073,6 +1120,48 @@ void launch_block_partial(const BlockLaunch& L, hipStream_t stream) {
       case kF16: launch_general<kF16>(L, stream); break;
       default: throw Error(-6, "block_partial: dtype must be BF16, F16 or F32");
     }
+  }
+  HCP_HIP(hipGetLastError());
+}
+
+// Visible (query, key) pairs of one block, for ordering the pairs of a group: exact for
+// contiguous positions, lq * lk / 2 for explicit ones.
+static double block_work(const BlockLaunch& L) {
+  const double lq = static_cast<double>(L.lq), lk = static_cast<double>(L.lk);
+  if (!L.causal) return lq * lk;
+  if (L.q_lim != nullptr) return lq * lk / 2;
+  // row i sees min(max(c + i, 0), lk) keys, c = q_off - k_off + 1
+  const int64_t c = L.q_off - L.k_off + 1;
+  const int64_t i0 = std::min<int64_t>(std::max<int64_t>(0, 1 - c), L.lq);
+  const int64_t i1 = std::min<int64_t>(std::max<int64_t>(0, L.lk - c), L.lq);
+  double w = static_cast<double>(L.lq - std::max(i0, i1)) * lk;
+  if (i1 > i0) w += static_cast<double>(i1 - i0) * static_cast<double>(c) + 0.5 * static_cast<double>(i0 + i1 - 1) * static_cast<double>(i1 - i0);
+  return w;
+}
+
+void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
+  std::vector<const BlockLaunch*> live;
+  for (int i = 0; i < n; ++i)
+    if (Ls[i].lq > 0) live.push_back(&Ls[i]);
+  if (live.empty()) return;
+  const BlockLaunch& f = *live[0];
+  bool grouped = !f.force_general && block_uses_mfma(f.dtype, f.d) && f.d == kD3;
+  for (const BlockLaunch* L : live)
+    grouped = grouped && !L->force_general && L->dtype == f.dtype && L->d == f.d && L->hq == f.hq &&
+              L->hkv == f.hkv && (L->causal && L->q_lim != nullptr) == (f.causal && f.q_lim != nullptr);
+  if (!grouped) {
+    for (const BlockLaunch* L : live) launch_block_partial(*L, stream);
+    return;
+  }
+  // heaviest pairs first: their workgroups are dispatched first on every XCD
+  std::stable_sort(live.begin(), live.end(),
+                   [](const BlockLaunch* x, const BlockLaunch* y) { return block_work(*x) > block_work(*y); });
+  for (size_t base = 0; base < live.size(); base += kMaxGroup) {
+    BlockGroup grp;
+    grp.n = static_cast<int32_t>(std::min<size_t>(kMaxGroup, live.size() - base));
+    for (int i = 0; i < grp.n; ++i) grp.a[i] = make_args(*live[base + i]);
+    if (f.dtype == kBF16) launch_pingpong<kBF16>(grp, stream);
+    else launch_pingpong<kF16>(grp, stream);
   }
   HCP_HIP(hipGetLastError());
 }

@@ -333,6 +333,8 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
                                 stream);
       });
     }
+    // The step's blocks write distinct targets' state: one grouped launch.
+    std::vector<BlockLaunch> step_launches;
     for (int t = 0; t < p.n; ++t) {
       const int src = ((t - s) % p.n + p.n) % p.n;
       int idx = -1;
@@ -376,8 +378,11 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
         L.fin_lse = lse_out ? lse_out + p.off[t] : nullptr;
         L.fin_lse_hs = p.seq;
       }
-      timed(kTimedBlock, stream, [&] { launch_block_partial(L, stream); });
+      step_launches.push_back(L);
     }
+    timed(kTimedBlock, stream, [&] {
+      launch_block_group(step_launches.data(), static_cast<int>(step_launches.size()), stream);
+    });
   }
 }
 

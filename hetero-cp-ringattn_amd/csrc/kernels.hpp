@@ -37,6 +37,9 @@ struct BlockLaunch {
 
 bool block_uses_mfma(int dtype, int d);
 void launch_block_partial(const BlockLaunch& L, hipStream_t stream);
+// Independent blocks (distinct outputs) in as few launches as the kernels allow: one
+// launch per up to 8 head-dim-128 MFMA blocks of the same head layout, else one each.
+void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream);
 
 void launch_lse_merge(int n, const float* const* o_parts, const float* const* lse_parts, int heads,
                       int64_t q_len, int d, int out_dtype, void* out, int64_t out_hs, int64_t out_ss,

@@ -260,6 +260,8 @@ RING_CASES = [
     ("c1_fp32", [640, 384], 8, 8, 64, torch.float32, 42),
     ("c2_small", [512, 320, 192], 16, 2, 128, torch.bfloat16, 43),
     ("uneven4", [300, 77, 500, 123], 8, 2, 128, torch.bfloat16, 50),
+    # 10 domains: the first ring steps hold 10 blocks, launched as groups of 8 + 2
+    ("ten_domains", [200, 64, 130, 96, 300, 50, 128, 77, 256, 99], 8, 2, 128, torch.bfloat16, 51),
 ]
 
 
