@@ -44,13 +44,18 @@ struct PagedCopyArgs {
 
 // Each thread moves kU vectors of each plane per pass: all 2*kU loads are issued before
 // any store, so a 256-thread workgroup keeps 2*kU*256*sizeof(V) bytes in flight.
-template <typename V, bool kGather, int kU>
-__device__ __forceinline__ void paged_copy_entry(const PagedCopyArgs& a, int bid) {
+// Range of entry bid of the concatenated ranges.
+__device__ __forceinline__ int range_of(const PagedCopyArgs& a, int bid) {
   int ri = 0;
   while (ri + 1 < a.n_ranges && bid >= a.block_begin[ri + 1]) ++ri;
+  return ri;
+}
+
+template <typename V, bool kGather, int kU>
+__device__ __forceinline__ void paged_copy_entry(const PagedCopyArgs& a, int bid, int32_t blk) {
+  const int ri = range_of(a, bid);
   const PagedRange& R = a.r[ri];
   const int64_t entry = R.first_entry + (bid - a.block_begin[ri]);
-  const int32_t blk = R.table[entry];
   if (blk < 0 || blk >= a.num_blocks) {
     if (threadIdx.x == 0) atomicOr(a.err, 1);
     return;
@@ -116,9 +121,30 @@ __device__ __forceinline__ void paged_copy_entry(const PagedCopyArgs& a, int bid
 
 template <typename V, bool kGather, int kU>
 __global__ __launch_bounds__(256) void paged_copy_kernel(PagedCopyArgs a) {
-  // Workgroup i copies table entries i, i + grid, ... of the concatenated ranges.
-  for (int bid = blockIdx.x; bid < a.block_begin[a.n_ranges]; bid += gridDim.x)
-    paged_copy_entry<V, kGather, kU>(a, bid);
+  // Workgroup i copies table entries i, i + grid, ... of the concatenated ranges.  The
+  // block ids of its next kPre entries are read in parallel (one lane each) before any
+  // of them is copied, so the table reads do not wait in line with the data.
+  constexpr int kPre = 8;
+  __shared__ int32_t blk_s[kPre];
+  const int n_all = a.block_begin[a.n_ranges];
+  for (int first = blockIdx.x; first < n_all; first += kPre * gridDim.x) {
+    if (threadIdx.x < kPre) {
+      const int bid = first + threadIdx.x * gridDim.x;
+      int32_t b = -1;
+      if (bid < n_all) {
+        const int ri = range_of(a, bid);
+        b = a.r[ri].table[a.r[ri].first_entry + (bid - a.block_begin[ri])];
+      }
+      blk_s[threadIdx.x] = b;
+    }
+    __syncthreads();
+    for (int j = 0; j < kPre; ++j) {
+      const int bid = first + j * gridDim.x;
+      if (bid >= n_all) break;
+      paged_copy_entry<V, kGather, kU>(a, bid, blk_s[j]);
+    }
+    __syncthreads();  // blk_s is rewritten by the next round
+  }
 }
 
 // Host launcher shared by gather and scatter.  Shapes were validated by the caller.
