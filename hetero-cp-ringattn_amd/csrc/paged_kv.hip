@@ -8,8 +8,11 @@
 //
 // One workgroup moves one table entry (a physical block: block_size x Hkv rows of
 // head_dim elements, both planes).  The pool side of a block is one contiguous span
-// per plane (32 KiB for bs=16, Hkv=8, D=128, bf16), read or written with 16-byte
-// accesses in address order; the ring-buffer side is Hkv runs of block_size rows.
+// per plane (32 KiB for bs=16, Hkv=8, D=128, bf16); the ring-buffer side is Hkv runs
+// of block_size rows.  Lanes walk the entry in ring-buffer order (head, token, chunk), so
+// a wave's 16-byte accesses cover 1 KiB contiguous of one head's run and four 256-byte
+// rows of the pool block (writing the head-major side in whole runs measured 17%
+// faster than writing it in 256-byte pieces).
 // HBM-bound byte copy: algorithmic traffic = 2 planes x rows x row_bytes x (read+write).
 #include "kernels.hpp"
 
@@ -62,8 +65,8 @@ __device__ __forceinline__ void paged_copy_entry(const PagedCopyArgs& a, int bid
   }
   constexpr int kVec = sizeof(V);
   const int vec_per_row = a.row_bytes / kVec;
-  const int vec_per_slot = vec_per_row * a.hkv;
-  const int total = vec_per_slot * a.bs;
+  const int vec_per_head = vec_per_row * a.bs;  // one head's rows of the block
+  const int total = vec_per_head * a.hkv;
   const int64_t block_tok0 = R.table_seq_offset + entry * a.bs;  // token of slot 0
   const int64_t block_bytes = static_cast<int64_t>(a.bs) * a.hkv * a.row_bytes;
   uint8_t* pk = a.pool + static_cast<int64_t>(blk) * block_bytes;
@@ -72,21 +75,27 @@ __device__ __forceinline__ void paged_copy_entry(const PagedCopyArgs& a, int bid
   for (int base = threadIdx.x; base < total; base += 256 * kU) {
     V rk[kU], rv[kU];
     int64_t boff[kU];
+    int pc[kU], slot_of[kU];
     bool ok[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
+      // Vector c of this entry in ring-buffer order (head, slot, chunk): the 64 lanes of
+      // a wave cover 4 consecutive tokens of one head, 1 KiB contiguous in the
+      // head-major buffer; in the pool they are 4 rows of 256 B (chunk pc).
       const int c = base + u * 256;
-      const int slot = c / vec_per_slot;
-      const int rem = c - slot * vec_per_slot;
-      const int h = rem / vec_per_row;
-      const int cv = rem - h * vec_per_row;
+      const int h = c / vec_per_head;
+      const int rem = c - h * vec_per_head;
+      const int slot = rem / vec_per_row;
+      const int cv = rem - slot * vec_per_row;
       const int64_t tok = block_tok0 + slot;
+      slot_of[u] = slot;
+      pc[u] = (slot * a.hkv + h) * vec_per_row + cv;
       ok[u] = (c < total) && tok >= R.t0 && tok < R.t1;
       boff[u] = h * R.head_stride_b + (tok - R.t0) * R.seq_stride_b + static_cast<int64_t>(cv) * kVec;
       if (ok[u]) {
         if constexpr (kGather) {
-          rk[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(pk + static_cast<int64_t>(c) * kVec));
-          rv[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(pv + static_cast<int64_t>(c) * kVec));
+          rk[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(pk + static_cast<int64_t>(pc[u]) * kVec));
+          rv[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(pv + static_cast<int64_t>(pc[u]) * kVec));
         } else {
           rk[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(R.k_buf + boff[u]));
           rv[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(R.v_buf + boff[u]));
@@ -101,18 +110,16 @@ __device__ __forceinline__ void paged_copy_entry(const PagedCopyArgs& a, int bid
           __builtin_nontemporal_store(rk[u], reinterpret_cast<V*>(R.k_buf + boff[u]));
           __builtin_nontemporal_store(rv[u], reinterpret_cast<V*>(R.v_buf + boff[u]));
         } else {
-          __builtin_nontemporal_store(rk[u], reinterpret_cast<V*>(pk + static_cast<int64_t>(c) * kVec));
-          __builtin_nontemporal_store(rv[u], reinterpret_cast<V*>(pv + static_cast<int64_t>(c) * kVec));
+          __builtin_nontemporal_store(rk[u], reinterpret_cast<V*>(pk + static_cast<int64_t>(pc[u]) * kVec));
+          __builtin_nontemporal_store(rv[u], reinterpret_cast<V*>(pv + static_cast<int64_t>(pc[u]) * kVec));
         }
       } else if (!kGather && a.zero_tail && c < total) {
         // Slots after the last written token of the sequence's last block.
-        const int slot = c / vec_per_slot;
-        const int64_t tok = block_tok0 + slot;
-        if (tok >= R.t1) {
+        if (block_tok0 + slot_of[u] >= R.t1) {
           V z;
           __builtin_memset(&z, 0, sizeof(V));
-          *reinterpret_cast<V*>(pk + static_cast<int64_t>(c) * kVec) = z;
-          *reinterpret_cast<V*>(pv + static_cast<int64_t>(c) * kVec) = z;
+          *reinterpret_cast<V*>(pk + static_cast<int64_t>(pc[u]) * kVec) = z;
+          *reinterpret_cast<V*>(pv + static_cast<int64_t>(pc[u]) * kVec) = z;
         }
       }
     }
