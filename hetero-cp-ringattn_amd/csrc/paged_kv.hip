@@ -6,15 +6,17 @@
 // (:304-337).  The ring buffer is the KvBlock layout [H, L, D]
 // (rust/src/model/transport/block.rs:11-35), here any strided [H, L, D] view.
 //
-// One workgroup moves one table entry (a physical block: block_size x Hkv rows of
-// head_dim elements, both planes).  The pool side of a block is one contiguous span
-// per plane (32 KiB for bs=16, Hkv=8, D=128, bf16); the ring-buffer side is Hkv runs
-// of block_size rows.  Lanes walk the entry in ring-buffer order (head, token, chunk), so
-// a wave's 16-byte accesses cover 1 KiB contiguous of one head's run and four 256-byte
-// rows of the pool block (writing the head-major side in whole runs measured 17%
-// faster than writing it in 256-byte pieces).
+// The pool side of a table entry (a physical block: block_size x Hkv rows of head_dim
+// elements) is one contiguous span per plane (32 KiB for bs=16, Hkv=8, D=128, bf16);
+// the ring-buffer side is Hkv runs of block_size rows.  Lanes walk an entry in
+// ring-buffer order (head, token, chunk), so the head-major side is written in 1 KiB
+// runs per wave instruction (writing it in the pool's 256-byte pieces measured 17%
+// slower).  The gather of 16-byte-aligned shapes goes through LDS (paged_gather_lds_kernel:
+// both sides contiguous, quarter planes per workgroup); scatter and other shapes copy
+// through registers (paged_copy_kernel, whole entries per workgroup).
 // HBM-bound byte copy: algorithmic traffic = 2 planes x rows x row_bytes x (read+write).
 #include "kernels.hpp"
+#include "lds_dma.hpp"
 
 namespace hcp {
 
@@ -154,6 +156,57 @@ __global__ __launch_bounds__(256) void paged_copy_kernel(PagedCopyArgs a) {
   }
 }
 
+// Gather through LDS (16-byte aligned): a work item is 1/P of one plane of one table
+// entry (bs/P consecutive slots, every kv head).  It reaches LDS by buffer_load ... lds
+// in address order (1 KiB per wave instruction, contiguous on both sides); the lanes
+// then read LDS in head-major order and write the ring buffer in runs of bs/P rows per
+// head.  Small items keep many workgroups resident per CU, so loads of some overlap the
+// stores of others.
+template <int P>
+__global__ __launch_bounds__(256) void paged_gather_lds_kernel(PagedCopyArgs a, int item_bytes) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t stage[];
+  const int n_items = P * 2 * a.block_begin[a.n_ranges];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int blk_bytes = a.bs * a.hkv * a.row_bytes;  // one plane of one block
+  const int n_dma = item_bytes >> 10;                 // 1 KiB DMA instructions per item
+  const int vec_per_row = a.row_bytes >> 4;
+  const int slots = a.bs / P;
+  const int vec_per_head = vec_per_row * slots;
+  const int total = vec_per_head * a.hkv;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int bid = item / (2 * P), plane = (item / P) & 1, part = item % P;
+    const int ri = range_of(a, bid);
+    const PagedRange& R = a.r[ri];
+    const int64_t entry = R.first_entry + (bid - a.block_begin[ri]);
+    const int32_t blk = __builtin_amdgcn_readfirstlane(R.table[entry]);
+    if (blk < 0 || blk >= a.num_blocks) {
+      if (threadIdx.x == 0 && plane == 0 && part == 0) atomicOr(a.err, 1);
+      continue;
+    }
+    const u32x4 srd = make_srd(a.pool + plane * a.plane_bytes + static_cast<int64_t>(blk) * blk_bytes +
+                                   static_cast<int64_t>(part) * item_bytes, item_bytes);
+    for (int i = wave; i < n_dma; i += 4)
+      dma16(srd, static_cast<uint32_t>((i << 10) + lane * 16), lds_offset(stage) + (i << 10));
+    wait_vmcnt<0>();
+    __syncthreads();
+    uint8_t* dst = plane ? R.v_buf : R.k_buf;
+    const int64_t tok0 = R.table_seq_offset + entry * a.bs + static_cast<int64_t>(part) * slots;
+    for (int c = threadIdx.x; c < total; c += 256) {
+      const int h = c / vec_per_head;
+      const int rem = c - h * vec_per_head;
+      const int slot = rem / vec_per_row;
+      const int cv = rem - slot * vec_per_row;
+      const int64_t tok = tok0 + slot;
+      if (tok < R.t0 || tok >= R.t1) continue;
+      const int pc = ((slot * a.hkv + h) * vec_per_row + cv) << 4;
+      const int64_t boff = h * R.head_stride_b + (tok - R.t0) * R.seq_stride_b + static_cast<int64_t>(cv) * 16;
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&stage[pc]), reinterpret_cast<u32x4*>(dst + boff));
+    }
+    __syncthreads();  // the stage is refilled by the next item
+  }
+}
+
 // Host launcher shared by gather and scatter.  Shapes were validated by the caller.
 void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs, int hkv, int d,
                              int elem_bytes, int n, const PagedRangeDesc* ranges, int zero_tail,
@@ -203,7 +256,21 @@ void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs
     // About two table entries per workgroup (128 KiB for bs=16, Hkv=8, D=128 bf16).
     const dim3 grid(static_cast<unsigned>(blocks > 2048 ? (blocks + 1) / 2 : blocks));
     // Widest access that every row start and stride allows.
-    if (al16) {
+    const int64_t blk_bytes = static_cast<int64_t>(bs) * hkv * a.row_bytes;
+    // LDS path: 1/P of a plane per item, P the largest of 4, 2, 1 leaving whole-KiB items
+    // of at most 32 KiB (measured on c5 against P = 8, 2, 1 and the register path: 4 is
+    // fastest).
+    int parts = 0;
+    for (int pp : {4, 2, 1})
+      if (parts == 0 && bs % pp == 0 && (blk_bytes / pp) % 1024 == 0 && blk_bytes / pp <= 32768) parts = pp;
+    if (gather && al16 && parts > 0) {
+      const int item_bytes = static_cast<int>(blk_bytes / parts);
+      const int64_t items = 2LL * parts * blocks;
+      const dim3 lgrid(static_cast<unsigned>(items < 32768 ? items : 32768));
+      if (parts == 4) paged_gather_lds_kernel<4><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+      else if (parts == 2) paged_gather_lds_kernel<2><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+      else paged_gather_lds_kernel<1><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+    } else if (al16) {
       if (gather) paged_copy_kernel<u32x4, true, 8><<<grid, 256, 0, stream>>>(a);
       else paged_copy_kernel<u32x4, false, 8><<<grid, 256, 0, stream>>>(a);
     } else if (al4) {
