@@ -266,7 +266,8 @@ void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs
     if (gather && al16 && parts > 0) {
       const int item_bytes = static_cast<int>(blk_bytes / parts);
       const int64_t items = 2LL * parts * blocks;
-      const dim3 lgrid(static_cast<unsigned>(items < 32768 ? items : 32768));
+      // one item per workgroup (measured on c5: 5758-5777 GB/s against 5495-5537 with two)
+      const dim3 lgrid(static_cast<unsigned>(items < (1LL << 24) ? items : (1LL << 24)));
       if (parts == 4) paged_gather_lds_kernel<4><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
       else if (parts == 2) paged_gather_lds_kernel<2><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
       else paged_gather_lds_kernel<1><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
