@@ -384,7 +384,14 @@ def bench_staged(H, torch, steps: int, warmup: int, full_prefill: bool = True):
     gbytes = 2 * seq * hkv * d * 2 * 2
     exact = bool(torch.equal(stage_k.view(torch.int16), k.permute(1, 0, 2).contiguous().view(torch.int16))) and \
         bool(torch.equal(stage_v.view(torch.int16), v.permute(1, 0, 2).contiguous().view(torch.int16)))
-    res = dict(gather_ms=ms, gather_gbs=gbytes / (ms * 1e-3) / 1e9, gather_bytes=gbytes, bit_exact=exact)
+    # the reverse direction (KvCache::update): scatter the whole sequence back into the pool
+    kh, vh = stage_k, stage_v
+    scatter = lambda: H.paged_kv_scatter(pool, table, 0, 0, seq, kh, vh)
+    for _ in range(warmup):
+        scatter()
+    ms_s = time_cuda(torch, scatter, steps)
+    res = dict(gather_ms=ms, gather_gbs=gbytes / (ms * 1e-3) / 1e9, gather_bytes=gbytes, bit_exact=exact,
+               scatter_ms=ms_s, scatter_gbs=gbytes / (ms_s * 1e-3) / 1e9)
     del stage_k, stage_v
     if full_prefill:
         ws = torch.empty(H.replay_workspace_size(torch.bfloat16, c["hq"], hkv, d, c["chunks"], paged=True),
@@ -522,7 +529,8 @@ def main():
                                     "permuted bs=16 block pool",
                         "value": round(stg["gather_gbs"], 1), "unit": "GB/s", "ms": round(stg["gather_ms"], 4),
                         "frac_hbm": round(stg["gather_gbs"] / PEAK_HBM_GBS, 4), "bytes": stg["gather_bytes"],
-                        "bit_exact": stg["bit_exact"]},
+                        "bit_exact": stg["bit_exact"], "scatter_gbs": round(stg["scatter_gbs"], 1),
+                        "scatter_ms": round(stg["scatter_ms"], 4)},
             staged_prefill_128k={"value": round(stg.get("prefill_tflops", 0.0), 1), "unit": "TFLOP/s",
                                  "ms": round(stg.get("prefill_ms", 0.0), 3),
                                  "frac_mfma": round(stg.get("prefill_tflops", 0.0) / PEAK_BF16_TFLOPS, 4)},

@@ -12,8 +12,9 @@
 // ring-buffer order (head, token, chunk), so the head-major side is written in 1 KiB
 // runs per wave instruction (writing it in the pool's 256-byte pieces measured 17%
 // slower).  The gather of 16-byte-aligned shapes goes through LDS (paged_gather_lds_kernel:
-// both sides contiguous, quarter planes per workgroup); scatter and other shapes copy
-// through registers (paged_copy_kernel, whole entries per workgroup).
+// both sides contiguous, quarter planes per workgroup), and so does the scatter
+// (paged_scatter_lds_kernel); other shapes copy through registers (paged_copy_kernel,
+// whole entries per workgroup).
 // HBM-bound byte copy: algorithmic traffic = 2 planes x rows x row_bytes x (read+write).
 #include "kernels.hpp"
 #include "lds_dma.hpp"
@@ -207,6 +208,58 @@ __global__ __launch_bounds__(256) void paged_gather_lds_kernel(PagedCopyArgs a, 
   }
 }
 
+// Scatter through LDS, the mirror of the gather above: the lanes read an item's rows
+// from the head-major buffer in 1 KiB runs (head, token, chunk order) into LDS at
+// their pool positions, then write the pool block span in address order.  Slots before
+// t0 are left alone; slots from t1 on are zero-filled when zero_tail is set.
+template <int P>
+__global__ __launch_bounds__(256) void paged_scatter_lds_kernel(PagedCopyArgs a, int item_bytes) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t stage[];
+  const int n_items = P * 2 * a.block_begin[a.n_ranges];
+  const int blk_bytes = a.bs * a.hkv * a.row_bytes;
+  const int vec_per_row = a.row_bytes >> 4;
+  const int slots = a.bs / P;
+  const int vec_per_head = vec_per_row * slots;
+  const int vec_per_slot = vec_per_row * a.hkv;
+  const int total = vec_per_head * a.hkv;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int bid = item / (2 * P), plane = (item / P) & 1, part = item % P;
+    const int ri = range_of(a, bid);
+    const PagedRange& R = a.r[ri];
+    const int64_t entry = R.first_entry + (bid - a.block_begin[ri]);
+    const int32_t blk = __builtin_amdgcn_readfirstlane(R.table[entry]);
+    if (blk < 0 || blk >= a.num_blocks) {
+      if (threadIdx.x == 0 && plane == 0 && part == 0) atomicOr(a.err, 1);
+      continue;
+    }
+    const uint8_t* src = plane ? R.v_buf : R.k_buf;
+    const int64_t tok0 = R.table_seq_offset + entry * a.bs + static_cast<int64_t>(part) * slots;
+    for (int c = threadIdx.x; c < total; c += 256) {
+      const int h = c / vec_per_head;
+      const int rem = c - h * vec_per_head;
+      const int slot = rem / vec_per_row;
+      const int cv = rem - slot * vec_per_row;
+      const int64_t tok = tok0 + slot;
+      if (tok < R.t0 || tok >= R.t1) continue;
+      const int pc = ((slot * a.hkv + h) * vec_per_row + cv) << 4;
+      const int64_t boff = h * R.head_stride_b + (tok - R.t0) * R.seq_stride_b + static_cast<int64_t>(cv) * 16;
+      *reinterpret_cast<u32x4*>(&stage[pc]) = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + boff));
+    }
+    __syncthreads();
+    uint8_t* dst = a.pool + plane * a.plane_bytes + static_cast<int64_t>(blk) * blk_bytes +
+                   static_cast<int64_t>(part) * item_bytes;
+    for (int c = threadIdx.x; c < total; c += 256) {
+      const int64_t tok = tok0 + c / vec_per_slot;
+      if (tok >= R.t0 && tok < R.t1) {
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&stage[c << 4]), reinterpret_cast<u32x4*>(dst + (c << 4)));
+      } else if (tok >= R.t1 && a.zero_tail) {
+        *reinterpret_cast<u32x4*>(dst + (c << 4)) = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    __syncthreads();  // the stage is refilled by the next item
+  }
+}
+
 // Host launcher shared by gather and scatter.  Shapes were validated by the caller.
 void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs, int hkv, int d,
                              int elem_bytes, int n, const PagedRangeDesc* ranges, int zero_tail,
@@ -263,14 +316,20 @@ void launch_paged_copy_batch(bool gather, void* pool, int64_t num_blocks, int bs
     int parts = 0;
     for (int pp : {4, 2, 1})
       if (parts == 0 && bs % pp == 0 && (blk_bytes / pp) % 1024 == 0 && blk_bytes / pp <= 32768) parts = pp;
-    if (gather && al16 && parts > 0) {
+    if (al16 && parts > 0) {
       const int item_bytes = static_cast<int>(blk_bytes / parts);
       const int64_t items = 2LL * parts * blocks;
       // one item per workgroup (measured on c5: 5758-5777 GB/s against 5495-5537 with two)
       const dim3 lgrid(static_cast<unsigned>(items < (1LL << 24) ? items : (1LL << 24)));
-      if (parts == 4) paged_gather_lds_kernel<4><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
-      else if (parts == 2) paged_gather_lds_kernel<2><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
-      else paged_gather_lds_kernel<1><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+      if (gather) {
+        if (parts == 4) paged_gather_lds_kernel<4><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+        else if (parts == 2) paged_gather_lds_kernel<2><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+        else paged_gather_lds_kernel<1><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+      } else {
+        if (parts == 4) paged_scatter_lds_kernel<4><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+        else if (parts == 2) paged_scatter_lds_kernel<2><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+        else paged_scatter_lds_kernel<1><<<lgrid, 256, item_bytes, stream>>>(a, item_bytes);
+      }
     } else if (al16) {
       if (gather) paged_copy_kernel<u32x4, true, 8><<<grid, 256, 0, stream>>>(a);
       else paged_copy_kernel<u32x4, false, 8><<<grid, 256, 0, stream>>>(a);

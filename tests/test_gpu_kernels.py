@@ -169,6 +169,13 @@ def test_paged_gather_scatter_bit_exact(gpu, dtype):
     # gather(scatter(x)) == x
     k3, v3 = H.paged_kv_gather(pool, table, off, t0, t1)
     assert np.array_equal(_np_bits(k3), _np_bits(k2)) and np.array_equal(_np_bits(v3), _np_bits(v2))
+    # a sub-range in the middle without the zero tail leaves every other slot alone
+    k4 = torch.roll(k2, 3, dims=1)[:, :100].contiguous()
+    v4 = torch.roll(v2, 5, dims=1)[:, :100].contiguous()
+    H.paged_kv_scatter(pool, table, off, t0 + 7, t0 + 107, k4, v4, zero_tail=False)
+    torch.cuda.synchronize()
+    clib.paged_scatter(pool_np, table_np, off, t0 + 7, t0 + 107, _np_bits(k4), _np_bits(v4), zero_tail=False)
+    assert np.array_equal(_np_bits(pool), pool_np)
     assert H.fetch_device_errors() == 0
 
 
