@@ -623,6 +623,7 @@ int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_
 }
 
 // ---- decode Q-ring replay ----
+}  // extern "C": internal helpers below have C++ linkage
 namespace {
 struct DecodeRingPlan {
   size_t part_o = 0, part_lse = 0, part_bytes = 0, dec_off = 0, total = 0;
@@ -647,6 +648,7 @@ DecodeRingPlan plan_decode_ring(const hcp_paged_decode_desc* desc, int n, const 
   return p;
 }
 }  // namespace
+extern "C" {
 
 int hcp_decode_ring_owner(int64_t global_pos, int32_t num_domains) {
   if (num_domains <= 0 || global_pos < 0) return HCP_RING_E_INVALID;
@@ -709,6 +711,7 @@ int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_po
   });
 }
 
+}  // extern "C": internal helpers below have C++ linkage
 namespace {
 
 void check_kv_frame(const hcp_kv_frame_desc* d) {
@@ -778,6 +781,7 @@ int field_dtype(const JVal& o, const char* key) {
 }
 
 }  // namespace
+extern "C" {
 
 size_t hcp_kv_frame_payload_bytes(const hcp_kv_frame_desc* desc) {
   try {
@@ -959,6 +963,7 @@ int hcp_packet_frame_unpack(const hcp_packet_frame_desc* desc, const void* paylo
   });
 }
 
+}  // extern "C": internal helpers below have C++ linkage
 namespace {
 
 bool aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
@@ -1015,6 +1020,7 @@ void check_qkv_out(const hcp_ring_view& v, const char* name) {
 }
 
 }  // namespace
+extern "C" {
 
 int hcp_rope_table(int32_t head_dim, int64_t rows, double base, float* table, void* stream) {
   return guarded(__func__, [&] {
@@ -1070,6 +1076,7 @@ int hcp_qkv_rope_project_paged(const hcp_qkv_desc* desc, const void* x, int64_t 
   });
 }
 
+}  // extern "C": internal helpers below have C++ linkage
 namespace {
 
 int status_code(const hcp_ringattn::Status& st, const char* fn) {
@@ -1099,6 +1106,7 @@ hcp_ringattn::BoundaryTensor host_f32(const char* name, std::vector<int64_t> sha
 }
 
 }  // namespace
+extern "C" {
 
 struct hcp_ringattn_runtime {
   std::unique_ptr<hcp_ringattn::RingAttnRuntime> impl;

@@ -24,13 +24,19 @@ __device__ __forceinline__ u32x4 make_srd(const void* base, int64_t bytes) {
 }
 
 // One wave-wide 16-byte-per-lane load straight into LDS at lds_addr + 16 * lane.  The
-// compiler does not track it: callers wait with s_waitcnt vmcnt themselves.
+// compiler does not track it: callers wait with s_waitcnt vmcnt themselves.  M0 is set
+// and consumed inside the statement; clang warns that a clobber of the reserved M0 is
+// not preserved around it, which is harmless here (the kernels keep no value of their
+// own in M0: every M0 access in their code is this statement's).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(u32x4 srd, uint32_t voff, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
                : "v"(voff), "s"(srd), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // s_waitcnt vmcnt(N) for N < 64 (vmcnt bits [3:0] and [15:14]); expcnt and lgkmcnt
 // left unconstrained.
