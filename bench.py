@@ -111,15 +111,21 @@ def bench_prefill(H, torch, steps: int, warmup: int):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    H.replay_timing(True)
-    H.replay_timing_read()
+    # whole-step time without instrumentation (per-launch events add ~10 us between launches)
     log(f"c3 prefill timed x{steps}")
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    # then the same steps with HIP events around every block launch, for the kernel's own
+    # average launch time (the roofline)
+    H.replay_timing(True)
+    H.replay_timing_read()
+    log(f"c3 prefill per-launch timing x{steps}")
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
     tm = H.replay_timing_read()
     H.replay_timing(False)
     flops = causal_flops(seq, c["hq"], c["d"])
