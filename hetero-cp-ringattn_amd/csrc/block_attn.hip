@@ -512,9 +512,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 // use swz = r & 15, V rows 4 * (r & 3), which makes the fragment reads bank-conflict
 // free.  K fragments (A of S^T) are ds_read_b128; V^T fragments (A of O^T = V^T P^T)
 // come from row-major V through ds_read_b64_tr_b16, two reads giving one lane the 8
-// keys of its head-dim column.  K and V have rings of two 32 KiB buffers each (the
-// kernel also compiles for 64-key tiles with rings of three; 128 keys halve the
-// per-tile barriers, DMA issue and softmax bookkeeping and measured 5% faster).
+// keys of its head-dim column.  K has a ring of two 32 KiB buffers and V a ring of
+// three (160 KiB of LDS, all of it; V's third buffer gives its loads a super-step more
+// slack).  The kernel also compiles for 64-key tiles with rings of three; 128 keys
+// halve the per-tile barriers, DMA issue and softmax bookkeeping and measured 5% faster.
 //
 // Ping-pong.  The work of a tile is split in two phases per wave -- M: the MFMA phase
 // (O^T += V^T P^T of the previous tile, then S^T = K Q^T of this tile: 64 MFMAs fed by
@@ -527,10 +528,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
 // priority 1, so its MFMAs issue first and the VALU stream fills the gaps.
 //
 // Tile t's K is read in super-step t, its V in super-step t + 1 (by the PV product of
-// M(t + 1)).  With NB buffers per ring, in super-step u each wave issues its DMA share
-// of K_{u+NB-1} and V_{u+NB-2} (into buffers freed by the previous super-step's closing
-// barrier; the lead group issues after its first barrier, so its MFMA phase starts at
-// once), and at its end waits for K_{u+1} and V_u.
+// M(t + 1)).  With NBK and NBV buffers per ring, in super-step u each wave issues its
+// DMA share of K_{u+NBK-1} and V_{u+NBV-2} (into buffers freed by the previous
+// super-step's closing barrier; the lead group issues after its first barrier, so its
+// MFMA phase starts at once), and at its end waits for K_{u+1} and V_u.
 // ----------------------------------------------------------------------------------
 constexpr int kBK3 = 128;  // keys per K/V tile of the head-dim-128 kernel
 constexpr int kD3 = 128;
@@ -565,11 +566,16 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   constexpr int kTile = BK * D * 2;              // bytes of one K or V tile
   constexpr int NKB = BK / 32;                   // 32-key blocks of S^T per tile
   constexpr int NPS = BK / 16;                   // 16-key steps of the PV product per tile
-  constexpr int NB = BK == 64 ? 3 : 2;           // LDS buffers per ring (96 or 128 KiB in all)
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[NB * BK * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[NB * BK * D];
-  __shared__ int lim_red[kWaves];
-  __shared__ int simd_of[kWaves];
+  // LDS buffers per ring: 3 + 3 tiles of 64 keys (96 KiB); 2 K + 3 V tiles of 128 keys
+  // (160 KiB; two V buffers measured 0.4% slower).
+  constexpr int NBK = BK == 64 ? 3 : 2;
+  constexpr int NBV = 3;
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[NBK * BK * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[NBV * BK * D];
+  // Two small reduction arrays live at the start of the last V buffer, which the DMA
+  // first writes in super-step 1, after every read of them.
+  int* const lim_red = reinterpret_cast<int*>(v_lds + (NBV - 1) * BK * D);
+  int* const simd_of = lim_red + kWaves;
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
   const int per_hg = grp.qt_begin[grp.n];
@@ -624,12 +630,12 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     for (int j = 0; j < kDmaPerWave; ++j) dma16(s, v_voff[j], v_lds0 + buf * kTile + j * 1024);
   };
 
-  // prologue: K_0 .. K_{NB-2}, V_0 .. V_{NB-3}
+  // prologue: K_0 .. K_{NBK-2}, V_0 .. V_{NBV-3}
 #pragma unroll
-  for (int t = 0; t < NB - 1; ++t)
+  for (int t = 0; t < NBK - 1; ++t)
     if (t < n_tiles) issue_k(t, t);
 #pragma unroll
-  for (int t = 0; t < NB - 2; ++t)
+  for (int t = 0; t < NBV - 2; ++t)
     if (t < n_tiles) issue_v(t, t);
 
   frag qf[KS];
@@ -795,22 +801,28 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     pin(l_run);
   };
 
-  // Super-step u (u = 0 .. n_tiles): issue K_{u+NB-1} and V_{u+NB-2}; two phases
-  // separated by a barrier; wait for this wave's share of K_{u+1} and V_u (issued NB-2
-  // super-steps earlier); barrier.  Buffers rotate with r = u mod NB: K_u in K buffer
-  // r, V_{u-1} in V buffer r - 1.  Every wave passes the same barriers.
-  auto dma_count = [&](int w) __attribute__((always_inline)) {
-    return (w + NB - 1 < n_tiles ? kDmaPerWave : 0) + (w + NB - 2 < n_tiles ? kDmaPerWave : 0);
+  // Super-step u (u = 0 .. n_tiles): issue K_{u+NBK-1} and V_{u+NBV-2} (K first); two
+  // phases separated by a barrier; wait for this wave's share of K_{u+1} and V_u;
+  // barrier.  K_t sits in K buffer t mod NBK, V_t in V buffer t mod NBV; a K buffer is
+  // free after the super-step that reads it, a V buffer after the one that follows.
+  // Every wave passes the same barriers.
+  auto k_count = [&](int w) __attribute__((always_inline)) {
+    return w >= 0 && w + NBK - 1 < n_tiles ? kDmaPerWave : 0;
   };
-  auto issue = [&](int u, int r) __attribute__((always_inline)) {
-    if (u + NB - 1 < n_tiles) issue_k(u + NB - 1, r == 0 ? NB - 1 : r - 1);
-    if (u + NB - 2 < n_tiles) issue_v(u + NB - 2, r < 2 ? r + NB - 2 : r - 2);
+  auto v_count = [&](int w) __attribute__((always_inline)) {
+    return w >= 0 && w + NBV - 2 < n_tiles ? kDmaPerWave : 0;
+  };
+  auto issue = [&](int u) __attribute__((always_inline)) {
+    if (u + NBK - 1 < n_tiles) issue_k(u + NBK - 1, (u + NBK - 1) % NBK);
+    if (u + NBV - 2 < n_tiles) issue_v(u + NBV - 2, (u + NBV - 2) % NBV);
   };
   auto settle = [&](int u) __attribute__((always_inline)) {
     if (u < n_tiles) {
-      int allow = 0;
-      for (int w = max(0, u + 3 - NB); w <= u; ++w) allow += dma_count(w);
-      static_assert(NB <= 4, "wait table covers NB <= 4");
+      // Loads issued after the later of K_{u+1} (issued in super-step u + 2 - NBK) and
+      // V_u (in u + 2 - NBV; V after K within a super-step) may stay in flight.
+      const int sk = u + 2 - NBK, sv = u + 2 - NBV;
+      int allow = sk > sv ? v_count(sk) : 0;
+      for (int w = max(sk, sv) + 1; w <= u; ++w) allow += k_count(w) + v_count(w);
       if (allow >= 8) wait_vmcnt<8>();
       else if (allow >= 6) wait_vmcnt<6>();
       else if (allow >= 4) wait_vmcnt<4>();
@@ -820,46 +832,48 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     }
   };
   const int hot = max(last_live, 0);  // super-steps 1 .. hot have both products live
+  // Ring positions of super-step u: rk = u mod NBK (K_u), rv = (u - 1) mod NBV (V_{u-1}).
+  auto next = [](int r, int nb) __attribute__((always_inline)) { return r + 1 == nb ? 0 : r + 1; };
   // The lead group issues its DMA share after the first barrier, at the start of its
   // softmax phase, so its MFMA phase starts right after the barrier that opens it.
   if (lead) {
     if (live(0)) s_part(0);
     __syncthreads();
-    issue(0, 0);
+    issue(0);
     if (live(0)) xphase(0);
     settle(0);
-    int u = 1, r = 1;
-    for (; u <= hot; ++u, r = r == NB - 1 ? 0 : r + 1) {
-      m_full(r, r == 0 ? NB - 1 : r - 1);
+    int u = 1, rk = 1 % NBK, rv = 0;
+    for (; u <= hot; ++u, rk = next(rk, NBK), rv = next(rv, NBV)) {
+      m_full(rk, rv);
       __syncthreads();
-      issue(u, r);
+      issue(u);
       xphase(u);
       settle(u);
     }
-    for (; u <= n_tiles; ++u, r = r == NB - 1 ? 0 : r + 1) {
-      if (live(u - 1)) pv_part(r == 0 ? NB - 1 : r - 1);
+    for (; u <= n_tiles; ++u, rv = next(rv, NBV)) {
+      if (live(u - 1)) pv_part(rv);
       __syncthreads();
-      issue(u, r);
+      issue(u);
       settle(u);
     }
   } else {
-    issue(0, 0);
+    issue(0);
     __syncthreads();
     if (live(0)) s_part(0);
     settle(0);
-    int u = 1, r = 1;
-    for (; u <= hot; ++u, r = r == NB - 1 ? 0 : r + 1) {
-      issue(u, r);
+    int u = 1, rk = 1 % NBK, rv = 0;
+    for (; u <= hot; ++u, rk = next(rk, NBK), rv = next(rv, NBV)) {
+      issue(u);
       xphase(u - 1);
       __syncthreads();
-      m_full(r, r == 0 ? NB - 1 : r - 1);
+      m_full(rk, rv);
       settle(u);
     }
-    for (; u <= n_tiles; ++u, r = r == NB - 1 ? 0 : r + 1) {
-      issue(u, r);
+    for (; u <= n_tiles; ++u, rv = next(rv, NBV)) {
+      issue(u);
       if (live(u - 1)) xphase(u - 1);
       __syncthreads();
-      if (live(u - 1)) pv_part(r == 0 ? NB - 1 : r - 1);
+      if (live(u - 1)) pv_part(rv);
       settle(u);
     }
   }
