@@ -487,8 +487,10 @@ def copy_calibration():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    # The first few c3 steps on a fresh box run 2-7% slower than later ones (measured in
+    # the kernel trace); the default warmup covers them.
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
