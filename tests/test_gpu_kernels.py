@@ -114,17 +114,23 @@ def test_block_partial_accumulate_is_positioned_merge(gpu):
     assert np.abs(l2.cpu().numpy() - ref_l.T).max() <= LSE_TOL
 
 
-def test_lse_merge_matches_closed_form(gpu):
-    rng = np.random.default_rng(4)
-    h, l, d, n = 8, 333, 128, 5
+@pytest.mark.parametrize("h,l,n", [(8, 333, 5), (3, 37, 1), (1, 45, 2), (5, 21, 9)],
+                         ids=["five_parts", "one_part_odd_rows", "two_parts_odd_rows", "nine_parts_two_groups"])
+def test_lse_merge_matches_closed_form(gpu, h, l, n):
+    # row counts h * l both even and odd (each thread merges two consecutive rows), and
+    # part counts for every group size of the kernel (1, 2, 4, 8 and a second group)
+    rng = np.random.default_rng(4 + n)
+    d = 128
     os_ = [rng.standard_normal((h, l, d)).astype(np.float32) for _ in range(n)]
     ls = [rng.normal(3.0, 2.0, (h, l)).astype(np.float32) for _ in range(n)]
-    ls[1][:, :40] = -np.inf       # an empty partial on some rows
+    e = n - 1                     # an empty partial on some rows
+    ls[e][:, : l // 3] = -np.inf
+    os_[e][:, : l // 3] = 0
+    dead = l // 2                 # a row with no keys at all
     for x in ls:
-        x[0, 100] = -np.inf       # a row with no keys at all
-    os_[1][:, :40] = 0
+        x[0, dead] = -np.inf
     for x in os_:
-        x[0, 100] = 0
+        x[0, dead] = 0
     out, lse = H.lse_merge([torch.from_numpy(x).cuda() for x in os_], [torch.from_numpy(x).cuda() for x in ls],
                            out_dtype=torch.bfloat16)
     out32, lse32 = H.lse_merge([torch.from_numpy(x).cuda() for x in os_], [torch.from_numpy(x).cuda() for x in ls],
@@ -135,7 +141,7 @@ def test_lse_merge_matches_closed_form(gpu):
     # bf16 output: within one bf16 rounding (relative 2^-8) of the f64 merge
     assert np.all(np.abs(out.float().cpu().numpy() - ref_o) <= np.abs(ref_o) * 2.0**-8 + 1e-6)
     lse = lse.cpu().numpy()
-    assert lse[0, 100] == -np.inf and np.all(out.float().cpu().numpy()[0, 100] == 0)
+    assert lse[0, dead] == -np.inf and np.all(out.float().cpu().numpy()[0, dead] == 0)
     fin = np.isfinite(ref_l)
     assert np.abs(lse[fin] - ref_l[fin]).max() < 1e-5
 
