@@ -131,3 +131,41 @@ def test_runtime_smoke_and_init_validation():
     bad = H.RingAttnRuntime("cpu")
     with pytest.raises(H.HcpRingError):
         bad.init(0, ids, lens, 2, 8, torch.float32)
+
+
+# Every entry point that takes a descriptor, pool, count or handle rejects a null or
+# zero one with status -6 (invalid arguments, the rust_bridge.cc:109-128 meaning) and
+# a message naming itself, before any device work.
+NULL_CHECKED = [
+    "hcp_ring_block_partial", "hcp_ring_block_partial_positioned", "hcp_ring_lse_merge",
+    "hcp_paged_kv_gather", "hcp_paged_kv_scatter", "hcp_paged_kv_gather_batch",
+    "hcp_paged_decode_partial", "hcp_decode_ring_replay", "hcp_ring_prefill_replay",
+    "hcp_ring_prefill_replay_paged", "hcp_kv_frame_header", "hcp_kv_frame_parse",
+    "hcp_kv_frame_pack", "hcp_kv_frame_unpack", "hcp_packet_frame_header",
+    "hcp_packet_frame_parse", "hcp_packet_frame_pack", "hcp_packet_frame_unpack",
+    "hcp_qkv_rope_project", "hcp_qkv_rope_project_paged", "hcp_ring_build_assignment",
+    "hcp_ring_domain_positions", "hcp_ring_inverse_perm", "hcp_rope_table",
+    "hcp_ringattn_runtime_init", "hcp_ringattn_runtime_bind_layer",
+    "hcp_ringattn_runtime_run_layer", "hcp_ringattn_runtime_shutdown",
+]
+
+
+def _null_args(fn, view_type):
+    args = []
+    for t in fn.argtypes:
+        if t is view_type:
+            args.append(view_type(None, 0, 1))
+        elif t in (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_size_t, ctypes.c_double,
+                   ctypes.c_float, ctypes.c_int):
+            args.append(0)
+        else:
+            args.append(None)
+    return args
+
+
+@pytest.mark.parametrize("name", NULL_CHECKED)
+def test_null_or_zero_arguments_are_invalid(hcp, name):
+    fn = getattr(hcp.lib(), name)
+    rc = fn(*_null_args(fn, hcp.View))
+    assert rc == -6, (name, rc, hcp.last_error())
+    assert hcp.last_error().startswith(name + ":"), hcp.last_error()
