@@ -35,7 +35,8 @@ METRIC = "ring-prefill TFLOP/s (% MFMA peak) at 32k; paged-decode GB/s (% HBM pe
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU (dense)
 PEAK_HBM_GBS = 8000.0
 
-C3 = dict(chunks=[12288, 8192, 8192, 4096], hq=32, hkv=8, d=128, seed=44)
+C2 = dict(name="c2", chunks=[4096, 2560, 1536], hq=16, hkv=2, d=128, seed=43)
+C3 = dict(name="c3", chunks=[12288, 8192, 8192, 4096], hq=32, hkv=8, d=128, seed=44)
 C4 = dict(batch=64, hq=32, hkv=8, d=128, bs=16, ctx=16384, chunks=[8192, 5120, 3072],
           pool_blocks=65536, seed=45)
 C5 = dict(chunks=[21504, 13312, 18432, 23552, 24576, 9216, 8192, 12288], hq=32, hkv=8, d=128,
@@ -97,32 +98,39 @@ def time_cuda(torch, fn, reps: int) -> float:
 
 
 # ------------------------------------------------------------------ c3 prefill ----
-def bench_prefill(H, torch, steps: int, warmup: int):
-    c = C3
+def bench_prefill(H, torch, steps: int, warmup: int, c=None, schedule: str = "auto", tensors=None):
+    """One ring replay per step (``schedule`` "auto": the fused single launch; "per_step":
+    one grouped launch per ring step), inputs resident in HBM.  Whole-step time from the
+    wall clock between synchronisations, then the same steps again with HIP events
+    around every block-kernel launch for the kernel's own average launch time."""
+    c = c or C3
     seq = sum(c["chunks"])
-    q, k, v = synth_qkv(H, torch, seq, c["hq"], c["hkv"], c["d"], c["seed"])
+    if tensors is None:
+        tensors = synth_qkv(H, torch, seq, c["hq"], c["hkv"], c["d"], c["seed"])
+    q, k, v = tensors
     qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
-    ws = torch.empty(H.replay_workspace_size(torch.bfloat16, c["hq"], c["hkv"], c["d"], c["chunks"]),
-                     dtype=torch.uint8, device="cuda")
+    ws = torch.empty(max(H.replay_workspace_size(torch.bfloat16, c["hq"], c["hkv"], c["d"], c["chunks"],
+                                                 schedule=schedule), 1), dtype=torch.uint8, device="cuda")
     out = torch.empty(c["hq"], seq, c["d"], dtype=torch.bfloat16, device="cuda")
     lse = torch.empty(c["hq"], seq, dtype=torch.float32, device="cuda")
-    step = lambda: H.ring_attention_replay(qh, kh, vh, c["chunks"], out=out, lse_out=lse, workspace=ws)
-    log(f"c3 prefill warmup x{warmup}")
+    step = lambda: H.ring_attention_replay(qh, kh, vh, c["chunks"], out=out, lse_out=lse, workspace=ws,
+                                           schedule=schedule)
+    tag = f"{c.get('name', 'c3')} prefill ({schedule})"
+    log(f"{tag} warmup x{warmup}")
     for _ in range(warmup):
         step()
+    path = H.last_path()
     torch.cuda.synchronize()
     # whole-step time without instrumentation (per-launch events add ~10 us between launches)
-    log(f"c3 prefill timed x{steps}")
+    log(f"{tag} timed x{steps}")
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    # then the same steps with HIP events around every block launch, for the kernel's own
-    # average launch time (the roofline)
     H.replay_timing(True)
     H.replay_timing_read()
-    log(f"c3 prefill per-launch timing x{steps}")
+    log(f"{tag} per-launch timing x{steps}")
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
@@ -135,15 +143,38 @@ def bench_prefill(H, torch, steps: int, warmup: int):
     per_launch_flops = flops * steps / blk_n
     avg_blk_ms = blk_ms / blk_n
     achieved = per_launch_flops / (avg_blk_ms * 1e-3) / 1e12
-    n = len(c["chunks"])
-    offs = [sum(c["chunks"][:i]) for i in range(n)]
-    blk_bytes = sum(b for _, _, b in block_launch_bytes(c))
+    if path == "ring_fused":
+        # compulsory traffic of the one launch: Q, K and V read once, output rows and LSE written
+        blk_bytes = seq * (c["hq"] * c["d"] * 2 * 2 + 2 * c["hkv"] * c["d"] * 2 + c["hq"] * 4)
+    else:
+        blk_bytes = sum(b for _, _, b in block_launch_bytes(c))
     finite = bool(torch.isfinite(lse).all().item()) and bool(torch.isfinite(out.float()).all().item())
     del ws
-    return dict(ms_step=ms_step, tflops=tflops, flops=flops, blk_launches=blk_n // steps,
+    return dict(ms_step=ms_step, tflops=tflops, flops=flops, blk_launches=blk_n // steps, path=path,
                 avg_blk_ms=avg_blk_ms, per_launch_flops=per_launch_flops, achieved=achieved, finite=finite,
-                alg_bytes_per_launch=blk_bytes * steps // blk_n,
-                tensors=(q, k, v))
+                alg_bytes_per_launch=blk_bytes * steps // blk_n, tensors=tensors, out=out, lse=lse)
+
+
+def prefill_summary(r):
+    """JSON object of a prefill leg (TFLOP/s of the whole step, and of the block kernel
+    from its own launch times)."""
+    return {"value": round(r["tflops"], 1), "unit": "TFLOP/s", "ms_per_step": round(r["ms_step"], 4),
+            "frac_mfma": round(r["tflops"] / PEAK_BF16_TFLOPS, 4), "kernel_path": r["path"],
+            "launches_per_step": r["blk_launches"], "kernel_tflops": round(r["achieved"], 1),
+            "finite": r["finite"]}
+
+
+def bench_c2(H, torch, steps: int, warmup: int):
+    """Config c2 (Qwen2.5-3B shape): S=8192 in [4096, 2560, 1536], 16 q / 2 kv heads, D=128,
+    bf16, causal, seed 43 -- both schedules."""
+    fused = bench_prefill(H, torch, steps, warmup, C2, "auto")
+    per = bench_prefill(H, torch, steps, warmup, C2, "per_step", tensors=fused["tensors"])
+    log(f"c2 prefill {fused['tflops']:.1f} TFLOP/s fused, {per['tflops']:.1f} per step")
+    res = {"workload": "c2: S=8192 in [4096,2560,1536], 16q/2kv heads, D=128, bf16, causal",
+           **prefill_summary(fused), "per_step": prefill_summary(per),
+           "max_abs_diff_schedules": round((fused["out"].float() - per["out"].float()).abs().max().item(), 5)}
+    del fused, per
+    return res
 
 
 def block_launch_bytes(c):
@@ -407,14 +438,57 @@ def bench_staged(H, torch, steps: int, warmup: int, full_prefill: bool = True):
         run = lambda: H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, c["chunks"], out=out,
                                                     lse_out=lse, workspace=ws)
         run()
-        reps = 2
+        path = H.last_path()
+        reps = 3
         ms_p = time_cuda(torch, run, reps)
-        res.update(prefill_ms=ms_p, prefill_tflops=causal_flops(seq, c["hq"], d) / (ms_p * 1e-3) / 1e12)
+        res.update(prefill_ms=ms_p, prefill_tflops=causal_flops(seq, c["hq"], d) / (ms_p * 1e-3) / 1e12,
+                   prefill_path=path,
+                   prefill_finite=bool(torch.isfinite(lse).all().item()) and bool(torch.isfinite(out.float()).all().item()))
+        # a few rows at domain boundaries against the f64 closed form (the parity tests check more)
+        rows = [offs[1] - 1, offs[4], offs[7], seq - 1]
+        e_o, e_l = sampled_rows_error(q, k, v, out, lse, rows)
+        res.update(sampled_rows=rows, sampled_err_out=e_o, sampled_err_lse=e_l)
         del ws
     return res
 
 
+def sampled_rows_error(q, k, v, out, lse, rows):
+    """Max |out - f64| and |lse - f64| over query rows `rows` of a causal vanilla replay
+    (q [S, Hq, D], k/v [S, Hkv, D]; out [Hq, S, D], lse [Hq, S]), all heads."""
+    import numpy as np
+    hq, hkv, d = q.shape[1], k.shape[1], q.shape[2]
+    rep = hq // hkv
+    k64 = k.double().cpu().numpy()
+    v64 = v.double().cpu().numpy()
+    e_o = e_l = 0.0
+    for r in rows:
+        qr = q[r].double().cpu().numpy()
+        go = out[:, r].double().cpu().numpy()
+        gl = lse[:, r].double().cpu().numpy()
+        for g in range(hkv):
+            s_ = qr[g * rep:(g + 1) * rep] @ k64[: r + 1, g].T / math.sqrt(d)
+            m = s_.max(axis=1, keepdims=True)
+            w = np.exp(s_ - m)
+            den = w.sum(axis=1, keepdims=True)
+            o = (w @ v64[: r + 1, g]) / den
+            e_o = max(e_o, float(np.abs(go[g * rep:(g + 1) * rep] - o).max()))
+            e_l = max(e_l, float(np.abs(gl[g * rep:(g + 1) * rep] - (m + np.log(den))[:, 0]).max()))
+    return round(e_o, 6), round(e_l, 7)
+
+
 # ------------------------------------------------------------------ CPU baseline ----
+def cpu_model() -> str:
+    """The host CPU's model string (/proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(torch, tensors, budget_s: float = 10.0):
     """The oracle's op-for-op libtorch restatement of ring.rs (ring_attention driver,
     process_kv_block folds, bf16 state, 2048 tiling, GQA-expand copies) on this host:
@@ -451,6 +525,7 @@ def cpu_baseline(torch, tensors, budget_s: float = 10.0):
         if t_total >= budget_s:
             break
     return dict(value=flops / t_total / 1e12, unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                nproc=os.cpu_count(), cpu_model=cpu_model(),
                 sample=f"c3 ring_attention of target domains {done} (of 4), op-for-op libtorch restatement of "
                        f"ring.rs:861-1398 (bf16 state, 2048 q/kv tiles, GQA-expanded K/V), {t_total:.1f} s; "
                        f"algorithmic causal FLOPs of those domains / time")
@@ -513,9 +588,18 @@ def main():
     torch.cuda.set_device(0)
     log(f"device {torch.cuda.get_device_name(0)}")
     pre = bench_prefill(H, torch, args.steps, args.warmup)
-    log(f"c3 prefill {pre['tflops']:.1f} TFLOP/s ({pre['ms_step']:.3f} ms/step)")
+    log(f"c3 prefill {pre['tflops']:.1f} TFLOP/s ({pre['ms_step']:.3f} ms/step, {pre['path']})")
     extra = {}
     if not args.no_extra:
+        # the same c3 replay under the per-step schedule (one grouped launch per ring step)
+        per = bench_prefill(H, torch, args.steps, args.warmup, schedule="per_step", tensors=pre["tensors"])
+        log(f"c3 prefill per step {per['tflops']:.1f} TFLOP/s")
+        c3_per_step = dict(workload="c3 with schedule per_step (one grouped launch per ring step, fp32 state "
+                                    "in HBM between steps)", **prefill_summary(per),
+                           max_abs_diff_vs_fused=round((per["out"].float() - pre["out"].float()).abs().max().item(),
+                                                       5))
+        del per
+        c2 = bench_c2(H, torch, args.steps, args.warmup)
         dec = bench_decode(H, torch, args.steps, args.warmup)
         log(f"c4 decode {dec['gbs']:.1f} GB/s")
         stg = bench_staged(H, torch, args.steps, args.warmup)
@@ -539,9 +623,17 @@ def main():
                         "frac_hbm": round(stg["gather_gbs"] / PEAK_HBM_GBS, 4), "bytes": stg["gather_bytes"],
                         "bit_exact": stg["bit_exact"], "scatter_gbs": round(stg["scatter_gbs"], 1),
                         "scatter_ms": round(stg["scatter_ms"], 4)},
-            staged_prefill_128k={"value": round(stg.get("prefill_tflops", 0.0), 1), "unit": "TFLOP/s",
+            staged_prefill_128k={"workload": "c5: every chunk gathered from the paged pool (one batched launch), "
+                                             "then the fused ring over 131072 tokens in 8 domains",
+                                 "value": round(stg.get("prefill_tflops", 0.0), 1), "unit": "TFLOP/s",
                                  "ms": round(stg.get("prefill_ms", 0.0), 3),
-                                 "frac_mfma": round(stg.get("prefill_tflops", 0.0) / PEAK_BF16_TFLOPS, 4)},
+                                 "frac_mfma": round(stg.get("prefill_tflops", 0.0) / PEAK_BF16_TFLOPS, 4),
+                                 "kernel_path": stg.get("prefill_path"), "finite": stg.get("prefill_finite"),
+                                 "sampled_rows": stg.get("sampled_rows"),
+                                 "sampled_max_abs_err_out": stg.get("sampled_err_out"),
+                                 "sampled_max_abs_err_lse": stg.get("sampled_err_lse")},
+            c2_prefill=c2,
+            c3_per_step=c3_per_step,
             lse_merge={"workload": "c3 ring partials of the 4 target domains (10 x [32, L, 128] fp32 + LSE) "
                                    "-> bf16 rows + fp32 LSE, one hcp_ring_lse_merge per domain",
                        "value": round(mrg["merge_gbs"], 1), "unit": "GB/s", "ms_per_step": round(mrg["merge_ms"], 4),
@@ -570,10 +662,12 @@ def main():
         "config": {"workload": "c3_llama3_8b_ring_prefill_32k", "chunks": C3["chunks"], "num_q_heads": C3["hq"],
                    "num_kv_heads": C3["hkv"], "head_dim": C3["d"], "causal": True,
                    "flops_per_step": pre["flops"], "frac_mfma_peak": round(pre["tflops"] / PEAK_BF16_TFLOPS, 4)},
-        "roofline": {"bound": "mfma", "kernel": "flash_block_pingpong_kernel",
+        "roofline": {"bound": "mfma",
+                     "kernel": "flash_ring_kernel" if pre["path"] == "ring_fused" else "flash_block_pingpong_kernel",
                      "achieved": round(pre["achieved"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(pre["achieved"] / PEAK_BF16_TFLOPS, 4),
-                     "traffic": profiled_traffic("flash_block_kernel_c3_prefill.md"),
+                     "traffic": profiled_traffic("flash_ring_kernel_c3_prefill.md" if pre["path"] == "ring_fused"
+                                                 else "flash_block_kernel_c3_prefill.md"),
                      "algorithmic_bytes_per_launch": pre["alg_bytes_per_launch"],
                      "launches_per_step": pre["blk_launches"], "avg_launch_ms": round(pre["avg_blk_ms"], 4),
                      "flops_per_launch": pre["per_launch_flops"]},

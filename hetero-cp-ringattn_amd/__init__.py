@@ -94,7 +94,7 @@ class ReplayDesc(ctypes.Structure):
                 ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
                 ("num_domains", ctypes.c_int32), ("causal", ctypes.c_int32),
                 ("chunk_lens", ctypes.POINTER(ctypes.c_int64)), ("scale", ctypes.c_float),
-                ("strategy", ctypes.c_int32)]
+                ("strategy", ctypes.c_int32), ("schedule", ctypes.c_int32)]
 
 
 class KvFrameDesc(ctypes.Structure):
@@ -118,6 +118,23 @@ class QkvDesc(ctypes.Structure):
 
 # RingSchedulingStrategy (strategy.rs:14-24) -> HCP_STRATEGY_*
 STRATEGIES = {"vanilla": 0, "striped": 1, "zigzag": 2}
+
+
+SCHEDULES = {"auto": 0, "per_step": 1, "fused": 2}
+PATHS = {0: "none", 1: "mfma", 2: "ring_fused", 3: "general"}
+
+
+def schedule_code(schedule) -> int:
+    """HCP_SCHEDULE_* of a name ("auto", "per_step", "fused") or an int."""
+    if isinstance(schedule, int):
+        return schedule
+    return SCHEDULES[schedule]
+
+
+def last_path() -> str:
+    """Kernel path of this thread's last attention call ("mfma", "ring_fused",
+    "general" -- the scalar fp32 kernel -- or "none"), hcp_ring_last_path."""
+    return PATHS[lib().hcp_ring_last_path()]
 
 
 def strategy_code(strategy) -> int:
@@ -144,6 +161,7 @@ def lib() -> ctypes.CDLL:
     sig = {
         "hcp_ring_last_error": ([], ctypes.c_char_p),
         "hcp_ring_abi_version": ([], ctypes.c_int),
+        "hcp_ring_last_path": ([], ctypes.c_int),
         "hcp_ring_device_count": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
         "hcp_ring_fetch_device_errors": ([vp, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
         "hcp_ring_block_partial": ([ctypes.POINTER(BlockDesc), View, View, View, vp, vp, vp],
@@ -508,29 +526,33 @@ def decode_ring_replay(q, pool, shards, seed_domain, scale=None, out=None, lse_o
 # ---------------------------------------------------------------------------------
 # (5) ring replay
 # ---------------------------------------------------------------------------------
-def replay_desc(dtype, hq, hkv, d, chunks, causal=True, scale=None, strategy="vanilla"):
+def replay_desc(dtype, hq, hkv, d, chunks, causal=True, scale=None, strategy="vanilla", schedule="auto"):
     arr = (ctypes.c_int64 * len(chunks))(*chunks)
     desc = ReplayDesc(dtype_code(dtype), hq, hkv, d, len(chunks), 1 if causal else 0, arr,
-                      scale if scale is not None else 1.0 / math.sqrt(d), strategy_code(strategy))
+                      scale if scale is not None else 1.0 / math.sqrt(d), strategy_code(strategy),
+                      schedule_code(schedule))
     return desc, arr
 
 
-def replay_workspace_size(dtype, hq, hkv, d, chunks, causal=True, paged=False, strategy="vanilla") -> int:
-    desc, _arr = replay_desc(dtype, hq, hkv, d, chunks, causal, strategy=strategy)
+def replay_workspace_size(dtype, hq, hkv, d, chunks, causal=True, paged=False, strategy="vanilla",
+                          schedule="auto") -> int:
+    desc, _arr = replay_desc(dtype, hq, hkv, d, chunks, causal, strategy=strategy, schedule=schedule)
     return lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 1 if paged else 0)
 
 
 def ring_attention_replay(q, k, v, chunks, causal=True, scale=None, out=None, lse_out=None,
-                          workspace=None, stream=None, strategy="vanilla"):
+                          workspace=None, stream=None, strategy="vanilla", schedule="auto"):
     """Every domain's ring on one GPU.  q [Hq, S, D], k/v [Hkv, S, D] (strided views ok)
     -> (out [Hq, S, D] in q's dtype, lse [Hq, S] fp32).
 
     Rows are in domain-major order (row r = position ``domain_positions(chunks,
-    strategy)[r]``; the global order for "vanilla"); ``inverse_perm`` maps back."""
+    strategy)[r]``; the global order for "vanilla"); ``inverse_perm`` maps back.
+    ``schedule``: "auto" (one fused launch where it applies), "per_step" (one grouped
+    launch per ring step) or "fused"."""
     torch = _torch()
     hq, s, d = q.shape
     hkv = k.shape[0]
-    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale, strategy)
+    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale, strategy, schedule)
     need = lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 0)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
@@ -546,13 +568,14 @@ def ring_attention_replay(q, k, v, chunks, causal=True, scale=None, out=None, ls
 
 
 def ring_attention_replay_paged(q, pool, block_table, chunks, causal=True, scale=None, out=None,
-                                lse_out=None, workspace=None, stream=None, strategy="vanilla"):
-    """As :func:`ring_attention_replay`, K/V gathered per ring step from a paged pool
-    (the pool holds the sequence in the same domain-major order)."""
+                                lse_out=None, workspace=None, stream=None, strategy="vanilla", schedule="auto"):
+    """As :func:`ring_attention_replay`, K/V gathered from a paged pool (the pool holds
+    the sequence in the same domain-major order): per ring step with "per_step", every
+    chunk once before the fused launch otherwise."""
     torch = _torch()
     hq, s, d = q.shape
     hkv = pool.shape[3]
-    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale, strategy)
+    desc, arr = replay_desc(q.dtype, hq, hkv, d, chunks, causal, scale, strategy, schedule)
     need = lib().hcp_ring_replay_workspace_size(ctypes.byref(desc), 1)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)

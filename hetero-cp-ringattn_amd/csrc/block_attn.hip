@@ -226,7 +226,8 @@ __device__ __forceinline__ void write_row(const BlockArgs& a, int head, int my_q
   const float inv = any ? 1.f / l_tot : 0.f;
   const float lse_new = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
   const int64_t row = static_cast<int64_t>(head) * a.lq + my_q;
-  float* orow = a.o + row * D;
+  // the running fp32 state (null in a fused ring, which writes final rows only)
+  float* orow = a.o != nullptr ? a.o + row * D : nullptr;
   float c_old = 0.f, c_new = inv, lse_out = lse_new;
   if (a.accumulate) {
     const float lse_old = a.lse[row];
@@ -262,6 +263,26 @@ __device__ __forceinline__ void write_row(const BlockArgs& a, int head, int my_q
       a.lse[row] = lse_out;
     }
   }
+}
+
+// Final-mode epilogue of one (head, query row) of a fused ring: normalised output row
+// in `dtype` at element offset `off` of `out`, natural-log LSE to *lse (if non-null);
+// lanes l and l + 32 hold the two interleaved 4-wide d slices of each 8-wide group.
+template <int D>
+__device__ __forceinline__ void write_final_row(void* out, int dtype, int64_t off, float* lse, int lhalf,
+                                                const f32x16 (&oacc)[D / 32], float m_run, float l_tot) {
+  constexpr int DB = D / 32;
+  const bool any = l_tot > 0.f;
+  const float inv = any ? 1.f / l_tot : 0.f;
+#pragma unroll
+  for (int b = 0; b < DB; ++b)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int dcol = 32 * b + 8 * j + 4 * lhalf;
+      store4(out, dtype, off + dcol, inv * oacc[b][4 * j], inv * oacc[b][4 * j + 1], inv * oacc[b][4 * j + 2],
+             inv * oacc[b][4 * j + 3]);
+    }
+  if (lhalf == 0 && lse != nullptr) *lse = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
 }
 
 template <int D, int DT, int G, bool POS>
@@ -553,8 +574,38 @@ __device__ __forceinline__ int simd_id() {
   return r;
 }
 
-template <int DT, int G, bool POS, int BK>
-__global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockGroup grp) {
+// Fused single-GPU ring replay (vanilla positions): every target domain's ring in one
+// launch.  A workgroup owns one query tile of one target domain t and folds that
+// target's sources in ring order -- t, t-1, ..., t-N+1 (mod N), the order in which
+// ring_attention receives them (ring.rs:1208-1311, mock.rs:143-149) -- skipping keys
+// wholly in its future (ring.rs:222-228); the running (m, l, O) stays in registers
+// across sources and the last tile writes the output rows and the LSE.  With the
+// domains' chunks stored in order, the keys of sources t-1, t-2, ..., 0 are the rows
+// [0, off_t) of the K/V views read backwards, and (without causal masking) those of
+// t-1 wrapping round to t+1 are then [off_t + len_t, S) read backwards: the 128-key
+// tiles after the local source are taken from the top of that range down, so each
+// source is folded whole, after its successor in the ring, and a tile's rows follow
+// from its index alone.  Workgroups are numbered tile-rank-major over head groups, so
+// blockIdx b goes to XCD b mod 8 with the heavier (later) query tiles first on every XCD.
+struct RingPlan {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t q_hs, q_ss, k_hs, k_ss, v_hs, v_ss;  // element strides (whole-sequence views)
+  void* out;
+  int64_t out_hs, out_ss;
+  float* lse;                                   // [Hq, S] rows, or null
+  int64_t lse_hs;
+  int32_t dtype;                                // query / output dtype
+  int32_t hq, hkv, rep, n_groups, n, causal;
+  float scale_log2;
+  int32_t off[kMaxDomains], len[kMaxDomains];   // rows (= global positions) of each domain
+  int32_t qt_begin[kMaxDomains + 1];            // query tiles of slot s (domain n-1-s)
+};
+static_assert(sizeof(RingPlan) <= 4096, "kernel arguments are limited to 4 KiB");
+
+template <int DT, int G, bool POS, int BK, bool RING, class P>
+__device__ __forceinline__ void pingpong_body(const P& plan) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
   constexpr int D = kD3;
@@ -577,36 +628,110 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   int* const lim_red = reinterpret_cast<int*>(v_lds + (NBV - 1) * BK * D);
   int* const simd_of = lim_red + kWaves;
 
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int per_hg = grp.qt_begin[grp.n];
-  const int hg = logical / per_hg;
-  const int rem = logical - hg * per_hg;
-  int pi = 0;
-  while (pi + 1 < grp.n && rem >= grp.qt_begin[pi + 1]) ++pi;
-  const BlockArgs& a = grp.a[pi];
-  const int qt = a.n_qtiles - 1 - (rem - grp.qt_begin[pi]);
-
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int lcol = lane & 31;
   const int lhalf = lane >> 5;
 
+  // ---- work item: head group, query tile, and the views it reads ----
+  int hg, qt, t_dom = 0;
+  const BlockArgs* ap = nullptr;  // block mode: the block of this workgroup
+  const uint16_t *qv, *kv, *vv;
+  int64_t q_hs, q_ss, k_hs, k_ss, v_hs, v_ss;
+  int lq, rep, causal;
+  float c;
+  if constexpr (RING) {
+    const int logical = blockIdx.x;
+    hg = logical % plan.n_groups;
+    const int rank = logical / plan.n_groups;
+    int slot = 0;
+    while (slot + 1 < plan.n && rank >= plan.qt_begin[slot + 1]) ++slot;
+    t_dom = plan.n - 1 - slot;
+    qt = plan.qt_begin[slot + 1] - 1 - rank;  // a domain's last (heaviest) tile first
+    qv = plan.q + static_cast<int64_t>(plan.off[t_dom]) * plan.q_ss;
+    kv = plan.k; vv = plan.v;
+    q_hs = plan.q_hs; q_ss = plan.q_ss; k_hs = plan.k_hs; k_ss = plan.k_ss; v_hs = plan.v_hs; v_ss = plan.v_ss;
+    lq = plan.len[t_dom];
+    rep = plan.rep;
+    causal = plan.causal;
+    c = plan.scale_log2;
+  } else {
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int per_hg = plan.qt_begin[plan.n];
+    hg = logical / per_hg;
+    const int rem = logical - hg * per_hg;
+    int pi = 0;
+    while (pi + 1 < plan.n && rem >= plan.qt_begin[pi + 1]) ++pi;
+    ap = &plan.a[pi];
+    qt = ap->n_qtiles - 1 - (rem - plan.qt_begin[pi]);
+    qv = ap->q; kv = ap->k; vv = ap->v;
+    q_hs = ap->q_hs; q_ss = ap->q_ss; k_hs = ap->k_hs; k_ss = ap->k_ss; v_hs = ap->v_hs; v_ss = ap->v_ss;
+    lq = ap->lq;
+    rep = ap->rep;
+    causal = ap->causal;
+    c = ap->scale_log2;
+  }
+
   const int head = hg * G + (wave % G);
-  const int kvh = (hg * G) / a.rep;
+  const int kvh = (hg * G) / rep;
   const int tq0 = qt * TQ;
   const int wq0 = tq0 + (wave / G) * 32;
   const int my_q = wq0 + lcol;
-  const int q_end = min(a.lq, tq0 + TQ);
+  const int q_end = min(lq, tq0 + TQ);
 
   if (lane == 0) simd_of[wave] = simd_id();
-  const RowLimits rl = row_limits<POS>(a, q_end, wq0, my_q, wave, lane, lim_red);
-  const int n_kv = rl.n_kv;
-  const int n_tiles = (n_kv + BK - 1) / BK;
+  RowLimits rl;
+  if constexpr (RING) {
+    rl.n_kv = 0;
+    rl.lane = rl.wave_first = rl.wave_last = 0;
+  } else {
+    rl = row_limits<POS>(*ap, q_end, wq0, my_q, wave, lane, lim_red);
+  }
+
+  // ---- key tiles ----
+  // Tiles 0 .. nt0-1 cover the rows [b0, e0) of the local source (the block's chunk), in
+  // order; in a fused ring, tiles nt0 .. nt0+na-1 then walk [0, off_t) from the top
+  // down and, without causal masking, the rest walk [off_t + len_t, S) the same way (the
+  // lowest tile of each range may be partial).  Key row r of the K/V views lies
+  // r + kdelta positions after query row 0 of the workgroup's block.
+  int b0, e0, na = 0, nb = 0, top_b = 0, low_b = 0;
+  int64_t kdelta;
+  if constexpr (RING) {
+    const int off_t = plan.off[t_dom];
+    b0 = off_t;
+    e0 = off_t + (causal ? q_end : lq);
+    na = (off_t + BK - 1) / BK;
+    if (!causal) {
+      low_b = off_t + lq;
+      top_b = plan.off[plan.n - 1] + plan.len[plan.n - 1];
+      nb = (top_b - low_b + BK - 1) / BK;
+    }
+    kdelta = -static_cast<int64_t>(off_t);
+  } else {
+    b0 = 0;
+    e0 = rl.n_kv;
+    kdelta = ap->k_off - ap->q_off;
+  }
+  const int nt0 = (e0 - b0 + BK - 1) / BK;
+  const int n_tiles = nt0 + na + nb;
+  // rows [kr, ke) of tile t (the keys visible to some row of the workgroup)
+  auto tile_rows = [&](int t, int& kr, int& ke) __attribute__((always_inline)) {
+    if (!RING || t < nt0) {
+      kr = b0 + t * BK;
+      ke = e0;
+    } else if (t < nt0 + na) {
+      ke = b0 - (t - nt0) * BK;
+      kr = max(ke - BK, 0);
+    } else {
+      ke = top_b - (t - nt0 - na) * BK;
+      kr = max(ke - BK, low_b);
+    }
+  };
 
   // ---- DMA set-up: wave w fills rows 8w .. 8w+7 of every K and V tile ----
-  const uint16_t* kbase = a.k + kvh * a.k_hs;
-  const uint16_t* vbase = a.v + kvh * a.v_hs;
+  const uint16_t* kbase = kv + kvh * k_hs;
+  const uint16_t* vbase = vv + kvh * v_hs;
   const uint32_t k_lds0 = lds_offset(k_lds) + wave * (kDmaPerWave * 1024);
   const uint32_t v_lds0 = lds_offset(v_lds) + wave * (kDmaPerWave * 1024);
   uint32_t k_voff[kDmaPerWave], v_voff[kDmaPerWave];
@@ -614,18 +739,20 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   for (int j = 0; j < kDmaPerWave; ++j) {
     const int r = (wave * kDmaPerWave + j) * 4 + (lane >> 4);
     const int p = lane & 15;
-    k_voff[j] = static_cast<uint32_t>(r * a.k_ss * 2 + ((p ^ (r & 15)) << 4));
-    v_voff[j] = static_cast<uint32_t>(r * a.v_ss * 2 + ((p ^ (4 * (r & 3))) << 4));
+    k_voff[j] = static_cast<uint32_t>(r * k_ss * 2 + ((p ^ (r & 15)) << 4));
+    v_voff[j] = static_cast<uint32_t>(r * v_ss * 2 + ((p ^ (4 * (r & 3))) << 4));
   }
   auto issue_k = [&](int t, int buf) __attribute__((always_inline)) {
-    const int kv0 = t * BK;
-    const u32x4 s = make_srd(kbase + static_cast<int64_t>(kv0) * a.k_ss, static_cast<int64_t>(a.lk - kv0) * a.k_ss * 2);
+    int kr, ke;
+    tile_rows(t, kr, ke);
+    const u32x4 s = make_srd(kbase + static_cast<int64_t>(kr) * k_ss, static_cast<int64_t>(ke - kr) * k_ss * 2);
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) dma16(s, k_voff[j], k_lds0 + buf * kTile + j * 1024);
   };
   auto issue_v = [&](int t, int buf) __attribute__((always_inline)) {
-    const int kv0 = t * BK;
-    const u32x4 s = make_srd(vbase + static_cast<int64_t>(kv0) * a.v_ss, static_cast<int64_t>(a.lk - kv0) * a.v_ss * 2);
+    int kr, ke;
+    tile_rows(t, kr, ke);
+    const u32x4 s = make_srd(vbase + static_cast<int64_t>(kr) * v_ss, static_cast<int64_t>(ke - kr) * v_ss * 2);
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) dma16(s, v_voff[j], v_lds0 + buf * kTile + j * 1024);
   };
@@ -640,9 +767,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
 
   frag qf[KS];
   {
-    const uint16_t* qbase = a.q + head * a.q_hs + static_cast<int64_t>(wq0) * a.q_ss;
-    const auto qr = make_rsrc(qbase, static_cast<int64_t>(a.lq - wq0) * a.q_ss * 2);
-    const int32_t qoff = (lcol * static_cast<int32_t>(a.q_ss) + lhalf * 8) * 2;
+    const uint16_t* qbase = qv + head * q_hs + static_cast<int64_t>(wq0) * q_ss;
+    const auto qr = make_rsrc(qbase, static_cast<int64_t>(lq - wq0) * q_ss * 2);
+    const int32_t qoff = (lcol * static_cast<int32_t>(q_ss) + lhalf * 8) * 2;
 #pragma unroll
     for (int s = 0; s < KS; ++s) qf[s] = as_frag<frag>(buf_load16(qr, qoff + 32 * s));
   }
@@ -670,7 +797,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   float m_run = kInitMax;
   float l_run = 0.f;
 
-  const float c = a.scale_log2;
   const int64_t qlim64 = rl.lane;
   const int64_t wave_lim_first = rl.wave_first;
   const int64_t wave_lim_last = rl.wave_last;
@@ -687,10 +813,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
 
   // Last tile with a key visible to some row of this wave (-1: none); the tiles a wave
   // computes are 0 .. last_live, so both phases of the steady-state loop below run
-  // unconditionally.
+  // unconditionally.  In a fused ring every tile up to the last is computed: tiles
+  // past a wave's rows occur only on the local source's diagonal and are masked.
   int last_live = n_tiles - 1;
-  if (wq0 >= a.lq) last_live = -1;
-  else if (a.causal) last_live = wave_lim_last < 0 ? -1 : static_cast<int>(min(static_cast<int64_t>(last_live), wave_lim_last / BK));
+  if (wq0 >= lq) last_live = -1;
+  else if (!RING && causal) last_live = wave_lim_last < 0 ? -1 : static_cast<int>(min(static_cast<int64_t>(last_live), wave_lim_last / BK));
   auto live = [&](int t) __attribute__((always_inline)) { return t >= 0 && t <= last_live; };
 
   // ---- M phase pieces: O^T += V^T P^T of the previous tile (V buffer vb), S^T = K Q^T of this tile (K buffer kb) ----
@@ -751,13 +878,18 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     for (int b = 0; b < NKB; ++b) pin(sacc[b]);
   };
 
-  // ---- X phase: mask, tile max, lazy rescale, P = 2^(s*c - m) of tile t ----
+  // ---- X phase: mask, tile max, lazy rescale, P = 2^(s*c - m) of the next tile ----
   auto xphase = [&](int t) __attribute__((always_inline)) {
-    const int kv0 = t * BK;
-    const bool need_mask = (kv0 + BK > a.lk) || (a.causal && kv0 + BK - 1 > wave_lim_first);
+    int kv0, ke;
+    tile_rows(t, kv0, ke);
+    const int rows_left = ke - kv0;                     // visible rows from the tile's first key on
+    const int64_t krel = kv0 + kdelta;                  // position of that key relative to query row 0
+    bool need_mask = rows_left < BK;
+    if (causal) need_mask = need_mask || (POS ? kv0 + BK - 1 > wave_lim_first : krel + BK - 1 > wq0);
     if (need_mask) {
-      int64_t lim64 = a.lk - 1 - kv0;
-      if (a.causal) lim64 = min(lim64, qlim64 - kv0);
+      // key kv0 + j of the segment is visible to this lane iff j <= lim
+      int64_t lim64 = rows_left - 1;
+      if (causal) lim64 = min(lim64, POS ? qlim64 - kv0 : static_cast<int64_t>(my_q) - krel);
       const int lim = static_cast<int>(max(min(lim64, static_cast<int64_t>(BK)), static_cast<int64_t>(-1))) - 8 * lhalf;
 #pragma unroll
       for (int b = 0; b < NKB; ++b)
@@ -878,8 +1010,25 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
     }
   }
 
-  if (my_q >= a.lq) return;
-  write_row<D>(a, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run));
+  if (my_q >= lq) return;
+  if constexpr (RING) {
+    const int64_t row = static_cast<int64_t>(plan.off[t_dom]) + my_q;
+    write_final_row<D>(plan.out, plan.dtype, head * plan.out_hs + row * plan.out_ss,
+                       plan.lse != nullptr ? plan.lse + head * plan.lse_hs + row : nullptr, lhalf, oacc, m_run,
+                       sum_xor32(l_run));
+  } else {
+    write_row<D>(*ap, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run));
+  }
+}
+
+template <int DT, int G, bool POS, int BK>
+__global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockGroup grp) {
+  pingpong_body<DT, G, POS, BK, false>(grp);
+}
+
+template <int DT, int G, int BK>
+__global__ __launch_bounds__(kThreads, 1) void flash_ring_kernel(RingPlan plan) {
+  pingpong_body<DT, G, false, BK, true>(plan);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1176,6 +1325,58 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
     for (int i = 0; i < grp.n; ++i) grp.a[i] = make_args(*live[base + i]);
     if (f.dtype == kBF16) launch_pingpong<kBF16>(grp, stream);
     else launch_pingpong<kF16>(grp, stream);
+  }
+  HCP_HIP(hipGetLastError());
+}
+
+bool ring_fused_applies(int dtype, int d) { return (dtype == kBF16 || dtype == kF16) && d == kD3; }
+
+void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
+  require(ring_fused_applies(L.dtype, L.d), "fused ring: dtype must be BF16 or F16 with head_dim 128");
+  require(L.n >= 1 && L.n <= kMaxDomains, "fused ring: 1 to 64 domains");
+  RingPlan p{};
+  p.q = static_cast<const uint16_t*>(L.q);
+  p.k = static_cast<const uint16_t*>(L.k);
+  p.v = static_cast<const uint16_t*>(L.v);
+  p.q_hs = L.q_hs; p.q_ss = L.q_ss; p.k_hs = L.k_hs; p.k_ss = L.k_ss; p.v_hs = L.v_hs; p.v_ss = L.v_ss;
+  p.out = L.out; p.out_hs = L.out_hs; p.out_ss = L.out_ss;
+  p.lse = L.lse; p.lse_hs = L.lse_hs;
+  p.dtype = L.dtype;
+  p.hq = L.hq; p.hkv = L.hkv; p.rep = L.hq / L.hkv;
+  const int g = heads_per_group(p.rep);
+  const int tq = 32 * (kWaves / g);
+  p.n_groups = L.hq / g;
+  p.n = L.n;
+  p.causal = L.causal;
+  p.scale_log2 = L.scale * kLog2e;
+  int64_t acc = 0;
+  for (int i = 0; i < L.n; ++i) {
+    require(L.len[i] >= 1, "fused ring: every chunk length must be >= 1");
+    p.off[i] = static_cast<int32_t>(acc);
+    p.len[i] = static_cast<int32_t>(L.len[i]);
+    acc += L.len[i];
+    require(acc <= INT32_MAX, "fused ring: total length must fit in int32");
+  }
+  // slot s holds domain n-1-s: later domains (more visible keys under causal masking) first
+  p.qt_begin[0] = 0;
+  for (int s = 0; s < L.n; ++s) p.qt_begin[s + 1] = p.qt_begin[s] + static_cast<int32_t>(ceil_div(p.len[L.n - 1 - s], tq));
+  const int64_t blocks = static_cast<int64_t>(p.qt_begin[L.n]) * p.n_groups;
+  require(blocks <= INT32_MAX, "fused ring: too many workgroups");
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (L.dtype == kBF16) {
+    switch (g) {
+      case 8: flash_ring_kernel<kBF16, 8, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
+      case 4: flash_ring_kernel<kBF16, 4, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
+      case 2: flash_ring_kernel<kBF16, 2, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
+      default: flash_ring_kernel<kBF16, 1, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
+    }
+  } else {
+    switch (g) {
+      case 8: flash_ring_kernel<kF16, 8, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
+      case 4: flash_ring_kernel<kF16, 4, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
+      case 2: flash_ring_kernel<kF16, 2, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
+      default: flash_ring_kernel<kF16, 1, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
+    }
   }
   HCP_HIP(hipGetLastError());
 }

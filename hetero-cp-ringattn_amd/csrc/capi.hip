@@ -39,6 +39,12 @@ int* device_error_flags() {
 namespace {
 
 thread_local std::string g_last_error;
+thread_local int g_last_path = HCP_PATH_NONE;
+
+// The kernel a block launch takes (see launch_block_partial / launch_block_group).
+int block_path(const BlockLaunch& L) {
+  return !L.force_general && block_uses_mfma(L.dtype, L.d) ? HCP_PATH_MFMA : HCP_PATH_GENERAL;
+}
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -143,6 +149,8 @@ StrategySpec make_spec(int32_t strategy, int32_t n, const int64_t* chunks, bool 
 struct ReplayPlan {
   int n;
   StrategySpec spec;
+  int schedule = HCP_SCHEDULE_AUTO;
+  size_t fused_stage_bytes = 0;           // fused paged replay: each of the K and V staging buffers [Hkv, S, D]
   bool positioned = false;                // causal with explicit positions (Striped / ZigZag)
   size_t pos_off = 0, lim_off = 0;        // workspace: positions int64 [S], key limits int32 [N, S]
   std::vector<int64_t> len, off, first, last;
@@ -202,6 +210,9 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
   require(d->num_domains >= 1 && d->num_domains <= 64, "num_domains must be in [1, 64]");
   require(d->chunk_lens != nullptr, "null chunk_lens");
   const StrategySpec spec = make_spec(d->strategy, d->num_domains, d->chunk_lens, false);
+  require(d->schedule == HCP_SCHEDULE_AUTO || d->schedule == HCP_SCHEDULE_PER_STEP ||
+              d->schedule == HCP_SCHEDULE_FUSED,
+          "schedule must be 0 (auto), 1 (per ring step) or 2 (fused)");
   require(d->num_q_heads > 0 && d->num_kv_heads > 0 && d->num_q_heads % d->num_kv_heads == 0,
           "bad head counts");
   require(d->head_dim > 0 && d->head_dim <= 256, "head_dim must be in [1, 256]");
@@ -257,7 +268,42 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
     cur += p.staging_bytes_per_domain * p.n;
   }
   p.total = cur;
+  p.schedule = d->schedule;
+  // The fused schedule keeps no state in HBM; paged, it stages the whole sequence once
+  // at the start of the workspace (the per-step layout's need covers it: its staging
+  // alone holds N chunks of the longest length).
+  p.fused_stage_bytes = align256(static_cast<size_t>(p.seq) * d->num_kv_heads * d->head_dim * es);
+  if (d->schedule == HCP_SCHEDULE_FUSED) {
+    require(!p.positioned, "the fused schedule needs vanilla positions (or causal = 0)");
+    p.total = paged ? 2 * p.fused_stage_bytes : 0;
+  }
   return p;
+}
+
+// Whole replay as one fused-ring launch (HCP_SCHEDULE_FUSED): q / k / v / out are the
+// whole-sequence views.
+void run_replay_fused(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ring_view q, hcp_ring_view k,
+                      hcp_ring_view v, hcp_ring_view out, float* lse_out, hipStream_t stream) {
+  RingLaunch L{};
+  L.dtype = d->dtype;
+  L.d = d->head_dim;
+  L.hq = d->num_q_heads;
+  L.hkv = d->num_kv_heads;
+  L.n = p.n;
+  L.causal = d->causal;
+  L.scale = d->scale;
+  L.q = q.data; L.k = k.data; L.v = v.data;
+  L.q_hs = q.head_stride; L.q_ss = q.seq_stride;
+  L.k_hs = k.head_stride; L.k_ss = k.seq_stride;
+  L.v_hs = v.head_stride; L.v_ss = v.seq_stride;
+  L.out = out.data;
+  L.out_hs = out.head_stride;
+  L.out_ss = out.seq_stride;
+  L.lse = lse_out;
+  L.lse_hs = p.seq;
+  L.len = p.len.data();
+  timed(kTimedBlock, stream, [&] { launch_ring_fused(L, stream); });
+  g_last_path = HCP_PATH_RING_FUSED;
 }
 
 void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k, hcp_ring_view v,
@@ -265,6 +311,7 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
                 hcp_ring_view out, float* lse_out, void* ws, size_t ws_bytes, hipStream_t stream) {
   const bool paged = pool != nullptr;
   ReplayPlan p = plan_replay(d, paged);
+  g_last_path = HCP_PATH_NONE;
   require(ws != nullptr || p.total == 0, "null workspace");
   require(ws_bytes >= p.total, "workspace too small: need " + std::to_string(p.total) + " bytes");
   check_view(q, "q", p.seq);
@@ -284,6 +331,34 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
   } else {
     check_view(k, "k", p.seq);
     check_view(v, "v", p.seq);
+  }
+  // Fused schedule: one launch over every domain's ring (vanilla positions, BF16/F16,
+  // head_dim 128, 16-byte rows); AUTO takes it wherever it applies.
+  const bool fused_ok = !p.positioned && ring_fused_applies(d->dtype, d->head_dim) && mfma_layout_ok(q) &&
+                        mfma_layout_ok(out) && (paged || (mfma_layout_ok(k) && mfma_layout_ok(v)));
+  if (p.schedule == HCP_SCHEDULE_FUSED)
+    require(fused_ok, "the fused schedule needs BF16/F16, head_dim 128 and 16-byte aligned rows and strides");
+  if (fused_ok && p.schedule != HCP_SCHEDULE_PER_STEP) {
+    hcp_ring_view kk = k, vv = v;
+    if (paged) {
+      // every chunk staged once, in one batched bit-exact gather, as [Hkv, S, D]
+      const int64_t hs = p.seq * d->head_dim;
+      kk = hcp_ring_view{base, hs, d->head_dim};
+      vv = hcp_ring_view{base + p.fused_stage_bytes, hs, d->head_dim};
+      std::vector<PagedRangeDesc> rs;
+      for (int s = 0; s < p.n; ++s) {
+        const int64_t o = p.off[s] * d->head_dim;
+        rs.push_back(PagedRangeDesc{table, 0, p.off[s], p.off[s] + p.len[s], static_cast<char*>(kk.data) + o * es,
+                                    static_cast<char*>(vv.data) + o * es, hs, d->head_dim});
+      }
+      timed(kTimedGather, stream, [&] {
+        launch_paged_copy_batch(true, pool->data, pool->num_blocks, pool->block_size, pool->num_kv_heads,
+                                pool->head_dim, pool->elem_bytes, static_cast<int>(rs.size()), rs.data(), 0, err,
+                                stream);
+      });
+    }
+    run_replay_fused(d, p, q, kk, vv, out, lse_out, stream);
+    return;
   }
   // Explicit positions: generate every domain's positions in HBM, then the key limits
   // of every (target row, source) pair, once per replay.
@@ -383,6 +458,8 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
     timed(kTimedBlock, stream, [&] {
       launch_block_group(step_launches.data(), static_cast<int>(step_launches.size()), stream);
     });
+    for (const BlockLaunch& L : step_launches)
+      if (g_last_path != HCP_PATH_GENERAL) g_last_path = block_path(L);
   }
 }
 
@@ -394,6 +471,8 @@ using namespace hcp;
 extern "C" {
 
 const char* hcp_ring_last_error(void) { return g_last_error.c_str(); }
+
+int hcp_ring_last_path(void) { return g_last_path; }
 
 int hcp_ring_abi_version(void) { return HCP_RING_ABI_VERSION; }
 
@@ -431,7 +510,9 @@ int hcp_ring_block_partial(const hcp_ring_block_desc* desc, hcp_ring_view q, hcp
     check_view(k, "k", desc->kv_len);
     check_view(v, "v", desc->kv_len);
     if (desc->q_len > 0) require(o != nullptr && lse != nullptr, "null o or lse");
-    launch_block_partial(make_launch(desc, q, k, v, o, lse), as_stream(stream));
+    const BlockLaunch L = make_launch(desc, q, k, v, o, lse);
+    launch_block_partial(L, as_stream(stream));
+    g_last_path = desc->q_len > 0 ? block_path(L) : HCP_PATH_NONE;
   });
 }
 
@@ -470,6 +551,7 @@ int hcp_ring_block_partial_positioned(const hcp_ring_block_desc* desc, hcp_ring_
       L.q_lim = la.lim;
     }
     launch_block_partial(L, as_stream(stream));
+    g_last_path = block_path(L);
   });
 }
 

@@ -41,6 +41,23 @@ void launch_block_partial(const BlockLaunch& L, hipStream_t stream);
 // launch per up to 8 head-dim-128 MFMA blocks of the same head layout, else one each.
 void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream);
 
+// A whole single-GPU ring replay with vanilla positions in one launch (fused ring, see
+// block_attn.hip): q / k / v / out are whole-sequence [heads, S, D] views whose rows
+// are the domains' chunks in order; lse [hq, lse_hs >= S] or null.
+struct RingLaunch {
+  int dtype, d, hq, hkv, n, causal;
+  float scale;
+  const void *q, *k, *v;
+  int64_t q_hs, q_ss, k_hs, k_ss, v_hs, v_ss;
+  void* out;
+  int64_t out_hs, out_ss;
+  float* lse;
+  int64_t lse_hs;
+  const int64_t* len;  // HOST array of n chunk lengths
+};
+bool ring_fused_applies(int dtype, int d);
+void launch_ring_fused(const RingLaunch& L, hipStream_t stream);
+
 void launch_lse_merge(int n, const float* const* o_parts, const float* const* lse_parts, int heads,
                       int64_t q_len, int d, int out_dtype, void* out, int64_t out_hs, int64_t out_ss,
                       float* lse_out, int64_t lse_out_hs, hipStream_t stream);

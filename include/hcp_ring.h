@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define HCP_RING_ABI_VERSION 1
+#define HCP_RING_ABI_VERSION 2
 
 enum hcp_ring_status {
   HCP_RING_OK = 0,
@@ -79,6 +79,21 @@ int hcp_ring_abi_version(void);
 
 /* Number of visible GPUs in *count; -5 when no HIP device is usable. */
 int hcp_ring_device_count(int* count);
+
+/*
+ * Kernel path taken by the last successful attention call on this thread (block
+ * partials, positioned partials, ring replays): lets a caller see that a view whose
+ * rows or strides are not 16-byte multiples, an fp32 dtype or a head_dim other than
+ * 64 / 128 went to the scalar general kernel instead of the matrix cores.  No
+ * reference counterpart (the reference has one ATen path).
+ */
+enum hcp_ring_path {
+  HCP_PATH_NONE = 0,        /* no attention call yet, or it launched nothing */
+  HCP_PATH_MFMA = 1,        /* matrix-core block kernels (one launch per block or ring step) */
+  HCP_PATH_RING_FUSED = 2,  /* the fused ring kernel (one launch per replay) */
+  HCP_PATH_GENERAL = 3      /* the scalar fp32 general kernel for at least one block */
+};
+int hcp_ring_last_path(void);
 
 /*
  * Reads and clears the sticky device-side error flags of the current device
@@ -339,7 +354,30 @@ int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_po
  * With a paged pool (hcp_ring_prefill_replay_paged), K/V are not given as views: each
  * source domain's chunk is first gathered with (3) from the pool through block_table
  * (table_seq_offset 0) into a staging area inside the workspace, then consumed.
+ *
+ * desc->schedule picks how the ring steps reach the GPU (the result is the same up to
+ * fp32 rounding; no reference counterpart, the reference runs one domain per process):
+ *   HCP_SCHEDULE_PER_STEP  one grouped block-kernel launch per ring step, the state
+ *                          of every domain with more than one source kept in fp32 in
+ *                          the workspace between steps (the schedule a multi-GPU ring
+ *                          would run, one step per exchange);
+ *   HCP_SCHEDULE_FUSED     one launch for the whole replay: each workgroup folds all
+ *                          sources of its domain's query tile in ring order with the
+ *                          running state in registers and writes the output rows (no
+ *                          fp32 state in HBM).  Applies to VANILLA positions (or
+ *                          causal = 0), BF16/F16, head_dim 128, and q/k/v views with
+ *                          16-byte aligned rows; -6 otherwise.  The paged form gathers
+ *                          every chunk once, in one batched launch, then runs it;
+ *   HCP_SCHEDULE_AUTO (0)  FUSED where it applies, else PER_STEP.
+ * Workspace: hcp_ring_replay_workspace_size reports the need of the requested schedule
+ * (AUTO: the PER_STEP need, which covers both); FUSED needs none unpaged.
  * ------------------------------------------------------------------------------- */
+enum hcp_ring_schedule {
+  HCP_SCHEDULE_AUTO = 0,
+  HCP_SCHEDULE_PER_STEP = 1,
+  HCP_SCHEDULE_FUSED = 2
+};
+
 typedef struct hcp_ring_replay_desc {
   int32_t dtype;
   int32_t num_q_heads;
@@ -350,6 +388,7 @@ typedef struct hcp_ring_replay_desc {
   const int64_t* chunk_lens; /* HOST array of num_domains lengths (each >= 1) */
   float scale;
   int32_t strategy;          /* HCP_STRATEGY_* (0 = vanilla) */
+  int32_t schedule;          /* HCP_SCHEDULE_* (0 = auto) */
 } hcp_ring_replay_desc;
 
 size_t hcp_ring_replay_workspace_size(const hcp_ring_replay_desc* desc, int32_t paged);

@@ -20,7 +20,7 @@ def test_library_exports_every_header_function(hcp):
 
 
 def test_abi_version(hcp):
-    assert hcp.lib().hcp_ring_abi_version() == 1
+    assert hcp.lib().hcp_ring_abi_version() == 2
 
 
 def test_null_descriptor_is_invalid(hcp):

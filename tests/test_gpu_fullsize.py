@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import hcp_ring_amd as H
+from oracle import inputs as I, tch_ring as T
 
 pytestmark = pytest.mark.gpu
 
@@ -74,6 +75,42 @@ def test_c3_full_ring_prefill_sampled_rows_and_strategy_invariance(gpu):
     assert (lz - lse).abs().max().item() <= 2 * LSE_TOL
 
 
+def test_c2_full_ring_prefill_both_schedules(gpu):
+    # Qwen2.5-3B shape at its stated size: S=8192 in [4096, 2560, 1536], 16 q / 2 kv heads
+    # (eight query heads per KV head), D=128, bf16, seed 43.
+    chunks, hq, hkv, d = [4096, 2560, 1536], 16, 2, 128
+    s = sum(chunks)
+    q, k, v = synth(43, [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    out, lse = H.ring_attention_replay(qh, kh, vh, chunks)
+    assert H.last_path() == "ring_fused"
+    out_s, lse_s = H.ring_attention_replay(qh, kh, vh, chunks, schedule="per_step")
+    assert H.last_path() == "mfma"
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    # every domain's first and last row, and a few inside, against the f64 closed form
+    rows = [0, 1, 2047, 4095, 4096, 5000, 6655, 6656, 7000, 8191]
+    q32, k32, v32 = (x.float().cpu().numpy() for x in (q, k, v))
+    ref_o, ref_l = rows_closed_form(q32, k32, v32, rows, 1 / math.sqrt(d), lambda r: r + 1)
+    for o, l in ((out, lse), (out_s, lse_s)):
+        got_o = o.float().cpu().numpy()[:, rows].transpose(1, 0, 2)
+        got_l = l.cpu().numpy()[:, rows].T
+        assert np.abs(got_o - ref_o).max() <= OUT_TOL
+        assert np.abs(got_l - ref_l).max() <= LSE_TOL
+    # the last domain whole against the op-for-op restatement of ring_attention
+    # (ring.rs:861-1398) on the fp32 upcasts: its local chunk, then domains 1 and 0
+    off = 6656
+    f = lambda x: torch.from_numpy(x).permute(1, 0, 2).unsqueeze(0)
+    kx, vx = T.repeat_kv_heads(f(k32), hq // hkv), T.repeat_kv_heads(f(v32), hq // hkv)
+    offs = [0, 4096, 6656]
+    sent = [T.local_micro_blocks(kx[:, :, o:o + L], vx[:, :, o:o + L], o, 3) for o, L in zip(offs, chunks)]
+    ro, rl = T.ring_attention(1 / math.sqrt(d), f(q32)[:, :, off:], kx[:, :, off:], vx[:, :, off:],
+                              torch.arange(off, s), off, 3, [sent[1], sent[0]], return_lse=True)
+    for o, l in ((out, lse), (out_s, lse_s)):
+        assert np.abs(o[:, off:].float().cpu().numpy() - ro[0].numpy()).max() <= OUT_TOL
+        assert np.abs(l[:, off:].cpu().numpy() - rl[0].numpy()).max() <= LSE_TOL
+
+
 def test_c4_full_paged_decode_sampled_sequences(gpu):
     batch, hq, hkv, d, bs, ctx, nb = 64, 32, 8, 128, 16, 16384, 65536
     chunks = [8192, 5120, 3072]
@@ -81,8 +118,8 @@ def test_c4_full_paged_decode_sampled_sequences(gpu):
     pool = torch.empty(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
     H.synth_normals(45, 0, q.numel(), q)
     H.synth_normals(45, q.numel(), pool.numel(), pool)
-    rng = np.random.default_rng(45)
-    tables_np = rng.permutation(nb)[: batch * (ctx // bs)].astype(np.int32).reshape(batch, ctx // bs)
+    # the config's block tables: the seeded LCG Fisher-Yates permutation of the pool (as the bench draws them)
+    tables_np = I.permuted_block_table(45, nb)[: batch * (ctx // bs)].reshape(batch, ctx // bs)
     tables = torch.from_numpy(tables_np).cuda()
     parts, t0 = [], 0
     for L in chunks:
@@ -128,6 +165,47 @@ def test_c5_full_staging_bit_exact_against_torch_indexing(gpu):
     for (_, _, a, b, ko, vo) in ranges:
         assert torch.equal(ko.view(torch.int16), k[a:b].permute(1, 0, 2).view(torch.int16))
         assert torch.equal(vo.view(torch.int16), v[a:b].permute(1, 0, 2).view(torch.int16))
+
+
+def test_c5_full_staged_prefill_output(gpu):
+    # The 128k staged replay at its config: 8 seeded chunks, Llama-3-8B heads, the K/V of
+    # the whole sequence in a bs=16 pool under the LCG-permuted block table (seed 42, as
+    # the bench).  Staging is bit-exact, so the paged replays equal the unpaged ones bit
+    # for bit; sampled rows at every domain boundary match the f64 closed form.
+    chunks = I.c5_chunks()
+    assert chunks == [21504, 13312, 18432, 23552, 24576, 9216, 8192, 12288]
+    hq, hkv, d, bs = 32, 8, 128, 16
+    s = sum(chunks)
+    q, k, v = synth(46, [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    nb = s // bs
+    table = torch.from_numpy(I.permuted_block_table(42, nb)).cuda()
+    pool = torch.zeros(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    H.paged_kv_scatter(pool, table, 0, 0, s, kh, vh)
+    out_p, lse_p = H.ring_attention_replay_paged(qh, pool, table, chunks)
+    assert H.last_path() == "ring_fused"
+    out_u, lse_u = H.ring_attention_replay(qh, kh, vh, chunks)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    assert torch.equal(out_p, out_u) and torch.equal(lse_p, lse_u)
+    assert torch.isfinite(out_p.float()).all() and torch.isfinite(lse_p).all()
+    offs = [sum(chunks[:i]) for i in range(len(chunks))]
+    rows = sorted({0, s - 1} | {o for o in offs} | {o - 1 for o in offs if o > 0} | {offs[3] + 777})
+    q32 = q[torch.tensor(rows, device="cuda")].float().cpu().numpy()
+    k32, v32 = k.float().cpu().numpy(), v.float().cpu().numpy()
+    ref_o, ref_l = rows_closed_form(q32, k32, v32, list(range(len(rows))), 1 / math.sqrt(d),
+                                    lambda i: rows[i] + 1)
+    got_o = out_p.float().cpu().numpy()[:, rows].transpose(1, 0, 2)
+    got_l = lse_p.cpu().numpy()[:, rows].T
+    assert np.abs(got_o - ref_o).max() <= OUT_TOL
+    assert np.abs(got_l - ref_l).max() <= LSE_TOL
+    # the per-step paged schedule (a gather per ring step into per-domain ring buffers,
+    # eight-pair grouped launches) agrees with the fused one within the tolerances
+    out_s, lse_s = H.ring_attention_replay_paged(qh, pool, table, chunks, schedule="per_step")
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    assert (out_s.float() - out_p.float()).abs().max().item() <= OUT_TOL
+    assert (lse_s - lse_p).abs().max().item() <= LSE_TOL
 
 
 @pytest.mark.parametrize("tokens", [4096, 2048, 12288, 12200])

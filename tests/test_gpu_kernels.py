@@ -275,17 +275,29 @@ RING_CASES = [
     ("uneven4", [300, 77, 500, 123], 8, 2, 128, torch.bfloat16, 50),
     # 10 domains: the first ring steps hold 10 blocks, launched as groups of 8 + 2
     ("ten_domains", [200, 64, 130, 96, 300, 50, 128, 77, 256, 99], 8, 2, 128, torch.bfloat16, 51),
+    # head ratios 1, 3 (one head per workgroup), 6 (two) and 8, chunks off the 128-key
+    # tile grid so past sources straddle tiles and end in partial ones
+    ("mha_unaligned", [190, 333, 61], 4, 4, 128, torch.bfloat16, 52),
+    ("gqa3_fp16", [257, 129, 400], 6, 2, 128, torch.float16, 53),
+    ("gqa6", [96, 450, 200], 12, 2, 128, torch.bfloat16, 54),
+    ("gqa8_two_domains", [1000, 536], 16, 2, 128, torch.bfloat16, 55),
+    ("single_domain", [700], 8, 2, 128, torch.bfloat16, 56),
 ]
 
 
+@pytest.mark.parametrize("schedule", ["auto", "per_step"])
 @pytest.mark.parametrize("case", RING_CASES, ids=[c[0] for c in RING_CASES])
-def test_ring_replay_matches_tch_blockwise(gpu, case):
+def test_ring_replay_matches_tch_blockwise(gpu, case, schedule):
     name, chunks, hq, hkv, d, dt, seed = case
     s = sum(chunks)
     (q, k, v), (q32, k32, v32) = draw(seed, [(s, hq, d), (s, hkv, d), (s, hkv, d)], dt)
     scale = 1 / math.sqrt(d)
-    out, lse = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+    out, lse = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
+                                       schedule=schedule)
     torch.cuda.synchronize()
+    # BF16/F16 at head_dim 128 take the fused ring kernel unless a per-step schedule is asked for
+    fused = dt != torch.float32 and d == 128 and schedule == "auto"
+    assert H.last_path() == ("ring_fused" if fused else "general" if dt == torch.float32 else "mfma")
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     # the reference driver on fp32 upcasts (ring.rs:861-1398 restated op for op)
@@ -303,7 +315,8 @@ def test_ring_replay_matches_tch_blockwise(gpu, case):
         assert np.abs(out - rb[0].float().numpy()).max() <= OUT_TOL
 
 
-def test_ring_replay_paged_matches_unpaged(gpu):
+@pytest.mark.parametrize("schedule", ["auto", "per_step", "fused"])
+def test_ring_replay_paged_matches_unpaged(gpu, schedule):
     chunks = [256, 96, 160]
     s, hq, hkv, d, bs = sum(chunks), 8, 2, 128, 16
     (q, k, v), _ = draw(77, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
@@ -312,10 +325,57 @@ def test_ring_replay_paged_matches_unpaged(gpu):
     table = torch.from_numpy(table_np).cuda()
     pool = torch.zeros(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
     H.paged_kv_scatter(pool, table, 0, 0, s, k.permute(1, 0, 2), v.permute(1, 0, 2))
-    o1, l1 = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
-    o2, l2 = H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, chunks)
+    o1, l1 = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
+                                     schedule=schedule)
+    # the fused schedule needs no workspace unpaged, and only the two staging buffers paged
+    if schedule == "fused":
+        assert H.replay_workspace_size(torch.bfloat16, hq, hkv, d, chunks, schedule="fused") == 0
+        assert H.replay_workspace_size(torch.bfloat16, hq, hkv, d, chunks, paged=True, schedule="fused") == \
+            2 * ((s * hkv * d * 2 + 255) // 256 * 256)
+    o2, l2 = H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, chunks, schedule=schedule)
     torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (6, 2), (16, 2)])
+def test_ring_replay_fused_noncausal_wraps_round_the_ring(gpu, hq, hkv):
+    # Without causal masking every domain folds every source; after source 0 the ring
+    # wraps to N-1, ..., t+1 (rows [off_t + len_t, S) read from the top down).
+    chunks, d = [200, 333, 150, 90], 128
+    s = sum(chunks)
+    (q, k, v), (q32, k32, v32) = draw(57, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
+    scale = 1 / math.sqrt(d)
+    outs = {}
+    for sched in ("fused", "per_step"):
+        outs[sched] = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
+                                              causal=False, schedule=sched)
+    torch.cuda.synchronize()
+    pos = np.arange(s)
+    ro, rl = C.attention_f64(q32, k32, v32, pos, pos, scale, causal=False)
+    for sched, (o, l) in outs.items():
+        assert np.abs(o.float().cpu().numpy() - ro.transpose(1, 0, 2)).max() <= OUT_TOL, sched
+        assert np.abs(l.cpu().numpy() - rl.T).max() <= LSE_TOL, sched
+
+
+def test_ring_replay_fused_rejects_what_it_cannot_run(gpu):
+    chunks, d = [64, 64], 128
+    s = sum(chunks)
+    q = torch.zeros(8, s, d, dtype=torch.bfloat16, device="cuda")
+    kv = torch.zeros(2, s, d, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(H.HcpRingError) as e:   # explicit positions
+        H.ring_attention_replay(q, kv, kv, chunks, strategy="zigzag", schedule="fused")
+    assert e.value.code == -6
+    with pytest.raises(H.HcpRingError) as e:   # fp32
+        H.ring_attention_replay(q.float(), kv.float(), kv.float(), chunks, schedule="fused")
+    assert e.value.code == -6
+    with pytest.raises(H.HcpRingError) as e:   # rows not on 16-byte boundaries
+        qq = torch.zeros(8, s, d + 4, dtype=torch.bfloat16, device="cuda")[:, :, 4:]
+        H.ring_attention_replay(qq, kv, kv, chunks, schedule="fused")
+    assert e.value.code == -6
+    # AUTO falls back to the per-step kernels for such views, and says so
+    H.ring_attention_replay(qq, kv, kv, chunks)
+    assert H.last_path() == "general"
 
 
 def test_paged_gather_batch_bit_exact(gpu):
