@@ -7,17 +7,19 @@
 // sequence's block table -- no gather, no GQA expand copy.
 //
 // Work split (HBM-bound: every K/V byte is read exactly once):
-//   * grid = (splits, batch, ceil(Hkv / 4)).  A workgroup (4 waves) owns one sequence,
-//     a contiguous run of 16-token groups of the chunk and 4 kv heads: wave w handles
-//     kv head 4*blockIdx.z + w, so per 16 tokens a wave reads 16 K rows and 16 V rows
-//     of its head (4 KiB each for D=128, bf16) straight from the pool.
+//   * grid = (splits, batch, ceil(Hkv / W)) with W = min(4, Hkv) waves per workgroup.
+//     A workgroup owns one sequence, a contiguous run of 16-token groups of the chunk
+//     and W kv heads: wave w handles kv head W*blockIdx.z + w, so per 16 tokens a wave
+//     reads 16 K rows and 16 V rows of its head (4 KiB each for D=128, bf16) straight
+//     from the pool.
 //   * Scores: S^T = K Q^T on MFMA 16x16x32 (A = 16 key rows loaded from the pool, 16
-//     bytes per lane; B = the rep <= 4 query heads of the kv head, zero-padded to 16
-//     columns, held in registers for the whole kernel).
+//     bytes per lane; B = the rep <= 16 query heads of the kv head -- the GQA group of
+//     repeat_decode_kv_heads, ring.rs:496-512 -- zero-padded to 16 columns, held in
+//     registers for the whole kernel).
 //   * Online softmax per query head in the log2 domain; P goes through a small LDS
 //     slot (broadcast reads) and PV runs on VALU with each lane owning 8 head-dim
-//     values of 4 of the 16 keys (fp32 accumulators), reduced across lanes once at the
-//     end.
+//     values of 4 of the 16 keys for R query heads (R = 4, 8 or 16, the smallest that
+//     holds rep; fp32 accumulators), reduced across lanes once at the end.
 //   * Each split writes (o, lse) to the workspace; the LSE merge kernel combines the
 //     splits of a sequence (heads = batch*Hq, q_len = 1).
 #include <map>
@@ -72,23 +74,23 @@ __device__ __forceinline__ float hi_half(uint32_t w) {
   return DT == kBF16 ? __uint_as_float(w & 0xffff0000u) : f16_bits_to_f32(static_cast<uint16_t>(w >> 16));
 }
 
-constexpr int kDecWaves = 4;  // kv heads per workgroup (one per wave)
+constexpr int kDecWaves = 4;  // most kv heads per workgroup (one per wave)
 
 // One wave per kv head.  Per 16-key group the wave needs the head's 16 K rows and 16 V
 // rows (4 KiB each for D=128); the loads of two groups are issued before either is
 // computed, so each wave keeps ~16 KiB of HBM reads in flight.
-template <int D, int DT>
+template <int D, int DT, int R>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;        // k-steps of 32 for the QK^T product
   constexpr int DCH = D / 8;        // 8-wide d chunks per row (16 for D=128)
   constexpr int TPL = 16 * DCH / 64;  // keys per lane in PV (4 for D=128)
 
-  __shared__ float p_lds[kDecWaves][16][4];  // [wave][key][query col]
+  __shared__ __attribute__((aligned(16))) float p_lds[kDecWaves][16][R];  // [wave][key][query col]
 
   const int b = blockIdx.y;
   const int split = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kvh = blockIdx.z * kDecWaves + wave;
+  const int kvh = blockIdx.z * (blockDim.x >> 6) + wave;
   if (kvh >= a.hkv) return;  // no workgroup barriers below
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;   // MFMA column = query head within the kv group
@@ -115,10 +117,10 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     qf[s] = v;
   }
 
-  // PV accumulators cover rep <= 4 query heads per kv head (checked by the launcher).
-  float acc[4][8];
+  // PV accumulators cover rep <= R query heads per kv head (checked by the launcher).
+  float acc[R][8];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < R; ++c)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
   float m_run = -1.0e30f, l_run = 0.f;
@@ -180,15 +182,15 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     for (int i = 0; i < 4; ++i) {
       const float p = __builtin_amdgcn_exp2f(sv[i] - m_new);
       psum += p;
-      if (col < 4) p_lds[wave][grp * 4 + i][col] = p;
+      if (col < R) p_lds[wave][grp * 4 + i][col] = p;
     }
     l_run = l_run * alpha + psum;  // per-lane partial over its keys (rescaled)
     // alpha of query column c lives in lane c.
-    float al[4];
+    float al[R];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) al[c] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), c));
+    for (int c = 0; c < R; ++c) al[c] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), c));
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < R; ++c)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[c][e] *= al[c];
     __builtin_amdgcn_wave_barrier();
@@ -199,7 +201,6 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
       const int64_t t = G.tok0 + key;
       const bool ok = t >= a.t0 && t < t_end;
       const u32x4 vv = ok ? G.v[j] : u32x4{0, 0, 0, 0};
-      const float4 p4 = *reinterpret_cast<const float4*>(&p_lds[wave][key][0]);
       float vf[8];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -207,11 +208,15 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
         vf[2 * w + 1] = hi_half<DT>(vv[w]);
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        acc[0][e] += p4.x * vf[e];
-        acc[1][e] += p4.y * vf[e];
-        acc[2][e] += p4.z * vf[e];
-        acc[3][e] += p4.w * vf[e];
+      for (int c4 = 0; c4 < R; c4 += 4) {
+        const float4 p4 = *reinterpret_cast<const float4*>(&p_lds[wave][key][c4]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc[c4][e] += p4.x * vf[e];
+          acc[c4 + 1][e] += p4.y * vf[e];
+          acc[c4 + 2][e] += p4.z * vf[e];
+          acc[c4 + 3][e] += p4.w * vf[e];
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -236,7 +241,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   l += __shfl_xor(l, 16);
   l += __shfl_xor(l, 32);  // lanes with the same col now hold the total over keys
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < R; ++c)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float v = acc[c][e];
@@ -244,12 +249,12 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
       for (int off = DCH; off < 64; off *= 2) v += __shfl_xor(v, off);
       acc[c][e] = v;
     }
-  float lc[4];
+  float lc[R];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) lc[c] = __shfl(l, c);
+  for (int c = 0; c < R; ++c) lc[c] = __shfl(l, c);
   if (pv_tg == 0) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < R; ++c) {
       if (c >= a.rep) break;
       const float inv = lc[c] > 0.f ? 1.f / lc[c] : 0.f;
       float* orow = a.ws_o + (ws_row_base + kvh * a.rep + c) * D + pv_dc * 8;
@@ -259,8 +264,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
           make_float4(acc[c][4] * inv, acc[c][5] * inv, acc[c][6] * inv, acc[c][7] * inv);
     }
   }
-  if (lane < a.rep && lane < 4) {
-    const float lt = lc[lane];
+  if (lane < a.rep && lane < R) {
+    const float lt = l;  // lane c holds column c's total
     a.ws_lse[ws_row_base + kvh * a.rep + lane] = lt > 0.f ? (m_run + __log2f(lt)) * kLn2 : -INFINITY;
   }
 }
@@ -272,28 +277,41 @@ struct DecodePlan {
   int64_t g_begin;
 };
 
+// Query heads per kv head the PV accumulators hold: the smallest of 4, 8, 16 >= rep.
+int decode_width(int rep) { return rep <= 4 ? 4 : rep <= 8 ? 8 : 16; }
+// Waves (kv heads) per workgroup.
+int decode_waves(int hkv) { return std::min(hkv, kDecWaves); }
+
+template <int D, int DT>
+const void* decode_fn(int r) {
+  switch (r) {
+    case 4: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 4>);
+    case 8: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 8>);
+    default: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 16>);
+  }
+}
+
 // Workgroups of the decode kernel resident at once on the current device (CUs x
-// occupancy); 768 (256 CUs x 3) when no device can be queried.
-int decode_slots(int d, int dtype) {
+// occupancy); 256 CUs x 3 when no device can be queried.
+int decode_slots(int d, int dtype, int r, int waves) {
   static std::mutex mu;
-  static std::map<std::tuple<int, int, int>, int> cache;
+  static std::map<std::tuple<int, int, int, int, int>, int> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     (void)hipGetLastError();
     return 768;
   }
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dev, d, dtype);
+  const auto key = std::make_tuple(dev, d, dtype, r, waves);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int cus = 0, per_cu = 0;
-  const void* fn = dtype == kBF16 ? (d == 128 ? reinterpret_cast<const void*>(&paged_decode_kernel<128, kBF16>)
-                                              : reinterpret_cast<const void*>(&paged_decode_kernel<64, kBF16>))
-                                  : (d == 128 ? reinterpret_cast<const void*>(&paged_decode_kernel<128, kF16>)
-                                              : reinterpret_cast<const void*>(&paged_decode_kernel<64, kF16>));
+  const void* fn = dtype == kBF16 ? (d == 128 ? decode_fn<128, kBF16>(r) : decode_fn<64, kBF16>(r))
+                                  : (d == 128 ? decode_fn<128, kF16>(r) : decode_fn<64, kF16>(r));
   int slots = 768;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) == hipSuccess && cus > 0 && per_cu > 0)
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * waves, 0) == hipSuccess && cus > 0 &&
+      per_cu > 0)
     slots = cus * per_cu;
   else
     (void)hipGetLastError();
@@ -301,7 +319,7 @@ int decode_slots(int d, int dtype) {
   return slots;
 }
 
-DecodePlan plan_decode(int batch, int hkv, int d, int dtype, int64_t t0, int64_t t1) {
+DecodePlan plan_decode(int batch, int hq, int hkv, int d, int dtype, int64_t t0, int64_t t1) {
   DecodePlan p;
   p.g_begin = t0 / 16;
   const int64_t g_end = t1 > t0 ? (t1 + 15) / 16 : p.g_begin;
@@ -310,8 +328,9 @@ DecodePlan plan_decode(int batch, int hkv, int d, int dtype, int64_t t0, int64_t
   // partial second round leaves most CUs idle for its whole length (a measured 13-25%
   // loss at c4), and fewer splits also mean fewer partials to merge.  At least 4 groups
   // (64 keys) per split.
-  const int rows = std::max(batch, 1) * ((hkv + kDecWaves - 1) / kDecWaves);
-  int splits = std::max(1, decode_slots(d, dtype) / rows);
+  const int waves = decode_waves(hkv);
+  const int rows = std::max(batch, 1) * ((hkv + waves - 1) / waves);
+  int splits = std::max(1, decode_slots(d, dtype, decode_width(hq / hkv), waves) / rows);
   splits = std::min(splits, 64);
   int gps = static_cast<int>(ceil_div(std::max(p.n_groups, 1), splits));
   gps = std::max(gps, 4);
@@ -321,10 +340,19 @@ DecodePlan plan_decode(int batch, int hkv, int d, int dtype, int64_t t0, int64_t
 }
 
 size_t decode_workspace_bytes(int dtype, int batch, int hq, int hkv, int d, int64_t t0, int64_t t1) {
-  const DecodePlan p = plan_decode(batch, hkv, d, dtype, t0, t1);
+  const DecodePlan p = plan_decode(batch, hq, hkv, d, dtype, t0, t1);
   const size_t rows = static_cast<size_t>(p.splits) * batch * hq;
   auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   return al(rows * d * sizeof(float)) + al(rows * sizeof(float));
+}
+
+template <int D, int DT>
+static void launch_decode_kernel(int r, dim3 grid, int waves, const DecodeArgs& a, hipStream_t stream) {
+  switch (r) {
+    case 4: paged_decode_kernel<D, DT, 4><<<grid, 64 * waves, 0, stream>>>(a); break;
+    case 8: paged_decode_kernel<D, DT, 8><<<grid, 64 * waves, 0, stream>>>(a); break;
+    default: paged_decode_kernel<D, DT, 16><<<grid, 64 * waves, 0, stream>>>(a); break;
+  }
 }
 
 void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const void* q, int64_t q_bs,
@@ -332,11 +360,11 @@ void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const voi
                          const int32_t* tables, int64_t table_stride, int64_t table_len,
                          const int32_t* seq_lens, int64_t t0, int64_t t1, float scale, float* o,
                          float* lse, void* ws, size_t ws_bytes, int* err, hipStream_t stream) {
-  require(hq % hkv == 0 && hq / hkv <= 4, "paged_decode: num_q_heads/num_kv_heads must be <= 4");
+  require(hq % hkv == 0 && hq / hkv <= 16, "paged_decode: num_q_heads/num_kv_heads must be <= 16");
   require(bs % 16 == 0, "paged_decode: block_size must be a multiple of 16");
   require(d == 64 || d == 128, "paged_decode: head_dim must be 64 or 128");
   require(dtype == kBF16 || dtype == kF16, "paged_decode: dtype must be BF16 or F16");
-  const DecodePlan p = plan_decode(batch, hkv, d, dtype, t0, t1);
+  const DecodePlan p = plan_decode(batch, hq, hkv, d, dtype, t0, t1);
   require(ws_bytes >= decode_workspace_bytes(dtype, batch, hq, hkv, d, t0, t1), "paged_decode: workspace too small");
   auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   const size_t rows = static_cast<size_t>(p.splits) * batch * hq;
@@ -368,14 +396,16 @@ void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const voi
   a.ws_lse = ws_lse;
   a.batch = batch;
   a.err = err;
+  const int waves = decode_waves(hkv);
+  const int r = decode_width(a.rep);
   const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(batch),
-                  static_cast<unsigned>((hkv + kDecWaves - 1) / kDecWaves));
+                  static_cast<unsigned>((hkv + waves - 1) / waves));
   if (dtype == kBF16) {
-    if (d == 128) paged_decode_kernel<128, kBF16><<<grid, 256, 0, stream>>>(a);
-    else paged_decode_kernel<64, kBF16><<<grid, 256, 0, stream>>>(a);
+    if (d == 128) launch_decode_kernel<128, kBF16>(r, grid, waves, a, stream);
+    else launch_decode_kernel<64, kBF16>(r, grid, waves, a, stream);
   } else {
-    if (d == 128) paged_decode_kernel<128, kF16><<<grid, 256, 0, stream>>>(a);
-    else paged_decode_kernel<64, kF16><<<grid, 256, 0, stream>>>(a);
+    if (d == 128) launch_decode_kernel<128, kF16>(r, grid, waves, a, stream);
+    else launch_decode_kernel<64, kF16>(r, grid, waves, a, stream);
   }
   HCP_HIP(hipGetLastError());
   // Merge the splits of every (sequence, head): rows = batch*hq, one token each.

@@ -223,6 +223,12 @@ DECODE_CASES = [
     ("middle_chunk", 3, 32, 8, 128, 16, 900, 320, 700, False),
     ("ragged_lens", 5, 16, 4, 128, 32, 600, 100, 600, True),
     ("d64_bs16", 2, 8, 2, 64, 16, 300, 7, 290, False),
+    # the reference's own models: Qwen2-0.5B (14 q / 2 kv, D=64: seven query heads per
+    # KV head, two waves per workgroup) and Qwen2.5-3B (16 q / 2 kv, D=128: eight)
+    ("qwen2_0p5b_rep7_d64", 3, 14, 2, 64, 16, 700, 0, 700, False),
+    ("qwen25_3b_rep8_d128", 4, 16, 2, 128, 16, 1000, 64, 1000, True),
+    ("rep16_one_kv_head", 2, 16, 1, 128, 32, 500, 0, 500, False),
+    ("rep12_three_kv_heads", 2, 36, 3, 64, 16, 333, 5, 333, False),
 ]
 
 
@@ -406,6 +412,8 @@ DECODE_RING_CASES = [
     ("three_domains_uneven", [300, 200, 200], [5, 9, 2], 16, 4, 128, 16),
     ("four_domains_one_empty", [160, 96, 64, 0], [0, 1, 2], 8, 2, 64, 32),
     ("four_domains_ragged_zero", [160, 96, 64, 0], [1, 2, 3], 32, 8, 128, 16),
+    ("qwen2_0p5b_rep7", [200, 120, 90], [3, 4], 14, 2, 64, 16),
+    ("qwen25_3b_rep8", [256, 100], [2, 5, 1], 16, 2, 128, 16),
 ]
 
 
