@@ -184,6 +184,8 @@ def lib() -> ctypes.CDLL:
                                              ctypes.POINTER(PagedPool)], ctypes.c_size_t),
         "hcp_paged_decode_partial": ([ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedPool), View,
                                       vp, vp, vp, vp, vp, ctypes.c_size_t, vp], ctypes.c_int),
+        "hcp_paged_decode_partial_static": ([ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedPool), View,
+                                             vp, vp, vp, vp, vp], ctypes.c_int),
         "hcp_decode_ring_owner": ([i64, i32], ctypes.c_int),
         "hcp_decode_ring_workspace_size": ([ctypes.POINTER(DecodeDesc), ctypes.POINTER(PagedPool), i32,
                                             ctypes.POINTER(DecodeShard)], ctypes.c_size_t),

@@ -21,6 +21,30 @@ namespace hcp {
 // Sticky device-side error flags, one copy per device (static device variable).
 __device__ int g_hcp_device_errors;
 
+// Scratch of hcp_paged_decode_partial_static (the per-split decode partials of one
+// call), one copy per device for the life of the process.  Host code never uses this
+// name as an address: static_scratch() resolves the device's copy.
+constexpr size_t kStaticScratchBytes = HCP_DECODE_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per device (with
+// that device current) by hipGetSymbolAddress.
+void* static_scratch() {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
+  int dev = 0;
+  HCP_HIP(hipGetDevice(&dev));
+  require(dev >= 0 && dev < 64, "device index out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* ptr = nullptr;
+    HCP_HIP(hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)));
+    require(ptr != nullptr, "no device address for the static scratch");
+    ptrs[dev] = ptr;
+  }
+  return ptrs[dev];
+}
+
 int* device_error_flags() {
   static std::mutex mu;
   static int* ptrs[64] = {};
@@ -701,6 +725,25 @@ int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_
                         q.seq_stride, q.head_stride, pool->data, pool->num_blocks, pool->block_size, block_tables,
                         desc->table_stride, desc->table_len, seq_lens, desc->t0, desc->t1, desc->scale, o, lse,
                         workspace, workspace_bytes, device_error_flags(), as_stream(stream));
+  });
+}
+
+int hcp_paged_decode_partial_static(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool,
+                                    hcp_ring_view q, const int32_t* block_tables, const int32_t* seq_lens, float* o,
+                                    float* lse, void* stream) {
+  return guarded(__func__, [&] {
+    require(desc != nullptr && pool != nullptr, "null descriptor or pool");
+    require(desc->batch > 0, "batch must be positive");
+    const size_t need = decode_workspace_bytes(desc->dtype, desc->batch, desc->num_q_heads, desc->num_kv_heads,
+                                               desc->head_dim, desc->t0, desc->t1);
+    require(need <= kStaticScratchBytes, "the split partials need " + std::to_string(need) +
+                                             " bytes, more than the static scratch's " +
+                                             std::to_string(kStaticScratchBytes) +
+                                             "; use hcp_paged_decode_partial with a workspace");
+    void* ws = static_scratch();
+    const int rc = hcp_paged_decode_partial(desc, pool, q, block_tables, seq_lens, o, lse, ws, kStaticScratchBytes,
+                                            stream);
+    if (rc != 0) throw Error(rc, g_last_error);
   });
 }
 

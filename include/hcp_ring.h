@@ -292,6 +292,23 @@ int hcp_paged_decode_partial(const hcp_paged_decode_desc* desc, const hcp_paged_
                              const int32_t* seq_lens, float* o, float* lse, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/*
+ * (4a) hcp_paged_decode_partial without a workspace argument: it allocates nothing,
+ * taking its split partials from a static device array of 16 MiB (HCP_DECODE_STATIC_
+ * SCRATCH_BYTES) that each GPU the library runs on holds until the process ends.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Returns -6 when the call needs more than the array
+ * (hcp_paged_decode_workspace_size(desc, pool) > HCP_DECODE_STATIC_SCRATCH_BYTES);
+ * otherwise the same results as hcp_paged_decode_partial.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (concurrent streams, other threads)
+ * race, so serialise them.  Every byte a call reads from the array it has written first.
+ */
+#define HCP_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
+int hcp_paged_decode_partial_static(const hcp_paged_decode_desc* desc, const hcp_paged_pool* pool,
+                                    hcp_ring_view q, const int32_t* block_tables,
+                                    const int32_t* seq_lens, float* o, float* lse, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * (4b) Decode Q-ring with growth sharding (ring_decode_attention, ring.rs:665-818;
  * ownership rule ring.rs:1921-1942; KvCache::update_sharded, cache.rs:40-48,104-121).
