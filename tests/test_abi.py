@@ -139,7 +139,8 @@ def test_runtime_smoke_and_init_validation():
 NULL_CHECKED = [
     "hcp_ring_block_partial", "hcp_ring_block_partial_positioned", "hcp_ring_lse_merge",
     "hcp_paged_kv_gather", "hcp_paged_kv_scatter", "hcp_paged_kv_gather_batch",
-    "hcp_paged_decode_partial", "hcp_decode_ring_replay", "hcp_ring_prefill_replay",
+    "hcp_paged_decode_partial", "hcp_paged_decode_partial_static", "hcp_decode_ring_replay",
+    "hcp_ring_prefill_replay",
     "hcp_ring_prefill_replay_paged", "hcp_kv_frame_header", "hcp_kv_frame_parse",
     "hcp_kv_frame_pack", "hcp_kv_frame_unpack", "hcp_packet_frame_header",
     "hcp_packet_frame_parse", "hcp_packet_frame_pack", "hcp_packet_frame_unpack",
