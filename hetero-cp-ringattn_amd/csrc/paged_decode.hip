@@ -77,8 +77,8 @@ __device__ __forceinline__ float hi_half(uint32_t w) {
 constexpr int kDecWaves = 4;  // most kv heads per workgroup (one per wave)
 
 // One wave per kv head.  Per 16-key group the wave needs the head's 16 K rows and 16 V
-// rows (4 KiB each for D=128); the loads of two groups are issued before either is
-// computed, so each wave keeps ~16 KiB of HBM reads in flight.
+// rows (4 KiB each for D=128); the next group's loads are issued before a group is
+// computed, and the block ids come from one table load per 64 groups.
 template <int D, int DT, int R>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;        // k-steps of 32 for the QK^T product
@@ -133,11 +133,23 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     int64_t tok0;
     bool ok;
   };
+  // Block ids of the split's groups, 64 at a time: lane i holds the table entry of
+  // group ids_base + i, read back with readlane, so no group waits on a table load.
+  // Keys tok0 .. tok0+15 of group g lie in table entry tok0 / bs (bs is a multiple of 16).
+  int ids = -1, ids_base = g0 - 64;
+  auto block_of = [&](int g, int64_t entry) __attribute__((always_inline)) {
+    if (g - ids_base >= 64) {
+      ids_base = g;
+      const int64_t e = (a.g_begin + g + lane) * 16 / a.bs;
+      ids = g + lane < g1 && e < a.table_len ? table[e] : -1;
+    }
+    const int32_t blk = __builtin_amdgcn_readlane(ids, g - ids_base);
+    return entry < a.table_len ? blk : -1;
+  };
   auto load_group = [&](int g, Group& G) {
     G.tok0 = (a.g_begin + g) * 16;
-    // Keys tok0 .. tok0+15 lie in table entry tok0 / bs (bs is a multiple of 16).
     const int64_t entry = G.tok0 / a.bs;
-    const int32_t blk = entry < a.table_len ? table[entry] : -1;
+    const int32_t blk = block_of(g, entry);
     G.ok = blk >= 0 && blk < a.num_blocks;
     if (!G.ok) {
       if (lane == 0 && entry < a.table_len) atomicOr(a.err, 1);
@@ -222,17 +234,14 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     __builtin_amdgcn_wave_barrier();
   };
 
+  // Rolling double buffer: group g + 1 is loading while group g is computed.
   Group ga, gb;
-  int g = g0;
-  for (; g + 1 < g1; g += 2) {
-    load_group(g, ga);
-    load_group(g + 1, gb);
+  if (g0 < g1) load_group(g0, ga);
+  for (int g = g0; g < g1; g += 2) {
+    if (g + 1 < g1) load_group(g + 1, gb);
     compute_group(ga);
-    compute_group(gb);
-  }
-  if (g < g1) {
-    load_group(g, ga);
-    compute_group(ga);
+    if (g + 2 < g1) load_group(g + 2, ga);
+    if (g + 1 < g1) compute_group(gb);
   }
 
   // ---- epilogue: reduce over key subgroups, normalise, write split partial ----
