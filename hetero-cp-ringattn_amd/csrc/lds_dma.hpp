@@ -24,10 +24,13 @@ __device__ __forceinline__ u32x4 make_srd(const void* base, int64_t bytes) {
 }
 
 // One wave-wide 16-byte-per-lane load straight into LDS at lds_addr + 16 * lane.  The
-// compiler does not track it: callers wait with s_waitcnt vmcnt themselves.  M0 is set
-// and consumed inside the statement; clang warns that a clobber of the reserved M0 is
-// not preserved around it, which is harmless here (the kernels keep no value of their
-// own in M0: every M0 access in their code is this statement's).
+// compiler does not track it: callers wait with s_waitcnt vmcnt themselves (the
+// compiler's own LDS-DMA builtin makes it wait for every DMA before any read of the same
+// LDS array, which would serialise the kernels' multi-buffer pipelines).  M0 is set and
+// consumed inside the statement; clang warns that a clobber of the reserved M0 is not
+// preserved around it.  That is harmless only while the compiler keeps no value of its
+// own in M0, so the build (build.py, check_m0) disassembles every object that includes
+// this header and fails if any instruction other than this statement's three touches M0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(u32x4 srd, uint32_t voff, uint32_t lds_addr) {

@@ -170,3 +170,28 @@ def test_null_or_zero_arguments_are_invalid(hcp, name):
     rc = fn(*_null_args(fn, hcp.View))
     assert rc == -6, (name, rc, hcp.last_error())
     assert hcp.last_error().startswith(name + ":"), hcp.last_error()
+
+
+def test_m0_scan_accepts_the_dma_sequence_and_rejects_anything_else():
+    # build.py's check that the LDS DMA helper owns M0 (csrc/lds_dma.hpp): planted
+    # violations in a synthetic instruction stream must raise.
+    import importlib.util
+    import os
+    spec = importlib.util.spec_from_file_location(
+        "hcp_build_m0", os.path.join(os.path.dirname(H.LIB_PATH), "..", "build.py"))
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    seq = ["s_mov_b32 m0, s12", "s_nop 0", "buffer_load_dwordx4 v3, s[8:11], 0 offen lds"]
+    ok = ["v_mov_b32_e32 v1, 0"] + seq + ["s_waitcnt vmcnt(0)"] + seq
+    assert b.scan_m0(ok) == 2
+    planted = [
+        ["s_mov_b32 m0, -1"] + seq,                                     # compiler M0 value
+        seq[:1] + ["v_mov_b32_e32 v1, 0"] + seq[2:],                    # something between def and DMA
+        ["buffer_load_dwordx4 v3, s[8:11], 0 offen lds"],                # DMA without its M0 def
+        seq + ["s_mov_b32 s4, m0"],                                     # M0 read elsewhere
+        seq + ["v_movrels_b32_e32 v0, v1"],                             # implicit M0 (indexing)
+        seq + ["s_sendmsg sendmsg(MSG_GS_DONE)"],                       # implicit M0 (messages)
+    ]
+    for ins in planted:
+        with pytest.raises(RuntimeError):
+            b.scan_m0(ins)
