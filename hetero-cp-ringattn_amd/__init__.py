@@ -97,6 +97,24 @@ class ReplayDesc(ctypes.Structure):
                 ("strategy", ctypes.c_int32), ("schedule", ctypes.c_int32)]
 
 
+BLOCK_AGENT_MAX = 64
+BLOCK_META_MAX = 256
+
+
+class BlockDescC(ctypes.Structure):
+    _fields_ = [("addr", ctypes.c_uint64), ("len", ctypes.c_uint64), ("dev_id", ctypes.c_uint64),
+                ("mem_type", ctypes.c_int32), ("meta_len", ctypes.c_uint32),
+                ("meta", ctypes.c_uint8 * BLOCK_META_MAX)]
+
+
+class RemoteBlockDescC(ctypes.Structure):
+    _fields_ = [("agent", ctypes.c_char * BLOCK_AGENT_MAX), ("block_id", ctypes.c_uint64), ("desc", BlockDescC)]
+
+
+class BlockCompletionC(ctypes.Structure):
+    _fields_ = [("block_id", ctypes.c_uint64), ("bytes", ctypes.c_uint64)]
+
+
 class KvFrameDesc(ctypes.Structure):
     _fields_ = [("layer_idx", ctypes.c_int64), ("global_seq_start", ctypes.c_int64),
                 ("global_seq_end", ctypes.c_int64), ("dtype", ctypes.c_int32), ("num_heads", ctypes.c_int32),
@@ -226,6 +244,20 @@ def lib() -> ctypes.CDLL:
         "hcp_ringattn_runtime_shutdown": ([vp], ctypes.c_int),
         "hcp_ringattn_cxx_smoke_domain_count": ([], ctypes.c_int),
         "hcp_synth_normals": ([ctypes.c_uint64, i64, i64, i32, vp, vp], ctypes.c_int),
+        "hcp_block_agent_pair_create": ([ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(vp), ctypes.POINTER(vp)],
+                                        ctypes.c_int),
+        "hcp_block_agent_destroy": ([vp], ctypes.c_int),
+        "hcp_block_register": ([vp, vp, ctypes.c_uint64, ctypes.POINTER(i64), i32, ctypes.POINTER(ctypes.c_uint64),
+                                ctypes.POINTER(BlockDescC)], ctypes.c_int),
+        "hcp_block_deregister": ([vp, ctypes.c_uint64], ctypes.c_int),
+        "hcp_block_local_metadata": ([vp, vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+        "hcp_block_load_remote_metadata": ([vp, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p], ctypes.c_int),
+        "hcp_block_remote_desc": ([vp, ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(RemoteBlockDescC)],
+                                  ctypes.c_int),
+        "hcp_block_submit_transfer": ([vp, ctypes.c_uint64, ctypes.POINTER(RemoteBlockDescC), vp], ctypes.c_int),
+        "hcp_block_poll_transfers": ([vp, ctypes.POINTER(BlockCompletionC), ctypes.c_size_t,
+                                      ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+        "hcp_block_wire_bytes": ([vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
         "hcp_ring_replay_timing": ([i32], ctypes.c_int),
         "hcp_ring_replay_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)],
                                         ctypes.c_int),
@@ -270,6 +302,10 @@ def dtype_code(t) -> int:
 
 
 def _stream(stream=None):
+    """hipStream_t of a torch stream (default: the current one); an int is taken as the
+    raw handle (0: the default stream)."""
+    if isinstance(stream, int):
+        return ctypes.c_void_p(stream)
     torch = _torch()
     s = stream if stream is not None else torch.cuda.current_stream()
     return ctypes.c_void_p(s.cuda_stream)
@@ -592,6 +628,84 @@ def ring_attention_replay_paged(q, pool, block_table, chunks, causal=True, scale
                                                _stream(stream)))
     del arr
     return out, lse_out
+
+
+# ---------------------------------------------------------------------------------
+# (6b) block-direct transport (block_transport.rs KvBlockTransport)
+# ---------------------------------------------------------------------------------
+class BlockAgent:
+    """One side of a linked pair of block transports (the KvBlockTransport methods of
+    block_transport.rs:97-126 over hcp_block_*).  Blocks are device or host memory given
+    as torch tensors / numpy arrays (kept referenced while registered)."""
+
+    def __init__(self, handle, name: str):
+        self._h = ctypes.c_void_p(handle)
+        self.name = name
+        self._keep = {}
+
+    @staticmethod
+    def pair(name_a: str = "agent-a", name_b: str = "agent-b"):
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        _check(lib().hcp_block_agent_pair_create(name_a.encode(), name_b.encode(), ctypes.byref(a), ctypes.byref(b)))
+        return BlockAgent(a.value, name_a), BlockAgent(b.value, name_b)
+
+    def register_block(self, tensor):
+        """(block id, descriptor dict) of the tensor's memory, its shape in the metadata."""
+        if hasattr(tensor, "data_ptr"):
+            ptr, nbytes, shape = tensor.data_ptr(), tensor.numel() * tensor.element_size(), list(tensor.shape)
+        else:
+            ptr, nbytes, shape = tensor.ctypes.data, tensor.nbytes, list(tensor.shape)
+        dims = (ctypes.c_int64 * max(len(shape), 1))(*shape)
+        bid, desc = ctypes.c_uint64(), BlockDescC()
+        _check(lib().hcp_block_register(self._h, ptr, nbytes, dims, len(shape), ctypes.byref(bid), ctypes.byref(desc)))
+        self._keep[bid.value] = tensor
+        return bid.value, block_desc_dict(desc)
+
+    def deregister_block(self, block_id: int):
+        _check(lib().hcp_block_deregister(self._h, block_id))
+        self._keep.pop(block_id, None)
+
+    def local_metadata(self) -> bytes:
+        n = ctypes.c_size_t()
+        _check(lib().hcp_block_local_metadata(self._h, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(max(n.value, 1))
+        _check(lib().hcp_block_local_metadata(self._h, buf, n.value, ctypes.byref(n)))
+        return buf.raw[: n.value]
+
+    def load_remote_metadata(self, blob: bytes) -> str:
+        name = ctypes.create_string_buffer(BLOCK_AGENT_MAX)
+        _check(lib().hcp_block_load_remote_metadata(self._h, blob, len(blob), name))
+        return name.value.decode()
+
+    def remote_desc(self, peer: str, block_id: int) -> RemoteBlockDescC:
+        out = RemoteBlockDescC()
+        _check(lib().hcp_block_remote_desc(self._h, peer.encode(), block_id, ctypes.byref(out)))
+        return out
+
+    def submit_transfer(self, local_block_id: int, remote: RemoteBlockDescC, stream=None):
+        _check(lib().hcp_block_submit_transfer(self._h, local_block_id, ctypes.byref(remote), _stream(stream)))
+
+    def poll_transfers(self, capacity: int = 64):
+        out = (BlockCompletionC * capacity)()
+        n = ctypes.c_size_t()
+        _check(lib().hcp_block_poll_transfers(self._h, out, capacity, ctypes.byref(n)))
+        return [(out[i].block_id, out[i].bytes) for i in range(n.value)]
+
+    def wire_bytes(self):
+        sent, recv = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib().hcp_block_wire_bytes(self._h, ctypes.byref(sent), ctypes.byref(recv)))
+        return sent.value, recv.value
+
+    def destroy(self):
+        if self._h:
+            _check(lib().hcp_block_agent_destroy(self._h))
+            self._h = None
+            self._keep.clear()
+
+
+def block_desc_dict(d: BlockDescC) -> dict:
+    return {"addr": d.addr, "len": d.len, "dev_id": d.dev_id, "mem_type": d.mem_type,
+            "meta": bytes(d.meta[: d.meta_len])}
 
 
 # ---------------------------------------------------------------------------------

@@ -7,6 +7,7 @@
 // counterpart of HcpRingAttentionBackend::ring_attention, ring.rs:861-1398) lives here
 // too; it only enqueues kernels.
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -488,6 +489,9 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
 }
 
 }  // namespace
+
+int block_transport_guard(const char* fn, const std::function<void()>& body) { return guarded(fn, body); }
+
 }  // namespace hcp
 
 using namespace hcp;

@@ -580,6 +580,73 @@ int hcp_ringattn_runtime_shutdown(hcp_ringattn_runtime* rt);
 int hcp_ringattn_cxx_smoke_domain_count(void);
 
 /* ---------------------------------------------------------------------------------
+ * (6b) Block-direct transport (KvBlockTransport, rust/src/model/transport/
+ * block_transport.rs:36-126; in-memory reference implementation serialized_block.rs).
+ *
+ * The NIXL-style lifecycle on one GPU: two agents are created as a linked pair
+ * (SerializedBlockTransport::create_pair, serialized_block.rs:69-77); each registers
+ * memory blocks (register_block), advertises them as a metadata blob
+ * (local_metadata), ingests the peer's blob (load_remote_metadata), posts transfers
+ * from a local block into a peer block (submit_transfer: an asynchronous copy of the
+ * raw bytes on `stream`, device or host memory) and collects the completions posted to
+ * it without blocking (poll_transfers: an event query per transfer).  Descriptors are
+ * BlockDesc / RemoteBlockDesc in the reference's field order; mem_type follows
+ * BlockMemType (0 = Dram, 1 = Vram: device memory registers as Vram with dev_id = its
+ * device); meta is serde_json's compact text of the registered shape (e.g. "[1,2,3,4]",
+ * serialized_block.rs:103-115).  Metadata blobs are byte-compatible with the
+ * reference's bincode 1.3.3 serialisation of AgentMetadata (little-endian, u64
+ * lengths, u32 enum variants, blocks in ascending id).  A transfer needs equal block
+ * lengths and the peer's current registration (-6 otherwise); the wire counters count
+ * the bytes of posted transfers (sent) and polled completions (recv).  All calls on
+ * one pair are serialised by a mutex; strings are NUL-terminated host memory.
+ * ------------------------------------------------------------------------------- */
+#define HCP_BLOCK_AGENT_MAX 64
+#define HCP_BLOCK_META_MAX 256
+
+enum hcp_block_mem_type { HCP_BLOCK_DRAM = 0, HCP_BLOCK_VRAM = 1 };
+
+typedef struct hcp_block_desc {
+  uint64_t addr;
+  uint64_t len;
+  uint64_t dev_id;
+  int32_t mem_type;                 /* hcp_block_mem_type */
+  uint32_t meta_len;
+  uint8_t meta[HCP_BLOCK_META_MAX];
+} hcp_block_desc;
+
+typedef struct hcp_remote_block_desc {
+  char agent[HCP_BLOCK_AGENT_MAX];  /* owner agent name */
+  uint64_t block_id;                /* owner-local block id */
+  hcp_block_desc desc;
+} hcp_remote_block_desc;
+
+typedef struct hcp_block_completion {
+  uint64_t block_id;                /* receiver-local block that was written */
+  uint64_t bytes;
+} hcp_block_completion;
+
+typedef struct hcp_block_agent hcp_block_agent;
+
+int hcp_block_agent_pair_create(const char* name_a, const char* name_b, hcp_block_agent** a,
+                                hcp_block_agent** b);
+int hcp_block_agent_destroy(hcp_block_agent* agent);
+int hcp_block_register(hcp_block_agent* agent, void* data, uint64_t bytes, const int64_t* shape,
+                       int32_t ndim, uint64_t* block_id, hcp_block_desc* desc_out);
+int hcp_block_deregister(hcp_block_agent* agent, uint64_t block_id);
+/* out may be NULL to query the size into *written. */
+int hcp_block_local_metadata(const hcp_block_agent* agent, void* out, size_t capacity, size_t* written);
+/* agent_out (HCP_BLOCK_AGENT_MAX bytes, may be NULL) receives the peer's agent name. */
+int hcp_block_load_remote_metadata(hcp_block_agent* agent, const void* blob, size_t len, char* agent_out);
+/* The descriptor `peer` advertised for block_id in its last loaded metadata. */
+int hcp_block_remote_desc(const hcp_block_agent* agent, const char* peer, uint64_t block_id,
+                          hcp_remote_block_desc* out);
+int hcp_block_submit_transfer(hcp_block_agent* agent, uint64_t local_block_id,
+                              const hcp_remote_block_desc* remote, void* stream);
+int hcp_block_poll_transfers(hcp_block_agent* agent, hcp_block_completion* out, size_t capacity,
+                             size_t* n);
+int hcp_block_wire_bytes(const hcp_block_agent* agent, uint64_t* sent, uint64_t* recv);
+
+/* ---------------------------------------------------------------------------------
  * Replay kernel timing (no reference counterpart; benchmark instrumentation; the
  * reference logs wall-clock compute per phase to HCP_PERF_LOG, ring.rs:820-844).
  *

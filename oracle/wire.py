@@ -6,6 +6,8 @@ Follows rust/src/model/transport/tcp.rs:
 * :func:`kv_block_frame`      serialize_block_to_buffer :161-207 (+ tensor_to_bytes :90-110)
 * :func:`ring_packet_frame`   serialize_packet_to_buffer :209-243
 * :func:`parse_kv_block_frame` the KV branch of decode_frame_from_reader :604-787
+* :func:`agent_metadata_bincode` the AgentMetadata blob of the block transport
+  (block_transport.rs:36-86, serialized_block.rs:125-141)
 
 serde_json 1.0.149 (rust/Cargo.lock), without its "preserve_order" feature, keeps a
 ``json!`` object in a BTreeMap, so ``to_string()`` writes the keys sorted, with no
@@ -103,3 +105,24 @@ def parse_kv_block_frame(frame: bytes):
         pm = meta["position_ids"]
         pos = np.frombuffer(frame[off:off + pm["bytes"]], dtype="<i8").reshape(pm["shape"])
     return meta, k, v, pos
+
+
+def agent_metadata_bincode(agent: str, blocks) -> bytes:
+    """bincode 1.3.3 ``serialize(&AgentMetadata { agent, blocks })`` (rust/Cargo.lock;
+    serialized_block.rs:125-141), its default configuration: little-endian, fixed-width
+    integers, u64 lengths before strings and sequences, u32 variant index for a unit
+    enum, struct fields in declaration order (block_transport.rs:36-86).  ``blocks`` is a
+    list of (owner agent, block_id, addr, len, dev_id, mem_type (0 Dram, 1 Vram), meta
+    bytes)."""
+    def s_(b: bytes) -> bytes:
+        return struct.pack("<Q", len(b)) + b
+    out = s_(agent.encode()) + struct.pack("<Q", len(blocks))
+    for owner, bid, addr, ln, dev, mem, meta in blocks:
+        out += s_(owner.encode()) + struct.pack("<QQQQI", bid, addr, ln, dev, mem) + s_(meta)
+    return out
+
+
+def shape_meta(shape) -> bytes:
+    """serde_json::to_vec of a Vec<i64> shape: compact, e.g. b"[1,2,3,4]"
+    (serialized_block.rs:103-115)."""
+    return ("[" + ",".join(str(int(x)) for x in shape) + "]").encode()

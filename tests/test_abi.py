@@ -147,7 +147,10 @@ NULL_CHECKED = [
     "hcp_qkv_rope_project", "hcp_qkv_rope_project_paged", "hcp_ring_build_assignment",
     "hcp_ring_domain_positions", "hcp_ring_inverse_perm", "hcp_rope_table",
     "hcp_ringattn_runtime_init", "hcp_ringattn_runtime_bind_layer",
-    "hcp_ringattn_runtime_run_layer", "hcp_ringattn_runtime_shutdown",
+    "hcp_ringattn_runtime_run_layer", "hcp_ringattn_runtime_shutdown", "hcp_block_agent_pair_create",
+    "hcp_block_agent_destroy", "hcp_block_register", "hcp_block_deregister", "hcp_block_local_metadata",
+    "hcp_block_load_remote_metadata", "hcp_block_remote_desc", "hcp_block_submit_transfer",
+    "hcp_block_poll_transfers", "hcp_block_wire_bytes",
 ]
 
 
@@ -195,3 +198,44 @@ def test_m0_scan_accepts_the_dma_sequence_and_rejects_anything_else():
     for ins in planted:
         with pytest.raises(RuntimeError):
             b.scan_m0(ins)
+
+
+def test_block_transport_metadata_without_a_gpu(hcp):
+    # register -> local_metadata -> load_remote_metadata on host blocks (Dram): the blob
+    # is the bincode AgentMetadata of the oracle (field order of block_transport.rs:36-86)
+    from oracle import wire as W
+    a, b = hcp.BlockAgent.pair("agent-a", "agent-b")
+    try:
+        x = np.arange(24, dtype=np.float32).reshape(1, 2, 3, 4)
+        y = np.zeros((5, 7), dtype=np.int16)
+        ix, dx = a.register_block(x)
+        iy, dy = a.register_block(y)
+        assert (ix, iy) == (0, 1)
+        assert dx["mem_type"] == 0 and dx["meta"] == b"[1,2,3,4]" and dx["len"] == 96 and dx["addr"] == x.ctypes.data
+        blob = a.local_metadata()
+        want = W.agent_metadata_bincode("agent-a", [("agent-a", i, d["addr"], d["len"], d["dev_id"], d["mem_type"],
+                                                     d["meta"]) for i, d in ((ix, dx), (iy, dy))])
+        assert blob == want
+        assert b.load_remote_metadata(blob) == "agent-a"
+        r = b.remote_desc("agent-a", iy)
+        assert r.agent == b"agent-a" and r.block_id == iy and hcp.block_desc_dict(r.desc) == dy
+        a.deregister_block(ix)
+        assert a.local_metadata() == W.agent_metadata_bincode("agent-a", [("agent-a", iy, dy["addr"], dy["len"], 0, 0,
+                                                                           dy["meta"])])
+        # malformed blobs: short, trailing byte, unknown BlockMemType variant
+        for bad in (blob[:-1], blob + b"\0", blob[:blob.index(b"[1,2") - 12] + b"\2" + blob[blob.index(b"[1,2") - 11:]):
+            with pytest.raises(hcp.HcpRingError) as e:
+                b.load_remote_metadata(bad)
+            assert e.value.code == -6
+        # transfers are checked before any device work: unknown local block, length mismatch
+        z = np.zeros(3, dtype=np.float32)
+        iz, _ = b.register_block(z)
+        b2 = a.load_remote_metadata(b.local_metadata())
+        with pytest.raises(hcp.HcpRingError):
+            a.submit_transfer(ix, a.remote_desc(b2, iz), stream=0)          # deregistered
+        with pytest.raises(hcp.HcpRingError):
+            a.submit_transfer(iy, a.remote_desc(b2, iz), stream=0)          # 70 bytes into 12
+        assert b.poll_transfers() == [] and a.wire_bytes() == (0, 0)
+    finally:
+        a.destroy()
+        b.destroy()

@@ -512,3 +512,25 @@ def test_qkv_forward_oracle_matches_closed_form():
     assert np.abs(q[0].numpy() - _rope_f64(rq, pos.astype(np.float64), d, 10000.0)).max() < 1e-3
     assert np.abs(k[0].numpy() - _rope_f64(rk, pos.astype(np.float64), d, 10000.0)).max() < 1e-3
     assert np.abs(v[0].numpy() - rv).max() < 1e-4
+
+
+def test_agent_metadata_bincode_known_answers():
+    # Byte strings written from bincode 1.3's published default encoding (little-endian,
+    # u64 length prefixes, u32 variant index), independent of the oracle's code.
+    from oracle import wire as W
+    assert W.agent_metadata_bincode("a", []) == bytes.fromhex("0100000000000000" "61" "0000000000000000")
+    one = W.agent_metadata_bincode("ab", [("ab", 3, 0x1122334455667788, 96, 1, 1, b"[2]")])
+    assert one == bytes.fromhex(
+        "0200000000000000" "6162"            # agent "ab"
+        "0100000000000000"                   # one block
+        "0200000000000000" "6162"            # owner agent
+        "0300000000000000"                   # block_id 3
+        "8877665544332211"                   # addr
+        "6000000000000000"                   # len 96
+        "0100000000000000"                   # dev_id 1
+        "01000000"                           # BlockMemType::Vram
+        "0300000000000000" "5b325d")         # meta "[2]"
+    assert W.shape_meta([1, 2, 3, 4]) == b"[1,2,3,4]" and W.shape_meta([]) == b"[]"
+    # a planted mistake (u32 length prefixes, as bincode's varint or a 32-bit config would
+    # not give) changes the bytes
+    assert W.agent_metadata_bincode("a", []) != bytes.fromhex("01000000" "61" "00000000")
