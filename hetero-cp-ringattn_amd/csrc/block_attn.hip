@@ -743,19 +743,40 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     k_voff[j] = static_cast<uint32_t>(r * k_ss * 2 + ((p ^ (r & 15)) << 4));
     v_voff[j] = static_cast<uint32_t>(r * v_ss * 2 + ((p ^ (4 * (r & 3))) << 4));
   }
+  // Buffer descriptors of a tile's rows [kr, ke): a few scalar instructions per tile
+  // (every wave of the CU shares one scalar unit, and the DMA issue sits on the
+  // critical path of both wave groups).  The launcher keeps a tile's bytes (BK rows)
+  // below 2^31, so row offsets and sizes are 32-bit products.
+  const uint64_t k_addr = reinterpret_cast<uint64_t>(kbase), v_addr = reinterpret_cast<uint64_t>(vbase);
+  const uint32_t k_rb = static_cast<uint32_t>(k_ss) * 2u, v_rb = static_cast<uint32_t>(v_ss) * 2u;
+  auto tile_srd = [](uint64_t base, uint32_t rb, int kr, int ke) __attribute__((always_inline)) {
+    const uint64_t at = base + static_cast<uint64_t>(static_cast<uint32_t>(kr)) * rb;
+    u32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(at));
+    r[1] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(at >> 32) & 0xffffu);
+    r[2] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(ke - kr) * rb);
+    r[3] = 0x00020000u;
+    return r;
+  };
+  auto dma_k = [&](int kr, int ke, int buf) __attribute__((always_inline)) {
+    const u32x4 sr = tile_srd(k_addr, k_rb, kr, ke);
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j) dma16(sr, k_voff[j], k_lds0 + buf * kTile + j * 1024);
+  };
+  auto dma_v = [&](int kr, int ke, int buf) __attribute__((always_inline)) {
+    const u32x4 sr = tile_srd(v_addr, v_rb, kr, ke);
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j) dma16(sr, v_voff[j], v_lds0 + buf * kTile + j * 1024);
+  };
   auto issue_k = [&](int t, int buf) __attribute__((always_inline)) {
     int kr, ke;
     tile_rows(t, kr, ke);
-    const u32x4 s = make_srd(kbase + static_cast<int64_t>(kr) * k_ss, static_cast<int64_t>(ke - kr) * k_ss * 2);
-#pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) dma16(s, k_voff[j], k_lds0 + buf * kTile + j * 1024);
+    dma_k(kr, ke, buf);
   };
   auto issue_v = [&](int t, int buf) __attribute__((always_inline)) {
     int kr, ke;
     tile_rows(t, kr, ke);
-    const u32x4 s = make_srd(vbase + static_cast<int64_t>(kr) * v_ss, static_cast<int64_t>(ke - kr) * v_ss * 2);
-#pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) dma16(s, v_voff[j], v_lds0 + buf * kTile + j * 1024);
+    dma_v(kr, ke, buf);
   };
 
   // prologue: K_0 .. K_{NBK-2}, V_0 .. V_{NBV-3}
@@ -918,17 +939,19 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
         for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
       m_run = m_new;
     }
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int b = 0; b < NKB; ++b) {
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][r], c, -m_run));
-        l_run += p[r];
+        ls[r & 3] += p[r];
       }
       pf[2 * b] = Ops::pack(p);
       pf[2 * b + 1] = Ops::pack(p + 8);
     }
+    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 #pragma unroll
     for (int s = 0; s < NPS; ++s) pin(pf[s]);
     pin(l_run);
@@ -946,8 +969,19 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     return w >= 0 && w + NBV - 2 < n_tiles ? kDmaPerWave : 0;
   };
   auto issue = [&](int u) __attribute__((always_inline)) {
-    if (u + NBK - 1 < n_tiles) issue_k(u + NBK - 1, (u + NBK - 1) % NBK);
-    if (u + NBV - 2 < n_tiles) issue_v(u + NBV - 2, (u + NBV - 2) % NBV);
+    if constexpr (NBK - 1 == NBV - 2) {
+      // K and V of the same tile: one row range for both
+      const int t = u + NBK - 1;
+      if (t < n_tiles) {
+        int kr, ke;
+        tile_rows(t, kr, ke);
+        dma_k(kr, ke, t % NBK);
+        dma_v(kr, ke, t % NBV);
+      }
+    } else {
+      if (u + NBK - 1 < n_tiles) issue_k(u + NBK - 1, (u + NBK - 1) % NBK);
+      if (u + NBV - 2 < n_tiles) issue_v(u + NBV - 2, (u + NBV - 2) % NBV);
+    }
   };
   auto settle = [&](int u) __attribute__((always_inline)) {
     if (u < n_tiles) {
@@ -1152,6 +1186,13 @@ static int heads_per_group(int rep) {
   return 1;
 }
 
+// The head-dim-128 kernels form buffer descriptors with 32-bit row arithmetic: a tile of
+// kBK3 rows of either view must stay below 2^31 bytes.
+static void check_tile_bytes(int64_t k_ss, int64_t v_ss) {
+  require(k_ss > 0 && v_ss > 0 && k_ss * 2 * kBK3 < (int64_t(1) << 31) && v_ss * 2 * kBK3 < (int64_t(1) << 31),
+          "k/v sequence strides too large for the matrix-core kernel");
+}
+
 static BlockArgs make_args(const BlockLaunch& L) {
   BlockArgs a;
   a.q = static_cast<const uint16_t*>(L.q);
@@ -1184,6 +1225,7 @@ static BlockArgs make_args(const BlockLaunch& L) {
 template <int DT>
 static void launch_pingpong(BlockGroup& grp, hipStream_t stream) {
   const BlockArgs& a0 = grp.a[0];
+  for (int i = 0; i < grp.n; ++i) check_tile_bytes(grp.a[i].k_ss, grp.a[i].v_ss);
   grp.qt_begin[0] = 0;
   for (int i = 0; i < grp.n; ++i) grp.qt_begin[i + 1] = grp.qt_begin[i] + grp.a[i].n_qtiles;
   const dim3 grid(static_cast<unsigned>(grp.qt_begin[grp.n] * a0.n_groups));
@@ -1328,6 +1370,7 @@ bool ring_fused_applies(int dtype, int d) { return (dtype == kBF16 || dtype == k
 
 void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
   require(ring_fused_applies(L.dtype, L.d), "fused ring: dtype must be BF16 or F16 with head_dim 128");
+  check_tile_bytes(L.k_ss, L.v_ss);
   require(L.n >= 1 && L.n <= kMaxDomains, "fused ring: 1 to 64 domains");
   RingPlan p{};
   p.q = static_cast<const uint16_t*>(L.q);
