@@ -83,6 +83,7 @@ constexpr int kKPad = 8;          // bf16 pad per K row in LDS
 constexpr int kVtStride = kBK + 8;  // bf16 per V^T row in LDS (144 B)
 constexpr float kRescaleThreshold = 8.0f;
 constexpr float kInitMax = -1.0e30f;
+constexpr float kGrowSum = 256.0f;  // 2^kRescaleThreshold: largest partial row sum kept without a max pass
 
 // C-row r of a 32x32 S^T block holds key kperm(r) of that block:
 // r = j*8 + h*4 + i  ->  16*(j/2) + 8*h + 4*(j%2) + i.
@@ -797,16 +798,17 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   }
 
   const int krow = kperm(lcol);
-  uint32_t k_rd[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) k_rd[s] = krow * (D * 2) + (((lhalf + 2 * s) ^ (krow & 15)) << 4);
+  // K fragment s of a lane sits at k_rd0 ^ (s << 5) in a tile: (lhalf + 2s) ^ (krow & 15)
+  // changes only bits 1-3 of the 16-byte column index with s, and tile bases are
+  // 1 KiB-aligned, so the XOR commutes with adding the base.
+  const uint32_t k_rd0 = krow * (D * 2) + ((lhalf ^ (krow & 15)) << 4);
   const int g16 = lane >> 4, sl = lane & 15;
   uint32_t v_rd[DB];
 #pragma unroll
   for (int b = 0; b < DB; ++b)
     v_rd[b] = (8 * (g16 >> 1) + (sl >> 2)) * (D * 2) +
               ((4 * (b ^ (sl >> 2)) + 2 * (g16 & 1) + ((sl & 3) >> 1)) << 4) + 8 * (sl & 1);
-  const char* k_lds_c = reinterpret_cast<const char*>(k_lds);
+  const uint32_t k_lds_off = lds_offset(k_lds);
   const char* v_lds_c = reinterpret_cast<const char*>(v_lds);
 
   f32x16 oacc[DB];
@@ -858,16 +860,18 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     }
   };
   auto s_part = [&](int kb) __attribute__((always_inline)) {
-    const char* kl = k_lds_c + kb * kTile;
+    const uint32_t kl = k_lds_off + kb * kTile + k_rd0;
 #pragma unroll
     for (int b = 0; b < NKB; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[b][r] = 0.f;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
+      const uint32_t ks = kl ^ static_cast<uint32_t>(s << 5);
 #pragma unroll
       for (int b = 0; b < NKB; ++b) {
-        const frag kf = as_frag<frag>(*reinterpret_cast<const u32x4*>(kl + k_rd[s] + b * 32 * D * 2));
+        const frag kf = as_frag<frag>(*reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+            static_cast<uintptr_t>(ks + b * 32 * D * 2)));
         sacc[b] = Ops::mma(kf, qf[s], sacc[b]);
       }
     }
@@ -900,7 +904,15 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     for (int b = 0; b < NKB; ++b) pin(sacc[b]);
   };
 
-  // ---- X phase: mask, tile max, lazy rescale, P = 2^(s*c - m) of the next tile ----
+  // ---- X phase: mask, P = 2^(s*c - m) against the running reference max m, lazy
+  // rescale.  The tile max (32 v_max3 and a cross-lane step per tile) is an eighth of
+  // the phase's VALU instructions, and VALU issue (about one instruction per 7 cycles
+  // per SIMD while the other wave's MFMAs run) bounds these kernels as much as the
+  // MFMA rate does, so the max is computed only when needed:
+  // on the first tile, and when some lane's partial row sum leaves [0, 2^T] (every p
+  // is at most that sum, so a sum within bounds means no p exceeded 2^T and the tile
+  // stands; otherwise the tile is redone against the new max, as the eager scheme
+  // would have done). ----
   auto xphase = [&](int t) __attribute__((always_inline)) {
     int kv0, ke;
     tile_rows(t, kv0, ke);
@@ -922,14 +934,34 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
           sacc[b][r] = kl0 <= lim ? sacc[b][r] : -INFINITY;
         }
     }
-    float tmax = -INFINITY;
+    auto exp_pack = [&](float& lsum) __attribute__((always_inline)) {
+      float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int b = 0; b < NKB; ++b)
+      for (int b = 0; b < NKB; ++b) {
+        float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[b][r]);
-    tmax = max_xor32(tmax) * c;
-    const bool grow = tmax > m_run + kRescaleThreshold;
-    if (__any(grow)) {
+        for (int r = 0; r < 16; ++r) {
+          p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][r], c, -m_run));
+          ls[r & 3] += p[r];
+        }
+        pf[2 * b] = Ops::pack(p);
+        pf[2 * b + 1] = Ops::pack(p + 8);
+      }
+      lsum = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    };
+    float lsum = 0.f;
+    bool redo = t == 0;
+    if (!redo) {
+      exp_pack(lsum);
+      redo = __any(!(lsum <= kGrowSum));
+    }
+    if (redo) {
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < NKB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[b][r]);
+      tmax = max_xor32(tmax) * c;
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = exp2f(m_run - m_new);
       l_run *= alpha;
@@ -938,20 +970,9 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
       m_run = m_new;
+      exp_pack(lsum);
     }
-    float ls[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int b = 0; b < NKB; ++b) {
-      float p[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][r], c, -m_run));
-        ls[r & 3] += p[r];
-      }
-      pf[2 * b] = Ops::pack(p);
-      pf[2 * b + 1] = Ops::pack(p + 8);
-    }
-    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    l_run += lsum;
 #pragma unroll
     for (int s = 0; s < NPS; ++s) pin(pf[s]);
     pin(l_run);
@@ -1002,41 +1023,37 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   // Ring positions of super-step u: rk = u mod NBK (K_u), rv = (u - 1) mod NBV (V_{u-1}).
   auto next = [](int r, int nb) __attribute__((always_inline)) { return r + 1 == nb ? 0 : r + 1; };
   // The lead group issues its DMA share between its two phases, so its MFMA phase
-  // starts right after the barrier that opens the super-step.
+  // starts right after the barrier that opens the super-step; the lag group passes the
+  // barrier right after its MFMA phase and issues the next super-step's share before
+  // its X phase.  Both groups run one loop body (M, then X, of tile u): a single copy
+  // of the phases in the kernel, which also keeps the register allocation to one
+  // assignment of the accumulators.
   if (lead) {
     if (live(0)) s_part(0);
     issue(0);
     if (live(0)) xphase(0);
     settle(0);
-    int u = 1, rk = 1 % NBK, rv = 0;
-    for (; u <= hot; ++u, rk = next(rk, NBK), rv = next(rv, NBV)) {
-      m_full(rk, rv);
-      issue(u);
-      xphase(u);
-      settle(u);
-    }
-    for (; u <= n_tiles; ++u, rv = next(rv, NBV)) {
-      if (live(u - 1)) pv_part(rv);
-      issue(u);
-      settle(u);
-    }
   } else {
     issue(0);
     if (live(0)) s_part(0);
     settle(0);
-    int u = 1, rk = 1 % NBK, rv = 0;
-    for (; u <= hot; ++u, rk = next(rk, NBK), rv = next(rv, NBV)) {
-      issue(u);
-      xphase(u - 1);
-      m_full(rk, rv);
-      settle(u);
-    }
-    for (; u <= n_tiles; ++u, rv = next(rv, NBV)) {
-      issue(u);
-      if (live(u - 1)) xphase(u - 1);
-      if (live(u - 1)) pv_part(rv);
-      settle(u);
-    }
+    issue(1);
+    if (live(0)) xphase(0);
+  }
+  const int lag = lead ? 0 : 1;
+  int u = 1, rk = 1 % NBK, rv = 0;
+  for (; u <= hot; ++u, rk = next(rk, NBK), rv = next(rv, NBV)) {
+    m_full(rk, rv);
+    if (!lead) settle(u);
+    issue(u + lag);
+    xphase(u);
+    if (lead) settle(u);
+  }
+  for (; u <= n_tiles; ++u, rv = next(rv, NBV)) {
+    if (live(u - 1)) pv_part(rv);
+    if (lead) issue(u);
+    settle(u);
+    if (!lead) issue(u + 1);
   }
 
   if (my_q >= lq) return;
