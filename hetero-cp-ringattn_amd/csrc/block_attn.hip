@@ -60,6 +60,8 @@ struct BlockArgs {
   float* fin_lse;
   int64_t fin_lse_hs;
   const int32_t* q_lim;    // positions mode when non-null (causal): row i sees keys [0, q_lim[i])
+  int32_t d;               // head dim of the views and the state (the head-dim-128 kernel: <= 128,
+                           // a multiple of 8; columns d .. 127 are zero padding in LDS and registers)
 };
 
 // Up to kMaxGroup independent (query chunk, KV chunk) pairs with the same head layout in
@@ -221,14 +223,14 @@ __device__ __forceinline__ void store4(void* base, int dtype, int64_t off, float
 // 4-wide d slices of each 8-wide group.
 template <int D>
 __device__ __forceinline__ void write_row(const BlockArgs& a, int head, int my_q, int lhalf,
-                                          const f32x16 (&oacc)[D / 32], float m_run, float l_tot) {
+                                          const f32x16 (&oacc)[D / 32], float m_run, float l_tot, int dn = D) {
   constexpr int DB = D / 32;
   const bool any = l_tot > 0.f;
   const float inv = any ? 1.f / l_tot : 0.f;
   const float lse_new = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
   const int64_t row = static_cast<int64_t>(head) * a.lq + my_q;
   // the running fp32 state (null in a fused ring, which writes final rows only)
-  float* orow = a.o != nullptr ? a.o + row * D : nullptr;
+  float* orow = a.o != nullptr ? a.o + row * dn : nullptr;
   float c_old = 0.f, c_new = inv, lse_out = lse_new;
   if (a.accumulate) {
     const float lse_old = a.lse[row];
@@ -248,6 +250,7 @@ __device__ __forceinline__ void write_row(const BlockArgs& a, int head, int my_q
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int dcol = 32 * b + 8 * j + 4 * lhalf;
+      if (dcol >= dn) continue;  // zero-padded columns
       float x0 = c_new * oacc[b][4 * j], x1 = c_new * oacc[b][4 * j + 1];
       float x2 = c_new * oacc[b][4 * j + 2], x3 = c_new * oacc[b][4 * j + 3];
       if (a.accumulate) {
@@ -271,7 +274,7 @@ __device__ __forceinline__ void write_row(const BlockArgs& a, int head, int my_q
 // lanes l and l + 32 hold the two interleaved 4-wide d slices of each 8-wide group.
 template <int D>
 __device__ __forceinline__ void write_final_row(void* out, int dtype, int64_t off, float* lse, int lhalf,
-                                                const f32x16 (&oacc)[D / 32], float m_run, float l_tot) {
+                                                const f32x16 (&oacc)[D / 32], float m_run, float l_tot, int dn) {
   constexpr int DB = D / 32;
   const bool any = l_tot > 0.f;
   const float inv = any ? 1.f / l_tot : 0.f;
@@ -280,6 +283,7 @@ __device__ __forceinline__ void write_final_row(void* out, int dtype, int64_t of
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int dcol = 32 * b + 8 * j + 4 * lhalf;
+      if (dcol >= dn) continue;  // zero-padded columns
       store4(out, dtype, off + dcol, inv * oacc[b][4 * j], inv * oacc[b][4 * j + 1], inv * oacc[b][4 * j + 2],
              inv * oacc[b][4 * j + 3]);
     }
@@ -599,6 +603,7 @@ struct RingPlan {
   float* lse;                                   // [Hq, S] rows, or null
   int64_t lse_hs;
   int32_t dtype;                                // query / output dtype
+  int32_t d;                                    // head dim (<= 128, multiple of 8; zero-padded to 128)
   int32_t hq, hkv, rep, n_groups, n, causal;
   float scale_log2;
   int32_t off[kMaxDomains], len[kMaxDomains];   // rows (= global positions) of each domain
@@ -641,7 +646,7 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   const BlockArgs* ap = nullptr;  // block mode: the block of this workgroup
   const uint16_t *qv, *kv, *vv;
   int64_t q_hs, q_ss, k_hs, k_ss, v_hs, v_ss;
-  int lq, rep, causal;
+  int lq, rep, causal, dn;
   float c;
   if constexpr (RING) {
     const int logical = blockIdx.x;
@@ -658,6 +663,7 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     rep = plan.rep;
     causal = plan.causal;
     c = plan.scale_log2;
+    dn = plan.d;
   } else {
     const int logical = xcd_remap(blockIdx.x, gridDim.x);
     const int per_hg = plan.qt_begin[plan.n];
@@ -673,6 +679,7 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     rep = ap->rep;
     causal = ap->causal;
     c = ap->scale_log2;
+    dn = ap->d;
   }
 
   const int head = hg * G + (wave % G);
@@ -741,8 +748,11 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   for (int j = 0; j < kDmaPerWave; ++j) {
     const int r = (wave * kDmaPerWave + j) * 4 + (lane >> 4);
     const int p = lane & 15;
-    k_voff[j] = static_cast<uint32_t>(r * k_ss * 2 + ((p ^ (r & 15)) << 4));
-    v_voff[j] = static_cast<uint32_t>(r * v_ss * 2 + ((p ^ (4 * (r & 3))) << 4));
+    // global chunk p ^ swz(r) of row r; chunks past the head dim get an offset beyond any
+    // tile's records (tiles stay below 2^31 bytes), so the DMA writes zeros there
+    const int kc = p ^ (r & 15), vc = p ^ (4 * (r & 3));
+    k_voff[j] = kc * 8 < dn ? static_cast<uint32_t>(r * k_ss * 2 + (kc << 4)) : 0x80000000u;
+    v_voff[j] = vc * 8 < dn ? static_cast<uint32_t>(r * v_ss * 2 + (vc << 4)) : 0x80000000u;
   }
   // Buffer descriptors of a tile's rows [kr, ke): a few scalar instructions per tile
   // (every wave of the CU shares one scalar unit, and the DMA issue sits on the
@@ -794,7 +804,11 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     const auto qr = make_rsrc(qbase, static_cast<int64_t>(lq - wq0) * q_ss * 2);
     const int32_t qoff = (lcol * static_cast<int32_t>(q_ss) + lhalf * 8) * 2;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = as_frag<frag>(buf_load16(qr, qoff + 32 * s));
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 x = buf_load16(qr, qoff + 32 * s);
+      // head-dim columns 16s + 8*lhalf .. +7; past the head dim: zero padding
+      qf[s] = as_frag<frag>(16 * s + 8 * lhalf < dn ? x : u32x4{0u, 0u, 0u, 0u});
+    }
   }
 
   const int krow = kperm(lcol);
@@ -1061,9 +1075,9 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     const int64_t row = static_cast<int64_t>(plan.off[t_dom]) + my_q;
     write_final_row<D>(plan.out, plan.dtype, head * plan.out_hs + row * plan.out_ss,
                        plan.lse != nullptr ? plan.lse + head * plan.lse_hs + row : nullptr, lhalf, oacc, m_run,
-                       sum_xor32(l_run));
+                       sum_xor32(l_run), dn);
   } else {
-    write_row<D>(*ap, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run));
+    write_row<D>(*ap, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run), dn);
   }
 }
 
@@ -1231,6 +1245,7 @@ static BlockArgs make_args(const BlockLaunch& L) {
   a.fin_out = L.fin_out; a.fin_dtype = L.fin_dtype; a.fin_hs = L.fin_hs; a.fin_ss = L.fin_ss;
   a.fin_lse = L.fin_lse; a.fin_lse_hs = L.fin_lse_hs;
   a.q_lim = L.causal ? L.q_lim : nullptr;
+  a.d = static_cast<int32_t>(L.d);
   const int g = heads_per_group(a.rep);
   a.n_qtiles = static_cast<int32_t>(ceil_div(L.lq, 32 * (kWaves / g)));
   a.n_groups = L.hq / g;
@@ -1315,19 +1330,23 @@ static void launch_general(const BlockLaunch& L, hipStream_t stream) {
   else general_block_kernel<DT, 256><<<grid, kGenRows, 0, stream>>>(a);
 }
 
-// True when the matrix-core kernel handles this shape.
+// Head dims the head-dim-128 kernel takes: up to 128 in 16-byte columns, zero-padded.
+static bool padded_d_ok(int d) { return d > 0 && d <= kD3 && d % 8 == 0 && d != 64; }
+
+// True when the matrix-core kernels handle this shape (head dim 64: its own kernel;
+// other multiples of 8 up to 128: the head-dim-128 kernel with zero padding).
 bool block_uses_mfma(int dtype, int d) {
-  return (dtype == kBF16 || dtype == kF16) && (d == 64 || d == 128);
+  return (dtype == kBF16 || dtype == kF16) && (d == 64 || padded_d_ok(d));
 }
 
 void launch_block_partial(const BlockLaunch& L, hipStream_t stream) {
   if (L.lq == 0) return;
   if (!L.force_general && block_uses_mfma(L.dtype, L.d)) {
     if (L.dtype == kBF16) {
-      if (L.d == 128) launch_mfma<128, kBF16>(L, stream);
+      if (L.d != 64) launch_mfma<128, kBF16>(L, stream);
       else launch_mfma<64, kBF16>(L, stream);
     } else {
-      if (L.d == 128) launch_mfma<128, kF16>(L, stream);
+      if (L.d != 64) launch_mfma<128, kF16>(L, stream);
       else launch_mfma<64, kF16>(L, stream);
     }
   } else {
@@ -1362,7 +1381,7 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
     if (Ls[i].lq > 0) live.push_back(&Ls[i]);
   if (live.empty()) return;
   const BlockLaunch& f = *live[0];
-  bool grouped = !f.force_general && block_uses_mfma(f.dtype, f.d) && f.d == kD3;
+  bool grouped = !f.force_general && block_uses_mfma(f.dtype, f.d) && padded_d_ok(f.d);
   for (const BlockLaunch* L : live)
     grouped = grouped && !L->force_general && L->dtype == f.dtype && L->d == f.d && L->hq == f.hq &&
               L->hkv == f.hkv && (L->causal && L->q_lim != nullptr) == (f.causal && f.q_lim != nullptr);
@@ -1383,10 +1402,11 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
   HCP_HIP(hipGetLastError());
 }
 
-bool ring_fused_applies(int dtype, int d) { return (dtype == kBF16 || dtype == kF16) && d == kD3; }
+bool ring_fused_applies(int dtype, int d) { return (dtype == kBF16 || dtype == kF16) && padded_d_ok(d); }
 
 void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
-  require(ring_fused_applies(L.dtype, L.d), "fused ring: dtype must be BF16 or F16 with head_dim 128");
+  require(ring_fused_applies(L.dtype, L.d),
+          "fused ring: dtype must be BF16 or F16 with head_dim a multiple of 8 up to 128, not 64");
   check_tile_bytes(L.k_ss, L.v_ss);
   require(L.n >= 1 && L.n <= kMaxDomains, "fused ring: 1 to 64 domains");
   RingPlan p{};
@@ -1397,6 +1417,7 @@ void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
   p.out = L.out; p.out_hs = L.out_hs; p.out_ss = L.out_ss;
   p.lse = L.lse; p.lse_hs = L.lse_hs;
   p.dtype = L.dtype;
+  p.d = L.d;
   p.hq = L.hq; p.hkv = L.hkv; p.rep = L.hq / L.hkv;
   const int g = heads_per_group(p.rep);
   const int tq = 32 * (kWaves / g);

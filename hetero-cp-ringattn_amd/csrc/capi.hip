@@ -358,11 +358,14 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
     check_view(v, "v", p.seq);
   }
   // Fused schedule: one launch over every domain's ring (vanilla positions, BF16/F16,
-  // head_dim 128, 16-byte rows); AUTO takes it wherever it applies.
+  // head_dim a multiple of 8 up to 128 other than 64, 16-byte rows); AUTO takes it
+  // wherever it applies.
   const bool fused_ok = !p.positioned && ring_fused_applies(d->dtype, d->head_dim) && mfma_layout_ok(q) &&
                         mfma_layout_ok(out) && (paged || (mfma_layout_ok(k) && mfma_layout_ok(v)));
   if (p.schedule == HCP_SCHEDULE_FUSED)
-    require(fused_ok, "the fused schedule needs BF16/F16, head_dim 128 and 16-byte aligned rows and strides");
+    require(fused_ok,
+            "the fused schedule needs BF16/F16, head_dim a multiple of 8 up to 128 (not 64) and 16-byte "
+            "aligned rows and strides");
   if (fused_ok && p.schedule != HCP_SCHEDULE_PER_STEP) {
     hcp_ring_view kk = k, vv = v;
     if (paged) {

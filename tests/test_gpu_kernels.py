@@ -55,6 +55,11 @@ BLOCK_CASES = [
     ("fp32_general_d64", 150, 150, 8, 8, 64, 0, 0, True, torch.float32),
     ("gqa2_long_noncausal", 160, 1000, 8, 4, 128, 0, 0, False, torch.bfloat16),
     ("gqa2_causal_long_past", 300, 1500, 4, 2, 128, 1200, 0, True, torch.bfloat16),
+    # head dims other than 64 and 128 run in the head-dim-128 kernel, zero-padded
+    ("d96_padded_gqa4", 200, 300, 8, 2, 96, 0, 0, True, torch.bfloat16),
+    ("d112_f16_noncausal", 150, 260, 4, 4, 112, 0, 0, False, torch.float16),
+    ("d48_full_past", 130, 250, 4, 2, 48, 300, 0, True, torch.bfloat16),
+    ("d8_diag", 70, 90, 2, 1, 8, 20, 0, True, torch.bfloat16),
 ]
 
 
@@ -102,14 +107,17 @@ def test_block_partial_head_major_and_unaligned_views(gpu):
         assert np.abs(l.cpu().numpy() - ref_l.T).max() <= LSE_TOL
 
 
-def test_block_partial_accumulate_is_positioned_merge(gpu):
-    # ring.rs:574-603: (o, lse) of source A merged in place with source B.
-    (q, k, v), (q32, k32, v32) = draw(11, [(150, 8, 128), (400, 2, 128), (400, 2, 128)], torch.bfloat16)
+@pytest.mark.parametrize("d", [128, 96], ids=["d128", "d96_padded"])
+def test_block_partial_accumulate_is_positioned_merge(gpu, d):
+    # ring.rs:574-603: (o, lse) of source A merged in place with source B; the running
+    # fp32 state keeps the caller's head dim (96: rows of 96 floats) on the padded path.
+    (q, k, v), (q32, k32, v32) = draw(11, [(150, 8, d), (400, 2, d), (400, 2, d)], torch.bfloat16)
     qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
     o, l = H.positioned_local_compact_partial(qh, 300, kh[:, 250:], vh[:, 250:], 250)
     o2, l2 = H.positioned_merge_compact_partial(qh, 300, o, l, kh[:, :250], vh[:, :250], 0)
     torch.cuda.synchronize()
-    ref_o, ref_l = C.attention_f64(q32, k32, v32, np.arange(300, 450), np.arange(400), 1 / math.sqrt(128))
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, np.arange(300, 450), np.arange(400), 1 / math.sqrt(d))
+    assert H.last_path() == "mfma"
     assert np.abs(o2.cpu().numpy() - ref_o.transpose(1, 0, 2)).max() <= OUT_TOL
     assert np.abs(l2.cpu().numpy() - ref_l.T).max() <= LSE_TOL
 
@@ -288,6 +296,10 @@ RING_CASES = [
     ("gqa6", [96, 450, 200], 12, 2, 128, torch.bfloat16, 54),
     ("gqa8_two_domains", [1000, 536], 16, 2, 128, torch.bfloat16, 55),
     ("single_domain", [700], 8, 2, 128, torch.bfloat16, 56),
+    # zero-padded head dims in the fused ring and the per-step kernel
+    ("d96_padded", [300, 200, 133], 8, 2, 96, torch.bfloat16, 58),
+    ("d80_f16", [150, 260], 4, 4, 80, torch.float16, 59),
+    ("d32_gqa4", [200, 100, 64], 8, 2, 32, torch.bfloat16, 60),
 ]
 
 
@@ -301,8 +313,9 @@ def test_ring_replay_matches_tch_blockwise(gpu, case, schedule):
     out, lse = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
                                        schedule=schedule)
     torch.cuda.synchronize()
-    # BF16/F16 at head_dim 128 take the fused ring kernel unless a per-step schedule is asked for
-    fused = dt != torch.float32 and d == 128 and schedule == "auto"
+    # BF16/F16 at head dims up to 128 (multiples of 8, 64 aside) take the fused ring kernel
+    # unless a per-step schedule is asked for
+    fused = dt != torch.float32 and d % 8 == 0 and d <= 128 and d != 64 and schedule == "auto"
     assert H.last_path() == ("ring_fused" if fused else "general" if dt == torch.float32 else "mfma")
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
@@ -315,10 +328,16 @@ def test_ring_replay_matches_tch_blockwise(gpu, case, schedule):
     else:
         assert np.abs(out - ro).max() <= OUT_TOL
         assert np.abs(lse - rl).max() <= LSE_TOL
-        # and the reference's own dtype (bf16 state) within the bf16 output tolerance
+        # and the reference's own dtype (bf16 state): at least as close to the fp32
+        # restatement as that path is, and within the bf16 output tolerance of it whenever
+        # it is itself within that tolerance of the fp32 result (its bf16 state drifts by
+        # 0.013-0.022 on these cases: 0.022 at d96_padded, where ours is 0.007 off)
         rb = T.ring_attention_replay(scale, bhsd(q32).to(torch.bfloat16), bhsd(k32).to(torch.bfloat16),
-                                     bhsd(v32).to(torch.bfloat16), chunks)
-        assert np.abs(out - rb[0].float().numpy()).max() <= OUT_TOL
+                                     bhsd(v32).to(torch.bfloat16), chunks)[0].float().numpy()
+        err_rb = np.abs(rb - ro).max()
+        assert np.abs(out - ro).max() <= err_rb
+        if err_rb <= OUT_TOL:
+            assert np.abs(out - rb).max() <= OUT_TOL
 
 
 @pytest.mark.parametrize("schedule", ["auto", "per_step", "fused"])
@@ -576,6 +595,7 @@ STRATEGY_RING_CASES = [
     ("fp32_3to1", [768, 256], 4, 4, 64, torch.float32, 60),
     ("bf16_uneven4", [900, 300, 500, 348], 8, 2, 128, torch.bfloat16, 61),
     ("f16_d64_three", [400, 250, 150], 4, 2, 64, torch.float16, 62),
+    ("bf16_d96_padded", [500, 300, 212], 8, 2, 96, torch.bfloat16, 63),
 ]
 
 
