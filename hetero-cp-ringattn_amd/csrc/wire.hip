@@ -17,6 +17,7 @@
 // as fp32; unpack converts back to the storage dtype (exact for values that were bf16
 // or fp16) and keeps one copy of each expanded head group.  The header is built and
 // parsed on the host.
+#include <algorithm>
 #include <charconv>
 #include <cmath>
 #include <cstring>
@@ -100,6 +101,106 @@ __global__ __launch_bounds__(kWireThreads) void wire_unpack_kernel(WireSeg s) {
   }
 }
 
+// Eight consecutive d of one storage row per thread: one 16-byte load (two for fp32)
+// and, for each of the row's rep expanded wire rows, two 16-byte stores (pack); the
+// mirror for unpack, which reads the first wire row of each group.  Needs 16-byte
+// aligned rows (checked by the launcher); index arithmetic in 32 bits when it fits.
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, int64_t i, float (&f)[8]) {
+  if constexpr (DT == kF32) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == kBF16) {
+        f[2 * j] = __uint_as_float(w[j] << 16);
+        f[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      } else {
+        f[2 * j] = f16_bits_to_f32(static_cast<uint16_t>(w[j] & 0xffffu));
+        f[2 * j + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[j] >> 16));
+      }
+    }
+  }
+}
+template <int DT>
+__device__ __forceinline__ void store8(void* p, int64_t i, const float4& a, const float4& b) {
+  if constexpr (DT == kF32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = a;
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i + 4) = b;
+  } else {
+    const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == kBF16)
+        w[j] = static_cast<uint32_t>(f32_to_bf16_bits(f[2 * j])) | (static_cast<uint32_t>(f32_to_bf16_bits(f[2 * j + 1])) << 16);
+      else
+        w[j] = static_cast<uint32_t>(f32_to_f16_bits(f[2 * j])) | (static_cast<uint32_t>(f32_to_f16_bits(f[2 * j + 1])) << 16);
+    }
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <int DT, typename I>
+__global__ __launch_bounds__(kWireThreads) void wire_pack8_kernel(WireSeg s) {
+  const I per_row = static_cast<I>(s.len * s.dim / 8);
+  const I dim = static_cast<I>(s.dim);
+  const I n = static_cast<I>(s.rows / s.rep) * per_row;
+  for (I g = static_cast<I>(blockIdx.x) * kWireThreads + threadIdx.x; g < n;
+       g += static_cast<I>(gridDim.x) * kWireThreads) {
+    const I h = g / per_row;
+    const I c = g - h * per_row;
+    const I e = c * 8;
+    const I t = e / dim, d = e - t * dim;
+    float f[8];
+    load8<DT>(s.tensor, static_cast<int64_t>(h) * s.hs + static_cast<int64_t>(t) * s.ss + d, f);
+    const float4 a = make_float4(f[0], f[1], f[2], f[3]), b = make_float4(f[4], f[5], f[6], f[7]);
+    float4* w = reinterpret_cast<float4*>(s.wire) + (static_cast<int64_t>(h) * s.rep * per_row + c) * 2;
+    for (int64_t r = 0; r < s.rep; ++r) {
+      w[r * per_row * 2] = a;
+      w[r * per_row * 2 + 1] = b;
+    }
+  }
+}
+
+template <int DT, typename I>
+__global__ __launch_bounds__(kWireThreads) void wire_unpack8_kernel(WireSeg s) {
+  const I per_row = static_cast<I>(s.len * s.dim / 8);
+  const I dim = static_cast<I>(s.dim);
+  const I n = static_cast<I>(s.rows / s.rep) * per_row;
+  for (I g = static_cast<I>(blockIdx.x) * kWireThreads + threadIdx.x; g < n;
+       g += static_cast<I>(gridDim.x) * kWireThreads) {
+    const I h = g / per_row;
+    const I c = g - h * per_row;
+    const I e = c * 8;
+    const I t = e / dim, d = e - t * dim;
+    const float4* w = reinterpret_cast<const float4*>(s.wire) + (static_cast<int64_t>(h) * s.rep * per_row + c) * 2;
+    store8<DT>(s.tensor, static_cast<int64_t>(h) * s.hs + static_cast<int64_t>(t) * s.ss + d, w[0], w[1]);
+  }
+}
+
+template <typename I>
+void launch_seg8(bool pack, int dtype, const WireSeg& s, hipStream_t stream) {
+  const int64_t n = (s.rows / s.rep) * (s.len * s.dim / 8);
+  if (n <= 0) return;
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, kWireThreads), 8192));
+#define HCP_WIRE8_LAUNCH(DTV)                                                                     \
+  if (pack) wire_pack8_kernel<DTV, I><<<grid, kWireThreads, 0, stream>>>(s);                     \
+  else wire_unpack8_kernel<DTV, I><<<grid, kWireThreads, 0, stream>>>(s);
+  switch (dtype) {
+    case kF32: HCP_WIRE8_LAUNCH(kF32) break;
+    case kBF16: HCP_WIRE8_LAUNCH(kBF16) break;
+    case kF16: HCP_WIRE8_LAUNCH(kF16) break;
+    default: throw Error(-6, "wire: dtype must be F16, BF16 or F32");
+  }
+#undef HCP_WIRE8_LAUNCH
+  HCP_HIP(hipGetLastError());
+}
+
 template <int VEC>
 void launch_seg(bool pack, int dtype, const WireSeg& s, hipStream_t stream) {
   const int64_t rows = pack ? s.rows : s.rows / s.rep;
@@ -125,7 +226,13 @@ void launch_wire_segment(bool pack, int dtype, void* tensor, float* wire, int64_
                          int64_t dim, int64_t hs, int64_t ss, hipStream_t stream) {
   WireSeg s{tensor, wire, rows, rep, len, dim, hs, ss};
   require(rep >= 1 && rows % rep == 0, "wire: rows must be a multiple of the expand factor");
-  if (dim % 4 == 0) {
+  const int64_t es = dtype == kF32 ? 4 : 2;
+  const bool rows16 = dim % 8 == 0 && reinterpret_cast<uintptr_t>(tensor) % 16 == 0 && (hs * es) % 16 == 0 &&
+                      (ss * es) % 16 == 0 && reinterpret_cast<uintptr_t>(wire) % 16 == 0;
+  if (rows16) {
+    if (rows / rep * len * dim < (int64_t(1) << 31)) launch_seg8<uint32_t>(pack, dtype, s, stream);
+    else launch_seg8<int64_t>(pack, dtype, s, stream);
+  } else if (dim % 4 == 0) {
     require(reinterpret_cast<uintptr_t>(wire) % 16 == 0, "wire: payload must be 16-byte aligned");
     launch_seg<4>(pack, dtype, s, stream);
   } else {
