@@ -60,6 +60,10 @@ BLOCK_CASES = [
     ("d112_f16_noncausal", 150, 260, 4, 4, 112, 0, 0, False, torch.float16),
     ("d48_full_past", 130, 250, 4, 2, 48, 300, 0, True, torch.bfloat16),
     ("d8_diag", 70, 90, 2, 1, 8, 20, 0, True, torch.bfloat16),
+    # GQA ratios that are not powers of two: Qwen2-0.5B (14 q / 2 kv heads, D=64: one
+    # head per workgroup in the head-dim-64 kernel) and 6 at D=128 (two per workgroup)
+    ("qwen2_0p5b_rep7_d64", 150, 300, 14, 2, 64, 150, 0, True, torch.bfloat16),
+    ("gqa6_d128", 120, 260, 12, 2, 128, 140, 0, True, torch.bfloat16),
 ]
 
 
