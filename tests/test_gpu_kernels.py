@@ -344,10 +344,10 @@ def test_ring_replay_matches_tch_blockwise(gpu, case, schedule):
             assert np.abs(out - rb).max() <= OUT_TOL
 
 
-@pytest.mark.parametrize("schedule", ["auto", "per_step", "fused"])
-def test_ring_replay_paged_matches_unpaged(gpu, schedule):
+@pytest.mark.parametrize("schedule,d", [("auto", 128), ("per_step", 128), ("fused", 128), ("fused", 96)])
+def test_ring_replay_paged_matches_unpaged(gpu, schedule, d):
     chunks = [256, 96, 160]
-    s, hq, hkv, d, bs = sum(chunks), 8, 2, 128, 16
+    s, hq, hkv, bs = sum(chunks), 8, 2, 16
     (q, k, v), _ = draw(77, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
     nb = s // bs + 5
     table_np = I.permuted_block_table(78, nb)[: s // bs]
@@ -367,11 +367,11 @@ def test_ring_replay_paged_matches_unpaged(gpu, schedule):
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
-@pytest.mark.parametrize("hq,hkv", [(8, 2), (6, 2), (16, 2)])
-def test_ring_replay_fused_noncausal_wraps_round_the_ring(gpu, hq, hkv):
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (6, 2, 128), (16, 2, 128), (8, 2, 80)])
+def test_ring_replay_fused_noncausal_wraps_round_the_ring(gpu, hq, hkv, d):
     # Without causal masking every domain folds every source; after source 0 the ring
     # wraps to N-1, ..., t+1 (rows [off_t + len_t, S) read from the top down).
-    chunks, d = [200, 333, 150, 90], 128
+    chunks = [200, 333, 150, 90]
     s = sum(chunks)
     (q, k, v), (q32, k32, v32) = draw(57, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
     scale = 1 / math.sqrt(d)
