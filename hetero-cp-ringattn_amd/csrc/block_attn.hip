@@ -765,7 +765,9 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     u32x4 r;
     r[0] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(at));
     r[1] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(at >> 32) & 0xffffu);
-    r[2] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(ke - kr) * rb);
+    // the tile's own rows only: at most BK of them (below 2^31 bytes), however long the
+    // rest of the range, so the records never wrap and 0x80000000 stays out of range
+    r[2] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(min(ke - kr, BK)) * rb);
     r[3] = 0x00020000u;
     return r;
   };

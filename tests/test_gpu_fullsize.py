@@ -248,3 +248,31 @@ def test_llama3_8b_qkv_rope_sampled_tokens(gpu, tokens):
         assert torch.equal(q.view(torch.int16), q2.view(torch.int16))
         assert torch.equal(k.view(torch.int16), k2.view(torch.int16))
         assert torch.equal(v.view(torch.int16), v2.view(torch.int16))
+
+
+def test_block_partial_key_range_beyond_4gib(gpu):
+    """K/V views spanning more than 4 GiB (2.2M keys stored token-major, [L, Hkv, D]):
+    every DMA descriptor covers one tile's rows, so no byte count wraps at 2^32.  The
+    whole range in one block partial equals the LSE merge of its two halves."""
+    lk, hkv, d, hq, lq = 2_200_000, 8, 128, 32, 128
+    q = torch.empty(lq, hq, d, dtype=torch.bfloat16, device="cuda")
+    k = torch.empty(lk, hkv, d, dtype=torch.bfloat16, device="cuda")
+    v = torch.empty_like(k)
+    off = 0
+    for t in (q, k, v):
+        H.synth_normals(47, off, t.numel(), t)
+        off += t.numel()
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    assert kh.stride(1) * 2 * lk > 2 ** 32
+    o, l = H.block_partial(qh, kh, vh, lk, 0)          # queries after every key
+    half = lk // 2
+    o1, l1 = H.block_partial(qh, kh[:, :half], vh[:, :half], lk, 0)
+    o2, l2 = H.block_partial(qh, kh[:, half:], vh[:, half:], lk, half)
+    om, lm = H.lse_merge([o1, o2], [l1, l2], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert H.last_path() in ("mfma", "general")
+    o, l, om, lm = (x.cpu().numpy() for x in (o, l, om, lm))
+    assert np.abs(l - lm).max() <= 1e-4
+    # both sides round P to bf16 against different reference maxima: up to 2 x 2^-9
+    assert np.abs(o - om).max() <= 4e-3 * np.abs(om).max()
+    del k, v
