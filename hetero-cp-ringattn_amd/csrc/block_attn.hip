@@ -5,7 +5,8 @@
 // positioned partial / merge wrappers (ring.rs:538-603).  The online softmax is the
 // same recurrence; scores never leave registers.
 //
-// Matrix-core path (bf16 / fp16, head_dim 64 or 128), gfx950 MFMA 32x32x16:
+// Matrix-core path (bf16 / fp16, head_dim 64, or 128 and every other multiple of 8 below
+// it zero-padded to 128), gfx950 MFMA 32x32x16:
 //   * A workgroup is 8 waves.  Each wave owns 32 query tokens of ONE query head.
 //     The 8 waves cover G query heads that share a KV head (GQA, G in {1,2,4,8}) times
 //     8/G blocks of 32 tokens, so one K/V tile in LDS feeds 256 query rows and the

@@ -49,6 +49,8 @@ struct DecodeArgs {
   float* ws_lse;        // [splits][batch*hq]
   int32_t batch;
   int* err;
+  int32_t dn;           // head dim of the pool rows, q and the partials (the D=128 kernel:
+                        // any multiple of 8 up to 128, columns past it read as zeros)
 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -79,8 +81,10 @@ constexpr int kDecWaves = 4;  // most kv heads per workgroup (one per wave)
 // One wave per kv head.  Per 16-key group the wave needs the head's 16 K rows and 16 V
 // rows (4 KiB each for D=128); the next group's loads are issued before a group is
 // computed, and the block ids come from one table load per 64 groups.
-template <int D, int DT, int R>
+template <int D, int DT, int R, bool PAD>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
+  // PAD: head dim a.dn < D; the 16-byte columns past it are not loaded (zeros) nor stored
+  const int dn = PAD ? a.dn : D;
   constexpr int KS = D / 32;        // k-steps of 32 for the QK^T product
   constexpr int DCH = D / 8;        // 8-wide d chunks per row (16 for D=128)
   constexpr int TPL = 16 * DCH / 64;  // keys per lane in PV (4 for D=128)
@@ -113,7 +117,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     u32x4 v = {0, 0, 0, 0};
-    if (col < a.rep) v = *reinterpret_cast<const u32x4*>(a.q + b * a.q_bs + (kvh * a.rep + col) * a.q_hs + grp * 8 + 32 * s);
+    if (col < a.rep && (!PAD || grp * 8 + 32 * s < dn))
+      v = *reinterpret_cast<const u32x4*>(a.q + b * a.q_bs + (kvh * a.rep + col) * a.q_hs + grp * 8 + 32 * s);
     qf[s] = v;
   }
 
@@ -125,7 +130,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
   float m_run = -1.0e30f, l_run = 0.f;
 
-  const int64_t row_elems = static_cast<int64_t>(a.hkv) * D;  // one slot, all heads
+  const int64_t row_elems = static_cast<int64_t>(a.hkv) * dn;  // one slot, all heads
 
   struct Group {
     u32x4 k[KS];
@@ -160,14 +165,18 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
       return;
     }
     const int slot0 = static_cast<int>(G.tok0 - entry * a.bs);
-    const uint16_t* kslot = a.pool + (static_cast<int64_t>(blk) * a.bs + slot0) * row_elems + kvh * D;
+    const uint16_t* kslot = a.pool + (static_cast<int64_t>(blk) * a.bs + slot0) * row_elems + kvh * dn;
     const uint16_t* krow = kslot + col * row_elems + grp * 8;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) G.k[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow + 32 * s));
+    for (int s = 0; s < KS; ++s)
+      G.k[s] = !PAD || grp * 8 + 32 * s < dn ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow + 32 * s))
+                                             : u32x4{0, 0, 0, 0};
     const uint16_t* vrow = kslot + a.plane_elems + pv_dc * 8;
+    const bool v_in = !PAD || pv_dc * 8 < dn;
 #pragma unroll
     for (int j = 0; j < TPL; ++j)
-      G.v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow + (pv_tg * TPL + j) * row_elems));
+      G.v[j] = v_in ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow + (pv_tg * TPL + j) * row_elems))
+                    : u32x4{0, 0, 0, 0};
   };
   auto compute_group = [&](const Group& G) {
     if (!G.ok) return;
@@ -261,12 +270,12 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   float lc[R];
 #pragma unroll
   for (int c = 0; c < R; ++c) lc[c] = __shfl(l, c);
-  if (pv_tg == 0) {
+  if (pv_tg == 0 && (!PAD || pv_dc * 8 < dn)) {
 #pragma unroll
     for (int c = 0; c < R; ++c) {
       if (c >= a.rep) break;
       const float inv = lc[c] > 0.f ? 1.f / lc[c] : 0.f;
-      float* orow = a.ws_o + (ws_row_base + kvh * a.rep + c) * D + pv_dc * 8;
+      float* orow = a.ws_o + (ws_row_base + kvh * a.rep + c) * dn + pv_dc * 8;
       reinterpret_cast<float4*>(orow)[0] =
           make_float4(acc[c][0] * inv, acc[c][1] * inv, acc[c][2] * inv, acc[c][3] * inv);
       reinterpret_cast<float4*>(orow)[1] =
@@ -291,12 +300,12 @@ int decode_width(int rep) { return rep <= 4 ? 4 : rep <= 8 ? 8 : 16; }
 // Waves (kv heads) per workgroup.
 int decode_waves(int hkv) { return std::min(hkv, kDecWaves); }
 
-template <int D, int DT>
+template <int D, int DT, bool PAD = false>
 const void* decode_fn(int r) {
   switch (r) {
-    case 4: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 4>);
-    case 8: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 8>);
-    default: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 16>);
+    case 4: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 4, PAD>);
+    case 8: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 8, PAD>);
+    default: return reinterpret_cast<const void*>(&paged_decode_kernel<D, DT, 16, PAD>);
   }
 }
 
@@ -315,8 +324,8 @@ int decode_slots(int d, int dtype, int r, int waves) {
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int cus = 0, per_cu = 0;
-  const void* fn = dtype == kBF16 ? (d == 128 ? decode_fn<128, kBF16>(r) : decode_fn<64, kBF16>(r))
-                                  : (d == 128 ? decode_fn<128, kF16>(r) : decode_fn<64, kF16>(r));
+  const void* fn = dtype == kBF16 ? (d != 64 ? decode_fn<128, kBF16>(r) : decode_fn<64, kBF16>(r))
+                                  : (d != 64 ? decode_fn<128, kF16>(r) : decode_fn<64, kF16>(r));
   int slots = 768;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * waves, 0) == hipSuccess && cus > 0 &&
@@ -355,12 +364,12 @@ size_t decode_workspace_bytes(int dtype, int batch, int hq, int hkv, int d, int6
   return al(rows * d * sizeof(float)) + al(rows * sizeof(float));
 }
 
-template <int D, int DT>
+template <int D, int DT, bool PAD = false>
 static void launch_decode_kernel(int r, dim3 grid, int waves, const DecodeArgs& a, hipStream_t stream) {
   switch (r) {
-    case 4: paged_decode_kernel<D, DT, 4><<<grid, 64 * waves, 0, stream>>>(a); break;
-    case 8: paged_decode_kernel<D, DT, 8><<<grid, 64 * waves, 0, stream>>>(a); break;
-    default: paged_decode_kernel<D, DT, 16><<<grid, 64 * waves, 0, stream>>>(a); break;
+    case 4: paged_decode_kernel<D, DT, 4, PAD><<<grid, 64 * waves, 0, stream>>>(a); break;
+    case 8: paged_decode_kernel<D, DT, 8, PAD><<<grid, 64 * waves, 0, stream>>>(a); break;
+    default: paged_decode_kernel<D, DT, 16, PAD><<<grid, 64 * waves, 0, stream>>>(a); break;
   }
 }
 
@@ -371,7 +380,7 @@ void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const voi
                          float* lse, void* ws, size_t ws_bytes, int* err, hipStream_t stream) {
   require(hq % hkv == 0 && hq / hkv <= 16, "paged_decode: num_q_heads/num_kv_heads must be <= 16");
   require(bs % 16 == 0, "paged_decode: block_size must be a multiple of 16");
-  require(d == 64 || d == 128, "paged_decode: head_dim must be 64 or 128");
+  require(d > 0 && d <= 128 && d % 8 == 0, "paged_decode: head_dim must be a multiple of 8 up to 128");
   require(dtype == kBF16 || dtype == kF16, "paged_decode: dtype must be BF16 or F16");
   const DecodePlan p = plan_decode(batch, hq, hkv, d, dtype, t0, t1);
   require(ws_bytes >= decode_workspace_bytes(dtype, batch, hq, hkv, d, t0, t1), "paged_decode: workspace too small");
@@ -405,16 +414,21 @@ void launch_paged_decode(int dtype, int batch, int hq, int hkv, int d, const voi
   a.ws_lse = ws_lse;
   a.batch = batch;
   a.err = err;
+  a.dn = d;
   const int waves = decode_waves(hkv);
   const int r = decode_width(a.rep);
   const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(batch),
                   static_cast<unsigned>((hkv + waves - 1) / waves));
+  // head dim 64: its own kernel; other multiples of 8 up to 128: the D=128 kernel with
+  // the columns past d zero-padded
   if (dtype == kBF16) {
     if (d == 128) launch_decode_kernel<128, kBF16>(r, grid, waves, a, stream);
-    else launch_decode_kernel<64, kBF16>(r, grid, waves, a, stream);
+    else if (d == 64) launch_decode_kernel<64, kBF16>(r, grid, waves, a, stream);
+    else launch_decode_kernel<128, kBF16, true>(r, grid, waves, a, stream);
   } else {
     if (d == 128) launch_decode_kernel<128, kF16>(r, grid, waves, a, stream);
-    else launch_decode_kernel<64, kF16>(r, grid, waves, a, stream);
+    else if (d == 64) launch_decode_kernel<64, kF16>(r, grid, waves, a, stream);
+    else launch_decode_kernel<128, kF16, true>(r, grid, waves, a, stream);
   }
   HCP_HIP(hipGetLastError());
   // Merge the splits of every (sequence, head): rows = batch*hq, one token each.

@@ -268,7 +268,9 @@ int hcp_paged_kv_gather_batch(const hcp_paged_pool* pool, int32_t num_ranges,
  *     range is empty).
  * The chunk is split across workgroups; workspace holds the split partials
  * (hcp_paged_decode_workspace_size bytes, 256-byte aligned).
- * dtype BF16 or F16, head_dim 64 or 128, block_size a multiple of 16, and at most 16
+ * dtype BF16 or F16, head_dim a multiple of 8 up to 128 (64: its own kernel; others run
+ * the head-dim-128 kernel with the columns past head_dim zero-padded), block_size a
+ * multiple of 16, and at most 16
  * query heads per KV head (num_q_heads / num_kv_heads <= 16: the GQA groups of
  * repeat_decode_kv_heads, ring.rs:496-512, of the reference's models -- 7 for
  * Qwen2-0.5B, 8 for Qwen2.5-3B, 4 for Llama-3-8B).

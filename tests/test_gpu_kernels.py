@@ -241,6 +241,10 @@ DECODE_CASES = [
     ("qwen25_3b_rep8_d128", 4, 16, 2, 128, 16, 1000, 64, 1000, True),
     ("rep16_one_kv_head", 2, 16, 1, 128, 32, 500, 0, 500, False),
     ("rep12_three_kv_heads", 2, 36, 3, 64, 16, 333, 5, 333, False),
+    # head dims other than 64 and 128: the D=128 kernel with zero-padded columns
+    ("d96_padded", 3, 32, 8, 96, 16, 700, 30, 700, True),
+    ("d80_rep5", 2, 10, 2, 80, 32, 450, 0, 450, False),
+    ("d32_rep4", 2, 8, 2, 32, 16, 260, 0, 260, False),
 ]
 
 
@@ -437,6 +441,7 @@ DECODE_RING_CASES = [
     ("four_domains_ragged_zero", [160, 96, 64, 0], [1, 2, 3], 32, 8, 128, 16),
     ("qwen2_0p5b_rep7", [200, 120, 90], [3, 4], 14, 2, 64, 16),
     ("qwen25_3b_rep8", [256, 100], [2, 5, 1], 16, 2, 128, 16),
+    ("d96_padded", [200, 150], [3, 2], 16, 4, 96, 16),
 ]
 
 
