@@ -49,6 +49,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
+// s_waitcnt lgkmcnt(0): this wave's LDS reads have returned; vmcnt and expcnt left
+// unconstrained.
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 template <int V>
 struct IntC {
   static constexpr int value = V;

@@ -17,7 +17,12 @@
 //   * Weight and token tiles of 32 hidden values reach LDS through buffer_load ... lds
 //     (four buffers, three stages in flight, one barrier per stage); chunk p of tile row
 //     r holds global chunk p ^ ((r >> 2) & 3), which keeps the fragment reads free of
-//     bank conflicts.
+//     bank conflicts.  The loop is software-pipelined: a stage's DMA instructions are
+//     spread through the MFMAs of the stage three before it, the second K half's
+//     fragments are read while the first half's MFMAs run, and the next stage's barrier
+//     sits inside this stage's second half, so its first fragments arrive while the
+//     matrix core still has this stage's MFMAs queued (measured on the Llama-3-8B layer:
+//     +7.6% over one barrier and one DMA burst at each stage start).
 //   * Epilogue, in fp32: + bias, rotate (x1 cos - x2 sin, x1 sin + x2 cos) with cos/sin
 //     from the table row of the token's position, round once to the storage dtype and
 //     store 4 consecutive head dims (8 bytes) per lane: q into [Hq, L, D], k / v into
@@ -135,32 +140,34 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
     x_voff[j] = static_cast<uint32_t>(r * a.x_ss * 2) + (((lane & 3) ^ qswz(tr)) << 4);
   }
   const uint32_t lds0 = lds_offset(lds);
-  auto issue = [&](int st, int buf) __attribute__((always_inline)) {
+  // DMA instruction j (< kPerStage) of stage st into buffer buf: weight rows first.
+  auto issue_one = [&](int st, int buf, int j) __attribute__((always_inline)) {
     const uint32_t kb = static_cast<uint32_t>(st) * kQRow;
-    const uint32_t wbase = lds0 + buf * kStage + wave * (32 * kQRow);
-    const uint32_t xbase = lds0 + buf * kStage + kQOperandW + wave * ((TN / 8) * kQRow);
+    if (j < 2) {
+      dma16(srd_w, w_voff[j] + kb, lds0 + buf * kStage + wave * (32 * kQRow) + j * 1024);
+    } else {
+      dma16(srd_x, x_voff[j - 2] + kb, lds0 + buf * kStage + kQOperandW + wave * ((TN / 8) * kQRow) + (j - 2) * 1024);
+    }
+  };
+  auto issue = [&](int st, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(srd_w, w_voff[j] + kb, wbase + j * 1024);
-#pragma unroll
-    for (int j = 0; j < XJ; ++j) dma16(srd_x, x_voff[j] + kb, xbase + j * 1024);
+    for (int j = 0; j < kPerStage; ++j) issue_one(st, buf, j);
   };
 
   // ---- fragment read offsets (bytes within a stage buffer) ----
-  uint32_t w_rd[2][2], x_rd[TB][2];
+  // Rows 32 tb and D/2 i apart share the swizzle key ((r >> 2) & 3 is unchanged by a
+  // multiple of 16), so one offset per sub-step and operand serves every block.
+  uint32_t w_rd[2], x_rd[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const int c = 2 * s + lhalf;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = fbase + (D / 2) * i + lcol;
-      w_rd[i][s] = r * kQRow + ((c ^ qswz(r)) << 4);
-    }
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int r = (TN / 2) * wt + 32 * tb + lcol;
-      x_rd[tb][s] = kQOperandW + r * kQRow + ((c ^ qswz(r)) << 4);
-    }
+    const int rw = fbase + lcol;
+    w_rd[s] = rw * kQRow + ((c ^ qswz(rw)) << 4);
+    const int rx = (TN / 2) * wt + lcol;
+    x_rd[s] = kQOperandW + rx * kQRow + ((c ^ qswz(rx)) << 4);
   }
+  constexpr uint32_t kWStep = (D / 2) * kQRow, kXStep = 32 * kQRow;
+  static_assert((D / 2) % 16 == 0, "swizzle key shared across the weight blocks");
 
   f32x16 acc[2][TB];
 #pragma unroll
@@ -175,38 +182,88 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
   if (n_st > 1) issue(1, 1);
   if (n_st > 2) issue(2, 2);
 
-  auto compute = [&](auto bufc) __attribute__((always_inline)) {
-    constexpr int bf = decltype(bufc)::value;
-    const uint8_t* L = lds + bf * kStage;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      frag wfr[2], xfr[TB];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) wfr[i] = __builtin_bit_cast(frag, *reinterpret_cast<const u32x4*>(L + w_rd[i][s]));
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) xfr[tb] = __builtin_bit_cast(frag, *reinterpret_cast<const u32x4*>(L + x_rd[tb][s]));
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb) acc[i][tb] = Ops::mma(wfr[i], xfr[tb], acc[i][tb]);
-    }
-  };
-  auto step = [&](int st, auto bufc) __attribute__((always_inline)) {
-    constexpr int bf = decltype(bufc)::value;
-    // Stage st is resident once at most the stages issued after it are in flight.
-    const int after = min(2, n_st - 1 - st);
+  // Stage st resident for every wave: this wave's DMA of it done (at most the stages
+  // issued after it still in flight), this wave's reads of older stages done, then the
+  // barrier.
+  auto sync_stage = [&](int st) __attribute__((always_inline)) {
+    const int after = min(2, max(0, n_st - 1 - st));
     if (after >= 2) wait_vmcnt<2 * kPerStage>();
     else if (after == 1) wait_vmcnt<kPerStage>();
     else wait_vmcnt<0>();
-    __syncthreads();  // stage st visible; every wave is done with stage st - 1's buffer
-    if (st + 3 < n_st) issue(st + 3, (bf + 3) & 3);
-    compute(bufc);
+    wait_lgkmcnt0();
+    __syncthreads();
+  };
+  auto rd = [&](int bf, uint32_t off) __attribute__((always_inline)) {
+    return __builtin_bit_cast(frag, *reinterpret_cast<const u32x4*>(lds + bf * kStage + off));
+  };
+  // MFMA (flat index over the stage) after which the next stage's barrier sits: after the
+  // last DMA instruction and at least two token blocks into the second K half.
+  constexpr int kMidA = 3 * (kPerStage - 1) + 1 > 2 * TB + 3 ? 3 * (kPerStage - 1) + 1 : 2 * TB + 3;
+  constexpr int kMid = kMidA % 2 ? kMidA : kMidA + 1;
+  constexpr int kMidTb = (kMid - 2 * TB) / 2;  // last second-half token block before it
+  static_assert(kMid < 4 * TB, "barrier inside the stage");
+  static_assert(3 * (kPerStage - 1) + 1 < 4 * TB, "every DMA instruction issued inside the stage");
+
+  frag w0[2], x0[TB];  // first-half fragments of the current stage, read ahead
+  if (n_st > 0) {
+    sync_stage(0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) w0[i] = rd(0, w_rd[0] + i * kWStep);
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) x0[tb] = rd(0, x_rd[0] + tb * kXStep);
+  }
+  // compute(st, bufc): the MFMAs of stage st (buffer bufc).  The DMA of stage st + 3 (into
+  // buffer (bufc + 3) & 3, last read in stage st - 1, before this stage's barrier) is
+  // spread through them, one instruction after every third MFMA from the second, so the
+  // waves' address traffic does not queue at the stage start.
+  auto compute = [&](int st, auto bufc) __attribute__((always_inline)) {
+    constexpr int bf = decltype(bufc)::value;
+    constexpr int nb = (bf + 1) & 3;
+    const int pf = st + 3 < n_st ? st + 3 : -1;
+    auto dma_after = [&](int m) __attribute__((always_inline)) {
+      if (m % 3 == 1 && m / 3 < kPerStage && pf >= 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue_one(pf, (bf + 3) & 3, m / 3);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    frag w1[2], x1[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      if (tb == TB - 1) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) w1[i] = rd(bf, w_rd[1] + i * kWStep);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        acc[i][tb] = Ops::mma(w0[i], x0[tb], acc[i][tb]);
+        dma_after(2 * tb + i);
+      }
+      x1[tb] = rd(bf, x_rd[1] + tb * kXStep);
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int m = 2 * TB + 2 * tb + i;
+        acc[i][tb] = Ops::mma(w1[i], x1[tb], acc[i][tb]);
+        dma_after(m);
+        if (m == kMid) {  // after the last stage: an extra barrier and unused reads
+          sync_stage(st + 1);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) w0[j] = rd(nb, w_rd[0] + j * kWStep);
+#pragma unroll
+          for (int t = 0; t <= kMidTb; ++t) x0[t] = rd(nb, x_rd[0] + t * kXStep);
+        }
+      }
+      if (tb > kMidTb) x0[tb] = rd(nb, x_rd[0] + tb * kXStep);
+    }
   };
   for (int st = 0; st < n_st; st += kQBufs) {
-    step(st, IntC<0>{});
-    if (st + 1 < n_st) step(st + 1, IntC<1>{});
-    if (st + 2 < n_st) step(st + 2, IntC<2>{});
-    if (st + 3 < n_st) step(st + 3, IntC<3>{});
+    compute(st, IntC<0>{});
+    if (st + 1 < n_st) compute(st + 1, IntC<1>{});
+    if (st + 2 < n_st) compute(st + 2, IntC<2>{});
+    if (st + 3 < n_st) compute(st + 3, IntC<3>{});
   }
 
   // ---- epilogue ----
