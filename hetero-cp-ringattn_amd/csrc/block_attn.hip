@@ -207,8 +207,8 @@ __device__ __forceinline__ void store4(void* base, int dtype, int64_t off, float
   } else {
     u32x2 w;
     if (dtype == kBF16) {
-      w[0] = static_cast<uint32_t>(f32_to_bf16_bits(x0)) | (static_cast<uint32_t>(f32_to_bf16_bits(x1)) << 16);
-      w[1] = static_cast<uint32_t>(f32_to_bf16_bits(x2)) | (static_cast<uint32_t>(f32_to_bf16_bits(x3)) << 16);
+      w[0] = f32x2_to_bf16x2_bits(x0, x1);
+      w[1] = f32x2_to_bf16x2_bits(x2, x3);
     } else {
       w[0] = static_cast<uint32_t>(f32_to_f16_bits(x0)) | (static_cast<uint32_t>(f32_to_f16_bits(x1)) << 16);
       w[1] = static_cast<uint32_t>(f32_to_f16_bits(x2)) | (static_cast<uint32_t>(f32_to_f16_bits(x3)) << 16);

@@ -49,12 +49,18 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 bits (finite and inf inputs; NaN stays NaN).
+// Round-to-nearest-even fp32 -> bf16 bits through gfx950's v_cvt_pk_bf16_f32: the same
+// bits as (u + 0x7fff + ((u >> 16) & 1)) >> 16 for every non-NaN input and the quieted
+// (u >> 16) | 0x40 for NaNs (all 2^32 inputs compared on the device).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Two values in one instruction: lo in bits 0-15, hi in bits 16-31.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {

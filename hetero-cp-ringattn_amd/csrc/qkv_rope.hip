@@ -67,7 +67,7 @@ __device__ __forceinline__ uint32_t qswz(int r) { return static_cast<uint32_t>((
 
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  if constexpr (DT == kBF16) return static_cast<uint32_t>(f32_to_bf16_bits(a)) | (static_cast<uint32_t>(f32_to_bf16_bits(b)) << 16);
+  if constexpr (DT == kBF16) return f32x2_to_bf16x2_bits(a, b);
   else return static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16);
 }
 

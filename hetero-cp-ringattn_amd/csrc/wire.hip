@@ -140,7 +140,7 @@ __device__ __forceinline__ void store8(void* p, int64_t i, const float4& a, cons
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if constexpr (DT == kBF16)
-        w[j] = static_cast<uint32_t>(f32_to_bf16_bits(f[2 * j])) | (static_cast<uint32_t>(f32_to_bf16_bits(f[2 * j + 1])) << 16);
+        w[j] = f32x2_to_bf16x2_bits(f[2 * j], f[2 * j + 1]);
       else
         w[j] = static_cast<uint32_t>(f32_to_f16_bits(f[2 * j])) | (static_cast<uint32_t>(f32_to_f16_bits(f[2 * j + 1])) << 16);
     }

@@ -158,6 +158,35 @@ def test_lse_merge_matches_closed_form(gpu, h, l, n):
     assert np.abs(lse[fin] - ref_l[fin]).max() < 1e-5
 
 
+def test_bf16_output_rounding_is_round_to_nearest_even(gpu):
+    # A one-part merge is the identity (weight exp(0) / 1 = 1 exactly), so its bf16 output
+    # is the kernels' shared fp32 -> bf16 rounding of the input, checked bit for bit
+    # against round-to-nearest-even on the bits: ties (low half 0x8000) with even and odd
+    # kept mantissas, carries into the next binade, the largest finite values (to inf) and
+    # infinities.  Inputs are normal or infinite, so the result does not depend on the
+    # kernel's denormal mode; -0 is left out (0 + 1 * -0 is +0).
+    rng = np.random.default_rng(6)
+    h, l, d = 2, 256, 128
+    bits = rng.integers(0, 2**32, h * l * d, dtype=np.uint64).astype(np.uint32)
+    bits[1::3] = (bits[1::3] & 0xFFFF0000) | 0x8000
+    special = np.array([0x3F808000, 0x3F818000, 0x3F807FFF, 0x3F808001, 0x3FFF8000, 0x3FFFFFFF, 0x7F7FFFFF,
+                        0x7F7F8000, 0x7F7F7FFF, 0xFF7FFFFF, 0xFF7F8000, 0x7F800000, 0xFF800000, 0x00800000,
+                        0x80808000, 0x477FE000, 0x3F800000], dtype=np.uint32)
+    bits[: special.size] = special
+    expo = bits & 0x7F800000
+    bits[expo == 0] |= 0x00800000                                   # no zeros or denormals
+    bits[(expo == 0x7F800000) & ((bits & 0x007FFFFF) != 0)] &= 0xFF800000   # NaN -> inf
+    o = bits.view(np.float32).reshape(h, l, d)
+    lse = rng.standard_normal((h, l)).astype(np.float32)
+    out, _ = H.lse_merge([torch.from_numpy(o).cuda()], [torch.from_numpy(lse).cuda()], out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    got = out.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    u = bits.astype(np.uint64)
+    want = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, [(hex(int(bits[i])), hex(int(got[i])), hex(int(want[i]))) for i in bad[:5]]
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_paged_gather_scatter_bit_exact(gpu, dtype):
     nb, bs, hkv, d = 96, 16, 8, 128
@@ -809,6 +838,49 @@ def test_qkv_rope_project_paged_append_matches_views(gpu):
     torch.cuda.synchronize()
     assert H.fetch_device_errors() == 0
     assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
+def test_qkv_rope_bad_positions_and_block_ids_flag_and_skip(gpu):
+    # A position outside the table leaves that token's q / k unrotated and raises flag 4;
+    # a block id outside the pool leaves that block's tokens unwritten and raises flag 1.
+    # Every other row is bit-identical to a clean launch.  Hq*D = 896 puts the q / k
+    # boundary inside a 256-feature tile.
+    tokens, hidden, hq, hkv, d, bs_, rows = 100, 256, 14, 2, 64, 16, 512
+    x, ws, _ = _qkv_inputs(tokens, hidden, hq, hkv, d, torch.bfloat16, False, 320)
+    x, ws = x.cuda(), [w.cuda() for w in ws]
+    table = H.rope_table(d, rows, 10000.0)
+    pos = torch.arange(3, 3 + tokens, dtype=torch.int64, device="cuda")
+    H.fetch_device_errors()
+    q1, k1, v1 = H.qkv_rope_project(x, *ws, hq, hkv, d, positions=pos, table=table)
+    qn, kn, _ = H.qkv_rope_project(x, *ws, hq, hkv, d, positions=pos, table=table, rope=False)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    bad_tok = [5, 70]
+    bad = pos.clone()
+    bad[5], bad[70] = rows, -1
+    q2, k2, v2 = H.qkv_rope_project(x, *ws, hq, hkv, d, positions=bad, table=table)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 4
+    keep = [t for t in range(tokens) if t not in bad_tok]
+    assert torch.equal(q2[:, keep], q1[:, keep]) and torch.equal(k2[:, keep], k1[:, keep])
+    assert torch.equal(q2[:, bad_tok], qn[:, bad_tok]) and torch.equal(k2[:, bad_tok], kn[:, bad_tok])
+    assert torch.equal(v2, v1)
+
+    nb = 12
+    blocks = torch.from_numpy(I.permuted_block_table(321, nb)[:7].astype(np.int32)).cuda()
+    pool1 = torch.zeros(2, nb, bs_, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.qkv_rope_project_paged(x, *ws, hq, hkv, d, pool1, blocks, 0, 0, positions=pos, table=table)
+    bad_blocks = blocks.clone()
+    bad_blocks[2] = nb
+    pool2 = torch.zeros_like(pool1)
+    q3 = H.qkv_rope_project_paged(x, *ws, hq, hkv, d, pool2, bad_blocks, 0, 0, positions=pos, table=table)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 1
+    assert torch.equal(q3, q1)
+    lost = int(blocks[2])
+    assert not pool2[:, lost].any()
+    others = [b for b in range(nb) if b != lost]
+    assert torch.equal(pool2[:, others], pool1[:, others])
 
 
 @pytest.mark.parametrize("dtype,chunks,hq,hkv,d", [(torch.float32, [40, 24, 36], 4, 2, 64),
