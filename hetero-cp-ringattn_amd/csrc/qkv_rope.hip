@@ -25,8 +25,11 @@
 //     +7.6% over one barrier and one DMA burst at each stage start).
 //   * Epilogue, in fp32: + bias, rotate (x1 cos - x2 sin, x1 sin + x2 cos) with cos/sin
 //     from the table row of the token's position, round once to the storage dtype and
-//     store 4 consecutive head dims (8 bytes) per lane: q into [Hq, L, D], k / v into
-//     [Hkv, L, D] views or appended to the paged pool through the block table.
+//     store 8 consecutive head dims (16 bytes) per lane -- the two lanes holding halves
+//     of an 8-dim group swap them with v_permlane32_swap, half the store instructions of
+//     8-byte stores (+2.3% on the Llama-3-8B layer); 8-byte stores when a row start is
+//     not 16-byte aligned: q into [Hq, L, D], k / v into [Hkv, L, D] views or appended to
+//     the paged pool through the block table.
 #include <cmath>
 
 #include "kernels.hpp"
@@ -281,6 +284,11 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
   const bool rot = a.rope && ow < 2;
   const int head = of / D;
   const int dh = of % D;             // head dim of block 0 (block 1 is dh + D/2)
+  // 16-byte stores need every row start 16-byte aligned
+  const bool st16 = (ow == 0 || a.pool == nullptr)
+                        ? ((reinterpret_cast<uintptr_t>(a.out[ow]) | static_cast<uintptr_t>(a.out_hs[ow]) * 2 |
+                            static_cast<uintptr_t>(a.out_ss[ow]) * 2) % 16) == 0
+                        : reinterpret_cast<uintptr_t>(a.pool) % 16 == 0;
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) {
     const int t = tok0 + (TN / 2) * wt + 32 * tb + lcol;
@@ -328,23 +336,45 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv_rope_kernel(QkvArgs a) {
       }
       slot = sp - entry * a.bs;
     }
+    uint16_t* row;
+    if (ow == 0 || a.pool == nullptr) {
+      row = a.out[ow] + head * a.out_hs[ow] + static_cast<int64_t>(t) * a.out_ss[ow];
+    } else {
+      row = a.pool + (ow == 2 ? a.plane_elems : 0) + ((static_cast<int64_t>(blk) * a.bs + slot) * a.hkv + head) * D;
+    }
+    u32x2 pk[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d0 = dh + (D / 2) * i + 8 * g + 4 * lhalf;
-        u32x2 pk;
-        pk[0] = pack2<DT>(v[i][4 * g], v[i][4 * g + 1]);
-        pk[1] = pack2<DT>(v[i][4 * g + 2], v[i][4 * g + 3]);
-        uint16_t* dst;
-        if (ow == 0 || a.pool == nullptr) {
-          dst = a.out[ow] + head * a.out_hs[ow] + static_cast<int64_t>(t) * a.out_ss[ow] + d0;
-        } else {
-          dst = a.pool + (ow == 2 ? a.plane_elems : 0) +
-                ((static_cast<int64_t>(blk) * a.bs + slot) * a.hkv + head) * D + d0;
-        }
-        *reinterpret_cast<u32x2*>(dst) = pk;
+        pk[i][g][0] = pack2<DT>(v[i][4 * g], v[i][4 * g + 1]);
+        pk[i][g][1] = pack2<DT>(v[i][4 * g + 2], v[i][4 * g + 3]);
       }
+    if (st16) {
+      // lanes 0-31 hold dims +0..3 of each 8-dim group, lanes 32-63 dims +4..7: after the
+      // swap of groups (g, g + 1) lane lhalf = 0 holds all 8 dims of group g + 1 and
+      // lhalf = 1 those of group g
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; g += 2) {
+          u32x4 w;
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const auto r = __builtin_amdgcn_permlane32_swap(pk[i][g + 1][k], pk[i][g][k], false, false);
+            w[k] = r[0];
+            w[2 + k] = r[1];
+          }
+          const int gs = g + 1 - lhalf;
+          *reinterpret_cast<u32x4*>(row + dh + (D / 2) * i + 8 * gs) = w;
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<u32x2*>(row + dh + (D / 2) * i + 8 * g + 4 * lhalf) = pk[i][g];
+    }
   }
 }
 

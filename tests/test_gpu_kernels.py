@@ -840,6 +840,24 @@ def test_qkv_rope_project_paged_append_matches_views(gpu):
     assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
 
 
+def test_qkv_rope_8_byte_aligned_views_match_contiguous(gpu):
+    # Row starts that are 8- but not 16-byte aligned (row stride D + 4 elements, base offset
+    # 4 elements) take the 8-byte store path; the values are those of contiguous outputs.
+    tokens, hidden, hq, hkv, d = 200, 256, 8, 2, 128
+    x, ws, bs = _qkv_inputs(tokens, hidden, hq, hkv, d, torch.bfloat16, True, 330)
+    x, ws, bs = x.cuda(), [w.cuda() for w in ws], [b.cuda() for b in bs]
+    table = H.rope_table(d, 512, 10000.0)
+    pos = torch.arange(7, 7 + tokens, dtype=torch.int64, device="cuda")
+    q1, k1, v1 = H.qkv_rope_project(x, *ws, hq, hkv, d, positions=pos, table=table, bq=bs[0], bk=bs[1], bv=bs[2])
+    views = [torch.zeros(h, tokens, d + 4, dtype=torch.bfloat16, device="cuda")[:, :, 4:] for h in (hq, hkv, hkv)]
+    q2, k2, v2 = H.qkv_rope_project(x, *ws, hq, hkv, d, positions=pos, table=table, bq=bs[0], bk=bs[1], bv=bs[2],
+                                    q_out=views[0], k_out=views[1], v_out=views[2])
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    assert views[0].data_ptr() % 16 == 8
+    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
 def test_qkv_rope_bad_positions_and_block_ids_flag_and_skip(gpu):
     # A position outside the table leaves that token's q / k unrotated and raises flag 4;
     # a block id outside the pool leaves that block's tokens unwritten and raises flag 1.
