@@ -200,20 +200,25 @@ __device__ __forceinline__ RowLimits row_limits(const BlockArgs& a, int q_end, i
   return r;
 }
 
+// 4 fp32 values as 16-bit `dtype` (bf16 or f16), packed in element order.
+__device__ __forceinline__ u32x2 pack4(int dtype, float x0, float x1, float x2, float x3) {
+  u32x2 w;
+  if (dtype == kBF16) {
+    w[0] = f32x2_to_bf16x2_bits(x0, x1);
+    w[1] = f32x2_to_bf16x2_bits(x2, x3);
+  } else {
+    w[0] = static_cast<uint32_t>(f32_to_f16_bits(x0)) | (static_cast<uint32_t>(f32_to_f16_bits(x1)) << 16);
+    w[1] = static_cast<uint32_t>(f32_to_f16_bits(x2)) | (static_cast<uint32_t>(f32_to_f16_bits(x3)) << 16);
+  }
+  return w;
+}
+
 // Stores 4 consecutive fp32 values as `dtype` at element offset `off` of `base`.
 __device__ __forceinline__ void store4(void* base, int dtype, int64_t off, float x0, float x1, float x2, float x3) {
   if (dtype == kF32) {
     *reinterpret_cast<float4*>(static_cast<float*>(base) + off) = make_float4(x0, x1, x2, x3);
   } else {
-    u32x2 w;
-    if (dtype == kBF16) {
-      w[0] = f32x2_to_bf16x2_bits(x0, x1);
-      w[1] = f32x2_to_bf16x2_bits(x2, x3);
-    } else {
-      w[0] = static_cast<uint32_t>(f32_to_f16_bits(x0)) | (static_cast<uint32_t>(f32_to_f16_bits(x1)) << 16);
-      w[1] = static_cast<uint32_t>(f32_to_f16_bits(x2)) | (static_cast<uint32_t>(f32_to_f16_bits(x3)) << 16);
-    }
-    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + off) = w;
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + off) = pack4(dtype, x0, x1, x2, x3);
   }
 }
 
@@ -279,15 +284,43 @@ __device__ __forceinline__ void write_final_row(void* out, int dtype, int64_t of
   constexpr int DB = D / 32;
   const bool any = l_tot > 0.f;
   const float inv = any ? 1.f / l_tot : 0.f;
+  // 16-bit rows whose starts are 16-byte aligned across the wave: lanes l and l + 32 hold
+  // the two 4-wide halves of each 8-wide group, so swapping groups (j, j + 1) with
+  // v_permlane32_swap hands each lane one whole group, stored as 16 bytes (half the store
+  // instructions of 8-byte stores).  Lanes l and l + 32 share their row, so both are
+  // active or neither.
+  const bool st16 = dtype != kF32 && __all(((reinterpret_cast<uintptr_t>(out) + static_cast<uintptr_t>(off) * 2) & 15) == 0);
+  if (st16) {
 #pragma unroll
-  for (int b = 0; b < DB; ++b)
+    for (int b = 0; b < DB; ++b)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int dcol = 32 * b + 8 * j + 4 * lhalf;
-      if (dcol >= dn) continue;  // zero-padded columns
-      store4(out, dtype, off + dcol, inv * oacc[b][4 * j], inv * oacc[b][4 * j + 1], inv * oacc[b][4 * j + 2],
-             inv * oacc[b][4 * j + 3]);
-    }
+      for (int j = 0; j < 4; j += 2) {
+        if (32 * b + 8 * j >= dn) continue;  // zero-padded columns
+        const u32x2 lo = pack4(dtype, inv * oacc[b][4 * j], inv * oacc[b][4 * j + 1], inv * oacc[b][4 * j + 2],
+                               inv * oacc[b][4 * j + 3]);
+        const u32x2 hi = pack4(dtype, inv * oacc[b][4 * j + 4], inv * oacc[b][4 * j + 5], inv * oacc[b][4 * j + 6],
+                               inv * oacc[b][4 * j + 7]);
+        u32x4 w;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const auto r = __builtin_amdgcn_permlane32_swap(hi[k], lo[k], false, false);
+          w[k] = r[0];
+          w[2 + k] = r[1];
+        }
+        const int dcol = 32 * b + 8 * (j + 1 - lhalf);
+        if (dcol < dn) *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + off + dcol) = w;
+      }
+  } else {
+#pragma unroll
+    for (int b = 0; b < DB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int dcol = 32 * b + 8 * j + 4 * lhalf;
+        if (dcol >= dn) continue;  // zero-padded columns
+        store4(out, dtype, off + dcol, inv * oacc[b][4 * j], inv * oacc[b][4 * j + 1], inv * oacc[b][4 * j + 2],
+               inv * oacc[b][4 * j + 3]);
+      }
+  }
   if (lhalf == 0 && lse != nullptr) *lse = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
 }
 
