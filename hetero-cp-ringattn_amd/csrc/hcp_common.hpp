@@ -72,6 +72,18 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
   return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }
 
+// Global stores with the nt and sc1 cache-policy bits (streamed, written back at system
+// scope), for write streams nothing reads again in the same kernel.  Measured in
+// same-run A/Bs: KV staging scatter +3.5% and gather +2.7% over nt alone (c5; sc1 alone
+// +3%, sc0 alone +0.7%), wire-frame pack +13.5% and unpack +6.3% over plain stores, LSE
+// merge +3.2%.
+__device__ __forceinline__ void store16_nt_sc1(void* p, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off nt sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store8_nt_sc1(void* p, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off nt sc1" : : "v"(p), "v"(v) : "memory");
+}
+
 // Element load/store by dtype (used by the general kernels).
 template <int DT>
 __device__ __forceinline__ float load_elem(const void* p, int64_t i);

@@ -39,6 +39,14 @@ __device__ __forceinline__ void dma16(u32x4 srd, uint32_t voff, uint32_t lds_add
                : "v"(voff), "s"(srd), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory", "m0");
 }
+// The same load with the nt (streaming) cache-policy bit, for data each workgroup reads
+// once and no other workgroup reads again (the KV staging gather: +2.2% on c5).
+__device__ __forceinline__ void dma16_nt(u32x4 srd, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+               :
+               : "v"(voff), "s"(srd), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // s_waitcnt vmcnt(N) for N < 64 (vmcnt bits [3:0] and [15:14]); expcnt and lgkmcnt

@@ -110,8 +110,8 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(MergeArgs a) {
     if (active) {
       const int64_t base = h * a.out_hs + t * a.out_ss + c;
       if constexpr (OUT_DT == kF32) {
-        *reinterpret_cast<float4*>(static_cast<float*>(a.out) + base) =
-            make_float4(acc[k].x * inv, acc[k].y * inv, acc[k].z * inv, acc[k].w * inv);
+        store16_nt_sc1(static_cast<float*>(a.out) + base,
+                       __builtin_bit_cast(u32x4, make_float4(acc[k].x * inv, acc[k].y * inv, acc[k].z * inv, acc[k].w * inv)));
       } else {
         uint16_t b0, b1, b2, b3;
         if constexpr (OUT_DT == kBF16) {
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(MergeArgs a) {
         uint2 packed;
         packed.x = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
         packed.y = static_cast<uint32_t>(b2) | (static_cast<uint32_t>(b3) << 16);
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + base) = packed;
+        store8_nt_sc1(static_cast<uint16_t*>(a.out) + base, u32x2{packed.x, packed.y});
       }
     }
     if (a.lse_out != nullptr && lane_in_row == 0) {

@@ -48,14 +48,6 @@ struct PagedCopyArgs {
   int* err;
 };
 
-// 16-byte store with the nt and sc1 cache-policy bits (streamed, written back at system
-// scope).  On the write side of the LDS-path copies -- randomly placed 8 KiB pool
-// pieces for the scatter, head-major runs for the gather -- it measured +4% and +2.8%
-// over nt alone on c5 (sc1 alone +3%, sc0 alone +0.7%; load-side bits no change).
-__device__ __forceinline__ void store16_nt_sc1(void* p, u32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off nt sc1" : : "v"(p), "v"(v) : "memory");
-}
-
 // Each thread moves kU vectors of each plane per pass: all 2*kU loads are issued before
 // any store, so a 256-thread workgroup keeps 2*kU*256*sizeof(V) bytes in flight.
 // Range of entry bid of the concatenated ranges.
@@ -196,7 +188,7 @@ __global__ __launch_bounds__(256) void paged_gather_lds_kernel(PagedCopyArgs a, 
     const u32x4 srd = make_srd(a.pool + plane * a.plane_bytes + static_cast<int64_t>(blk) * blk_bytes +
                                    static_cast<int64_t>(part) * item_bytes, item_bytes);
     for (int i = wave; i < n_dma; i += 4)
-      dma16(srd, static_cast<uint32_t>((i << 10) + lane * 16), lds_offset(stage) + (i << 10));
+      dma16_nt(srd, static_cast<uint32_t>((i << 10) + lane * 16), lds_offset(stage) + (i << 10));
     wait_vmcnt<0>();
     __syncthreads();
     uint8_t* dst = plane ? R.v_buf : R.k_buf;

@@ -105,7 +105,8 @@ __global__ __launch_bounds__(kWireThreads) void wire_unpack_kernel(WireSeg s) {
 // in 32 bits when it fits.  Pack: four consecutive d of one storage row per thread (one
 // 8-byte load for 2-byte dtypes), stored to each of the row's rep expanded wire rows, so
 // every store instruction of a wave writes one contiguous 1 KiB run (eight d per thread,
-// two 16-byte stores 32 bytes apart per lane, measured 18% slower).  Unpack: eight d per
+// two 16-byte stores 32 bytes apart per lane, measured 18% slower), with the nt + sc1
+// cache policy (+13.5% over plain stores; nt alone was slower).  Unpack: eight d per
 // thread from the first wire row of each group, one 16-byte store (four d per thread
 // measured 7% slower).
 template <int DT>
@@ -144,7 +145,7 @@ __device__ __forceinline__ void store8(void* p, int64_t i, const float4& a, cons
       else
         w[j] = static_cast<uint32_t>(f32_to_f16_bits(f[2 * j])) | (static_cast<uint32_t>(f32_to_f16_bits(f[2 * j + 1])) << 16);
     }
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+    store16_nt_sc1(static_cast<uint16_t*>(p) + i, u32x4{w[0], w[1], w[2], w[3]});
   }
 }
 
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(kWireThreads) void wire_pack8_kernel(WireSeg s) {
       }
     }
     float4* w = reinterpret_cast<float4*>(s.wire) + static_cast<int64_t>(h) * s.rep * per_row + c;
-    for (int64_t r = 0; r < s.rep; ++r) w[r * per_row] = a;
+    for (int64_t r = 0; r < s.rep; ++r) store16_nt_sc1(w + r * per_row, __builtin_bit_cast(u32x4, a));
   }
 }
 
