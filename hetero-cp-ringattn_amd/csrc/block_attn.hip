@@ -288,7 +288,8 @@ __device__ __forceinline__ void write_final_row(void* out, int dtype, int64_t of
   // the two 4-wide halves of each 8-wide group, so swapping groups (j, j + 1) with
   // v_permlane32_swap hands each lane one whole group, stored as 16 bytes (half the store
   // instructions of 8-byte stores).  Lanes l and l + 32 share their row, so both are
-  // active or neither.
+  // active or neither.  The fused schedule's launcher admits only 16-byte aligned
+  // outputs; the 8-byte path below is the fallback for any other caller.
   const bool st16 = dtype != kF32 && __all(((reinterpret_cast<uintptr_t>(out) + static_cast<uintptr_t>(off) * 2) & 15) == 0);
   if (st16) {
 #pragma unroll

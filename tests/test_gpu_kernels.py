@@ -400,6 +400,29 @@ def test_ring_replay_paged_matches_unpaged(gpu, schedule, d):
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 96)])
+def test_ring_replay_8_byte_aligned_output_takes_the_per_step_schedule(gpu, dtype, d):
+    # The fused schedule stores final rows 16 bytes at a time and so takes only 16-byte
+    # aligned outputs: an output whose rows are 8- but not 16-byte aligned (row stride
+    # D + 4 elements, base offset 4) is refused there, and "auto" replays it per step.
+    chunks = [256, 96, 160]
+    s, hq, hkv = sum(chunks), 8, 2
+    (q, k, v), _ = draw(79, [(s, hq, d), (s, hkv, d), (s, hkv, d)], dtype)
+    args = (q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+    o1, l1 = H.ring_attention_replay(*args, schedule="fused")
+    buf = torch.zeros(hq, s, d + 4, dtype=dtype, device="cuda")
+    out = buf[:, :, 4:]
+    assert out.data_ptr() % 16 == 8
+    with pytest.raises(H.HcpRingError, match="16-byte"):
+        H.ring_attention_replay(*args, schedule="fused", out=out)
+    o2, l2 = H.ring_attention_replay(*args, schedule="auto", out=out)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    assert (o1.float() - o2.float()).abs().max().item() <= OUT_TOL
+    assert (l1 - l2).abs().max().item() <= LSE_TOL
+    assert not buf[:, :, :4].any()
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (6, 2, 128), (16, 2, 128), (8, 2, 80)])
 def test_ring_replay_fused_noncausal_wraps_round_the_ring(gpu, hq, hkv, d):
     # Without causal masking every domain folds every source; after source 0 the ring
