@@ -1,5 +1,5 @@
-"""Parity at the full BASELINE sizes (c3 32k ring prefill, c4 paged decode, c5 128k
-staging), through properties that do not need the whole closed form: sampled query rows
+"""Parity at the full benchmark sizes (c2 8k and c3 32k ring prefill, c4 paged decode,
+c5 128k staging and prefill), through properties that do not need the whole closed form: sampled query rows
 against the f64 closed form, order invariance between strategies, bit-exactness against
 an independent GPU gather (torch advanced indexing) and scatter/gather round trips.
 Inputs come from the device LCG generator with the bench's seeds."""
