@@ -337,6 +337,10 @@ RING_CASES = [
     ("d96_padded", [300, 200, 133], 8, 2, 96, torch.bfloat16, 58),
     ("d80_f16", [150, 260], 4, 4, 80, torch.float16, 59),
     ("d32_gqa4", [200, 100, 64], 8, 2, 32, torch.bfloat16, 60),
+    # the reference's own model shape (Qwen2-0.5B: 14 q / 2 kv heads, D=64, GQA 7) and a
+    # D=64 fp16 multi-head case, both on the head-dim-64 block kernel
+    ("qwen2_0p5b_d64", [320, 200, 136], 14, 2, 64, torch.bfloat16, 61),
+    ("mha_d64_f16", [257, 190], 6, 6, 64, torch.float16, 62),
 ]
 
 
