@@ -5,8 +5,8 @@
 // positioned partial / merge wrappers (ring.rs:538-603).  The online softmax is the
 // same recurrence; scores never leave registers.
 //
-// Matrix-core path (bf16 / fp16, head_dim 64, or 128 and every other multiple of 8 below
-// it zero-padded to 128), gfx950 MFMA 32x32x16:
+// Matrix-core path (bf16 / fp16, head_dim 128 and every other multiple of 8 below it
+// zero-padded to 128), gfx950 MFMA 32x32x16:
 //   * A workgroup is 8 waves.  Each wave owns 32 query tokens of ONE query head.
 //     The 8 waves cover G query heads that share a KV head (GQA, G in {1,2,4,8}) times
 //     8/G blocks of 32 tokens, so one K/V tile in LDS feeds 256 query rows and the
@@ -21,11 +21,8 @@
 //   * Online softmax in the log2 domain with the scale folded in; the running max is
 //     only moved (and O rescaled) when a row's max grows by more than 8 (2^8 bound on
 //     P), which keeps the result exact and skips most rescales.
-//   * head_dim 64: K/V tiles of 64 keys, double-buffered in LDS, register-staged
-//     global loads of tile t+1 in flight while tile t is computed, one barrier per
-//     tile.  head_dim 128 (flash_block_pingpong_kernel): tiles of 128 keys,
-//     asynchronous global->LDS loads and two wave groups that alternate MFMA and
-//     softmax phases.
+//   * flash_block_pingpong_kernel / flash_ring_kernel: tiles of 128 keys, asynchronous
+//     global->LDS loads and two wave groups that alternate MFMA and softmax phases.
 //   * Causal: tiles wholly in a wave's future are skipped, tiles wholly visible are
 //     unmasked, only tiles straddling the diagonal (or the kv tail) are masked.  The
 //     visible keys of a row are a prefix of the chunk: j <= q_off + i - k_off for
@@ -81,12 +78,8 @@ namespace {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kBK = 64;           // keys per tile
-constexpr int kKPad = 8;          // bf16 pad per K row in LDS
-constexpr int kVtStride = kBK + 8;  // bf16 per V^T row in LDS (144 B)
-constexpr float kRescaleThreshold = 8.0f;
 constexpr float kInitMax = -1.0e30f;
-constexpr float kGrowSum = 256.0f;  // 2^kRescaleThreshold: largest partial row sum kept without a max pass
+constexpr float kGrowSum = 256.0f;  // 2^8: largest partial row sum kept without a max pass
 
 // C-row r of a 32x32 S^T block holds key kperm(r) of that block:
 // r = j*8 + h*4 + i  ->  16*(j/2) + 8*h + 4*(j%2) + i.
@@ -325,247 +318,11 @@ __device__ __forceinline__ void write_final_row(void* out, int dtype, int64_t of
   if (lhalf == 0 && lse != nullptr) *lse = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
 }
 
-template <int D, int DT, int G, bool POS>
-__global__ __launch_bounds__(kThreads, 1) void flash_block_kernel(BlockArgs a) {
-  using Ops = MfmaOps<DT>;
-  using frag = typename Ops::frag;
-  constexpr int TB = kWaves / G;  // 32-token blocks per workgroup
-  constexpr int TQ = 32 * TB;     // query tokens per workgroup
-  constexpr int KS = D / 16;      // k-steps of the QK^T product
-  constexpr int DB = D / 32;      // 32-row blocks of O^T
-  constexpr int KROW = D + kKPad; // bf16 per K row in LDS
-  constexpr int KCH = D / 8;      // 16-byte chunks per K/V row
-  constexpr int K_LOADS = kBK * KCH / 256;    // per K-loader thread
-  constexpr int V_ITEMS = (kBK / 4) * KCH;    // (4-row group, chunk) items
-
-  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[2][kBK * KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[2][D * kVtStride];
-
-  const int nblk = gridDim.x;
-  const int logical = xcd_remap(blockIdx.x, nblk);
-  // Head-group-major: each XCD's contiguous share of logical tiles covers the query
-  // tiles of as few KV heads as possible, so its CUs stream the same K/V through that
-  // XCD's L2.  Within a head group, heavier (later, causal) query tiles come first.
-  const int hg = logical / a.n_qtiles;
-  const int qt = a.n_qtiles - 1 - logical % a.n_qtiles;
-
-  const int tid = threadIdx.x;
-  // Wave index as a scalar: everything derived from it stays in SGPRs.
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int lcol = lane & 31;   // query column owned by this lane
-  const int lhalf = lane >> 5;  // 0/1: which 8-wide k slice this lane feeds
-
-  const int head = hg * G + (wave % G);
-  const int kvh = (hg * G) / a.rep;
-  const int tq0 = qt * TQ;                       // first query token of the workgroup
-  const int wq0 = tq0 + (wave / G) * 32;         // first query token of this wave
-  const int my_q = wq0 + lcol;                   // this lane's query token
-  const int q_end = min(a.lq, tq0 + TQ);
-
-  // Keys visible to some row of this workgroup.
-  __shared__ int lim_red[kWaves];
-  const RowLimits rl = row_limits<POS>(a, q_end, wq0, my_q, wave, lane, lim_red);
-  const int n_kv = rl.n_kv;
-  const int n_tiles = (n_kv + kBK - 1) / kBK;
-
-  // Q^T fragments (B operand): Q[my_q][lhalf*8 + 16*s .. +8]; rows past lq read zeros.
-  frag qf[KS];
-  {
-    const uint16_t* qbase = a.q + head * a.q_hs + static_cast<int64_t>(wq0) * a.q_ss;
-    const auto qr = make_rsrc(qbase, static_cast<int64_t>(a.lq - wq0) * a.q_ss * 2);
-    const int32_t qoff = (lcol * static_cast<int32_t>(a.q_ss) + lhalf * 8) * 2;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = as_frag<frag>(buf_load16(qr, qoff + 32 * s));
-  }
-
-  f32x16 oacc[DB];
-#pragma unroll
-  for (int b = 0; b < DB; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
-  float m_run = kInitMax;  // reference max, log2 domain (scaled)
-  float l_run = 0.f;       // this lane's partial row sum
-
-  // ---- loader roles: waves 0-3 stage K, waves 4-7 stage V (transposed) ----
-  const bool k_loader = wave < 4;
-  const int lt = tid & 255;
-  const uint16_t* kbase = a.k + kvh * a.k_hs;
-  const uint16_t* vbase = a.v + kvh * a.v_hs;
-  // V item of this thread: 4 consecutive keys x one 8-wide d chunk.
-  const int v_rg = lt % (kBK / 4);
-  const int v_dc = lt / (kBK / 4);
-  const bool v_active = !k_loader && lt < V_ITEMS;
-  // Byte offsets within a tile (tile base = row kv0).
-  int32_t ld_off[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (k_loader) {
-      const int c = lt + 256 * (i < K_LOADS ? i : 0);
-      ld_off[i] = ((c / KCH) * static_cast<int32_t>(a.k_ss) + (c % KCH) * 8) * 2;
-    } else {
-      ld_off[i] = ((v_rg * 4 + i) * static_cast<int32_t>(a.v_ss) + v_dc * 8) * 2;
-    }
-  }
-  const uint16_t* ld_base = k_loader ? kbase : vbase;
-  const int64_t ld_ss = k_loader ? a.k_ss : a.v_ss;
-
-  u32x4 stage[4];
-  auto load_tile = [&](int t) {
-    const int kv0 = t * kBK;
-    const auto r = make_rsrc(ld_base + kv0 * ld_ss, static_cast<int64_t>(a.lk - kv0) * ld_ss * 2);
-    if (k_loader) {
-#pragma unroll
-      for (int i = 0; i < K_LOADS; ++i) stage[i] = buf_load16(r, ld_off[i]);
-    } else if (v_active) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) stage[i] = buf_load16(r, ld_off[i]);
-    }
-  };
-  auto store_tile = [&](int buf) {
-    if (k_loader) {
-#pragma unroll
-      for (int i = 0; i < K_LOADS; ++i) {
-        const int c = lt + 256 * i;
-        const int row = c / KCH, ch = c % KCH;
-        *reinterpret_cast<u32x4*>(&ks_lds[buf][row * KROW + ch * 8]) = stage[i];
-      }
-    } else if (v_active) {
-      // stage[i] holds d = v_dc*8 .. +8 of key v_rg*4+i; write V^T rows d, keys v_rg*4..+4.
-#pragma unroll
-      for (int dd = 0; dd < 8; ++dd) {
-        const int w = dd >> 1;
-        u32x2 pk;
-        if (dd & 1) {
-          pk[0] = __builtin_amdgcn_perm(stage[1][w], stage[0][w], 0x07060302u);
-          pk[1] = __builtin_amdgcn_perm(stage[3][w], stage[2][w], 0x07060302u);
-        } else {
-          pk[0] = __builtin_amdgcn_perm(stage[1][w], stage[0][w], 0x05040100u);
-          pk[1] = __builtin_amdgcn_perm(stage[3][w], stage[2][w], 0x05040100u);
-        }
-        *reinterpret_cast<u32x2*>(&vt_lds[buf][(v_dc * 8 + dd) * kVtStride + v_rg * 4]) = pk;
-      }
-    }
-  };
-
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  // Q fragments and tile 0 are resident before the loop: the prefetch issued inside
-  // the loop is then the only outstanding memory traffic during the MFMA section.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  const int krow0 = kperm(lcol);  // permuted K row fed by this lane (within a 32-block)
-  const float c = a.scale_log2;
-  // Causal limit of this lane relative to key 0 of the chunk: key j visible iff j <= qlim.
-  const int64_t qlim64 = rl.lane;
-  const int64_t wave_lim_first = rl.wave_first;
-  const int64_t wave_lim_last = rl.wave_last;
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < n_tiles) load_tile(t + 1);
-
-    const int kv0 = t * kBK;
-    // Skip tiles wholly in this wave's future (causal) -- other waves may need them.
-    const bool wave_live = !a.causal || kv0 <= wave_lim_last;
-    if (wave_live && wq0 < a.lq) {
-      const bool need_mask = (kv0 + kBK > a.lk) || (a.causal && kv0 + kBK - 1 > wave_lim_first);
-
-      // ---- S^T = K Q^T for two 32-key blocks ----
-      f32x16 sacc[2];
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[b][r] = 0.f;
-      const uint16_t* kl = &ks_lds[buf][0];
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          const u32x4 raw = *reinterpret_cast<const u32x4*>(kl + (32 * b + krow0) * KROW + lhalf * 8 + 16 * s);
-          sacc[b] = Ops::mma(as_frag<frag>(raw), qf[s], sacc[b]);
-        }
-      }
-
-      // ---- mask (boundary tiles only), tile row max on raw scores ----
-      if (need_mask) {
-        // key kv0 + kl visible iff kl <= lim (kl = tile-local key index).
-        int64_t lim64 = a.lk - 1 - kv0;
-        if (a.causal) lim64 = min(lim64, qlim64 - kv0);
-        const int lim = static_cast<int>(max(min(lim64, static_cast<int64_t>(kBK)), static_cast<int64_t>(-1))) - 8 * lhalf;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int j = r >> 2, i = r & 3;
-            const int kl0 = 32 * b + 16 * (j >> 1) + 4 * (j & 1) + i;  // kl minus 8*lhalf
-            sacc[b][r] = kl0 <= lim ? sacc[b][r] : -INFINITY;
-          }
-      }
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[b][r]);
-      tmax = max_xor32(tmax) * c;
-
-      // ---- lazy rescale: move the reference max only when it grows by > 8 ----
-      const bool grow = tmax > m_run + kRescaleThreshold;
-      if (__any(grow)) {
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = exp2f(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int b = 0; b < DB; ++b)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
-        m_run = m_new;
-      }
-
-      // ---- P = 2^(s*c - m) as 16-bit B operands, row-sum partial ----
-      frag pf[4];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        float p[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][r], c, -m_run));
-          l_run += p[r];
-        }
-        pf[2 * b] = Ops::pack(p);
-        pf[2 * b + 1] = Ops::pack(p + 8);
-      }
-
-      // ---- O^T += V^T P^T ----
-      const uint16_t* vl = &vt_lds[buf][0];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-#pragma unroll
-        for (int b = 0; b < DB; ++b) {
-          const u32x4 raw = *reinterpret_cast<const u32x4*>(vl + (32 * b + lcol) * kVtStride + 16 * s + 8 * lhalf);
-          oacc[b] = Ops::mma(as_frag<frag>(raw), pf[s], oacc[b]);
-        }
-      }
-    }
-
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: normalise, LSE (natural log), optional merge with running partial ----
-  if (my_q >= a.lq) return;
-  write_row<D>(a, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run));
-}
-
 // ----------------------------------------------------------------------------------
 // Head-dim-128 kernel: asynchronous global->LDS tiles, two wave groups in ping-pong.
 //
-// Same wave layout and math as flash_block_kernel (8 waves, one query head and 32
-// query tokens per wave, S^T = K Q^T with K rows in kperm order, P^T straight from the
-// S^T accumulators), with two changes:
+// 8 waves, one query head and 32 query tokens per wave, S^T = K Q^T with K rows in
+// kperm order, P^T straight from the S^T accumulators.
 //
 // Tiles.  The K and V tiles of 128 keys reach LDS without passing through registers:
 // buffer_load_dwordx4 ... lds writes 1 KiB per wave instruction (4 rows of 128
@@ -1319,32 +1076,12 @@ static void launch_pingpong(BlockGroup& grp, hipStream_t stream) {
   }
 }
 
-template <int D, int DT>
+template <int DT>
 static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
-  BlockArgs a = make_args(L);
-  if (D == kD3) {
-    BlockGroup grp;
-    grp.n = 1;
-    grp.a[0] = a;
-    launch_pingpong<DT>(grp, stream);
-    return;
-  }
-  const dim3 grid(static_cast<unsigned>(a.n_qtiles * a.n_groups));
-  if (a.q_lim != nullptr) {
-    switch (heads_per_group(a.rep)) {
-      case 8: flash_block_kernel<D, DT, 8, true><<<grid, kThreads, 0, stream>>>(a); break;
-      case 4: flash_block_kernel<D, DT, 4, true><<<grid, kThreads, 0, stream>>>(a); break;
-      case 2: flash_block_kernel<D, DT, 2, true><<<grid, kThreads, 0, stream>>>(a); break;
-      default: flash_block_kernel<D, DT, 1, true><<<grid, kThreads, 0, stream>>>(a); break;
-    }
-  } else {
-    switch (heads_per_group(a.rep)) {
-      case 8: flash_block_kernel<D, DT, 8, false><<<grid, kThreads, 0, stream>>>(a); break;
-      case 4: flash_block_kernel<D, DT, 4, false><<<grid, kThreads, 0, stream>>>(a); break;
-      case 2: flash_block_kernel<D, DT, 2, false><<<grid, kThreads, 0, stream>>>(a); break;
-      default: flash_block_kernel<D, DT, 1, false><<<grid, kThreads, 0, stream>>>(a); break;
-    }
-  }
+  BlockGroup grp;
+  grp.n = 1;
+  grp.a[0] = make_args(L);
+  launch_pingpong<DT>(grp, stream);
 }
 
 template <int DT>
@@ -1368,24 +1105,19 @@ static void launch_general(const BlockLaunch& L, hipStream_t stream) {
 }
 
 // Head dims the head-dim-128 kernel takes: up to 128 in 16-byte columns, zero-padded.
-static bool padded_d_ok(int d) { return d > 0 && d <= kD3 && d % 8 == 0 && d != 64; }
+// Head dim 64 goes this way too: at half the MFMA work wasted it measured 7-29% faster
+// (Llama-3-8B / Qwen2-0.5B heads, 32k ring) than a dedicated head-dim-64 kernel with
+// register-staged 64-key tiles.
+static bool padded_d_ok(int d) { return d > 0 && d <= kD3 && d % 8 == 0; }
 
-// True when the matrix-core kernels handle this shape (head dim 64: its own kernel;
-// other multiples of 8 up to 128: the head-dim-128 kernel with zero padding).
-bool block_uses_mfma(int dtype, int d) {
-  return (dtype == kBF16 || dtype == kF16) && (d == 64 || padded_d_ok(d));
-}
+// True when the matrix-core kernels handle this shape.
+bool block_uses_mfma(int dtype, int d) { return (dtype == kBF16 || dtype == kF16) && padded_d_ok(d); }
 
 void launch_block_partial(const BlockLaunch& L, hipStream_t stream) {
   if (L.lq == 0) return;
   if (!L.force_general && block_uses_mfma(L.dtype, L.d)) {
-    if (L.dtype == kBF16) {
-      if (L.d != 64) launch_mfma<128, kBF16>(L, stream);
-      else launch_mfma<64, kBF16>(L, stream);
-    } else {
-      if (L.d != 64) launch_mfma<128, kF16>(L, stream);
-      else launch_mfma<64, kF16>(L, stream);
-    }
+    if (L.dtype == kBF16) launch_mfma<kBF16>(L, stream);
+    else launch_mfma<kF16>(L, stream);
   } else {
     switch (L.dtype) {
       case kF32: launch_general<kF32>(L, stream); break;
@@ -1443,7 +1175,7 @@ bool ring_fused_applies(int dtype, int d) { return (dtype == kBF16 || dtype == k
 
 void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
   require(ring_fused_applies(L.dtype, L.d),
-          "fused ring: dtype must be BF16 or F16 with head_dim a multiple of 8 up to 128, not 64");
+          "fused ring: dtype must be BF16 or F16 with head_dim a multiple of 8 up to 128");
   check_tile_bytes(L.k_ss, L.v_ss);
   require(L.n >= 1 && L.n <= kMaxDomains, "fused ring: 1 to 64 domains");
   RingPlan p{};

@@ -364,7 +364,7 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
                         mfma_layout_ok(out) && (paged || (mfma_layout_ok(k) && mfma_layout_ok(v)));
   if (p.schedule == HCP_SCHEDULE_FUSED)
     require(fused_ok,
-            "the fused schedule needs BF16/F16, head_dim a multiple of 8 up to 128 (not 64) and 16-byte "
+            "the fused schedule needs BF16/F16, head_dim a multiple of 8 up to 128 and 16-byte "
             "aligned rows and strides");
   if (fused_ok && p.schedule != HCP_SCHEDULE_PER_STEP) {
     hcp_ring_view kk = k, vv = v;

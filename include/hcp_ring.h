@@ -122,8 +122,8 @@ int hcp_ring_fetch_device_errors(void* stream, int* flags);
  *                                        that sees no key.
  * With accumulate=1, o/lse hold a running partial on entry and are replaced by the
  * merge of it with this block (the rm=lse, rs=1, obh=o re-entry of ring.rs:585-587).
- * dtype: BF16 or F16 (matrix-core path: head_dim 64, or any multiple of 8 up to 128,
- * which runs the head-dim-128 kernel with the columns past head_dim zero-padded) or
+ * dtype: BF16 or F16 (matrix-core path: head_dim any multiple of 8 up to 128, run by
+ * the head-dim-128 kernel with the columns past head_dim zero-padded) or
  * F32 (any head_dim <= 256; F16/BF16 with other head dims take the same general
  * kernel).
  * ------------------------------------------------------------------------------- */
@@ -391,7 +391,7 @@ int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_po
  *                          running state in registers and writes the output rows (no
  *                          fp32 state in HBM).  Applies to VANILLA positions (or
  *                          causal = 0), BF16/F16, head_dim a multiple of 8 up to
- *                          128 other than 64, and q/k/v views with
+ *                          128, and q/k/v/out views with
  *                          16-byte aligned rows; -6 otherwise.  The paged form gathers
  *                          every chunk once, in one batched launch, then runs it;
  *   HCP_SCHEDULE_AUTO (0)  FUSED where it applies, else PER_STEP.

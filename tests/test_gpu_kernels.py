@@ -354,9 +354,9 @@ def test_ring_replay_matches_tch_blockwise(gpu, case, schedule):
     out, lse = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
                                        schedule=schedule)
     torch.cuda.synchronize()
-    # BF16/F16 at head dims up to 128 (multiples of 8, 64 aside) take the fused ring kernel
+    # BF16/F16 at head dims that are multiples of 8 up to 128 take the fused ring kernel
     # unless a per-step schedule is asked for
-    fused = dt != torch.float32 and d % 8 == 0 and d <= 128 and d != 64 and schedule == "auto"
+    fused = dt != torch.float32 and d % 8 == 0 and d <= 128 and schedule == "auto"
     assert H.last_path() == ("ring_fused" if fused else "general" if dt == torch.float32 else "mfma")
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
