@@ -415,23 +415,28 @@ void launch_rope_table(int d, int64_t rows, double base, float* cos, float* sin,
   HCP_HIP(hipGetLastError());
 }
 
-// Token tile TN in {128, 256, 384}: the one with the fewest rounds of workgroups over
-// the device's compute units, each round weighted by the time one tile of that size
-// takes relative to TN = 256 (0.62 and 1.57, measured on MI355X: bigger tiles reuse
-// each LDS fragment more, smaller ones fill the last round better).  Llama-3-8B at
-// 12288 tokens: 768 tiles of 384 are 3 rounds of 256 CUs, 1152 of 256 are 4.5.
+// Token tile TN in {128, 256, 384}: the one with the least modelled time, i.e. rounds
+// of workgroups over the device's compute units times the time one tile of that size
+// takes relative to TN = 256 (0.62 and 1.41: bigger tiles reuse each LDS fragment more),
+// a partly filled last round counted as 0.5 + 0.5 x its fill (it runs at a higher clock
+// with part of the chip idle).  Fitted to a sweep of the Llama-3-8B projection over
+// 1024-24576 tokens on MI355X, where it picks the fastest tile at every count (the
+// earlier model, 1.57 and whole rounds, missed 4096, 6144 and 24576 tokens by 7-12%).
+// Llama-3-8B at 12288 tokens: 768 tiles of 384 are 3 full rounds of 256 CUs.
 static int qkv_token_tile(int64_t tiles_f, int64_t tokens) {
   int dev = 0, cus = 0;
   HCP_HIP(hipGetDevice(&dev));
   HCP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   if (cus <= 0) return 256;
   const int tn[3] = {128, 256, 384};
-  const double cost[3] = {0.62, 1.0, 1.57};
+  const double cost[3] = {0.62, 1.0, 1.41};
   int best = 1;
   double best_t = 0.0;
   for (int i = 0; i < 3; ++i) {
-    const int64_t rounds = ceil_div(tiles_f * ceil_div(tokens, tn[i]), cus);
-    const double t = static_cast<double>(rounds) * cost[i];
+    const int64_t tiles = tiles_f * ceil_div(tokens, tn[i]);
+    const int64_t full = tiles / cus;
+    const double fill = static_cast<double>(tiles - full * cus) / cus;
+    const double t = (static_cast<double>(full) + (fill > 0.0 ? 0.5 + 0.5 * fill : 0.0)) * cost[i];
     if (i == 0 || t < best_t - 1e-9 || (i == 1 && t <= best_t + 1e-9)) {
       best = i;
       best_t = t;
