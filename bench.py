@@ -569,6 +569,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
+    ap.add_argument("--leg", choices=["c2"], default=None,
+                    help="run one extra leg alone and print its JSON object (profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three plain 1 GiB device copies (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -587,6 +589,9 @@ def main():
     H = load_pkg()
     torch.cuda.set_device(0)
     log(f"device {torch.cuda.get_device_name(0)}")
+    if args.leg == "c2":
+        print(json.dumps({"c2_prefill": bench_c2(H, torch, args.steps, args.warmup)}), flush=True)
+        return
     pre = bench_prefill(H, torch, args.steps, args.warmup)
     log(f"c3 prefill {pre['tflops']:.1f} TFLOP/s ({pre['ms_step']:.3f} ms/step, {pre['path']})")
     extra = {}

@@ -32,6 +32,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 # compile-time options); the default is the in-tree build.
 LIB_PATH = os.environ.get("HCP_RING_AMD_LIB") or os.path.join(HERE, "lib", "libhcp_ring_amd.so")
 HEADER = os.path.join(HERE, "..", "include", "hcp_ring.h")
+# HCP_RING_ABI_VERSION these bindings are written against; lib() refuses any other.
+ABI_VERSION = 3
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 1, 2, 3
 
@@ -266,6 +268,9 @@ def lib() -> ctypes.CDLL:
         fn = getattr(L, name)
         fn.argtypes = args
         fn.restype = res
+    got = L.hcp_ring_abi_version()
+    if got != ABI_VERSION:
+        raise HcpRingError(-5, f"{LIB_PATH} has ABI version {got}; these bindings need {ABI_VERSION}")
     _lib = L
     return L
 
@@ -350,8 +355,9 @@ def block_partial_positioned(q, q_positions, k, v, kv_positions, causal: bool = 
                              scale: float | None = None, o=None, lse=None, accumulate: bool = False,
                              workspace=None, stream=None):
     """As :func:`block_partial` with explicit global positions: q_positions [Lq] and
-    kv_positions [Lk] (device int64, keys non-decreasing); key j is visible to query i
-    iff kv_positions[j] <= q_positions[i] (ring.rs:249-273)."""
+    kv_positions [Lk] (device int64 tensors, each in any order); key j is visible to
+    query i iff kv_positions[j] <= q_positions[i] (ring.rs:249-273).  A key list that
+    is not non-decreasing is sorted on the device with its K / V rows (workspace)."""
     torch = _torch()
     hq, lq, d = q.shape
     hkv, lk, _ = k.shape

@@ -27,7 +27,8 @@
 //     unmasked, only tiles straddling the diagonal (or the kv tail) are masked.  The
 //     visible keys of a row are a prefix of the chunk: j <= q_off + i - k_off for
 //     contiguous positions, j < q_lim[i] for explicit positions (Striped / ZigZag,
-//     ring.rs:1024-1046, with non-decreasing key positions; see positions.hip).
+//     ring.rs:1024-1046, with non-decreasing key positions; a key list in any other
+//     order is read through sorted-row copies, see positions.hip).
 //
 // General path (fp32, or any head_dim <= 256): one thread per (query row, head), K/V
 // tiles staged in LDS as fp32.  Used for the fp32 CPU-smoke config.
@@ -60,6 +61,11 @@ struct BlockArgs {
   const int32_t* q_lim;    // positions mode when non-null (causal): row i sees keys [0, q_lim[i])
   int32_t d;               // head dim of the views and the state (the head-dim-128 kernel: <= 128,
                            // a multiple of 8; columns d .. 127 are zero padding in LDS and registers)
+  // positions mode, keys in any order: K / V come from the sorted-row copies when *kv_sel
+  const int32_t* kv_sel;
+  const uint16_t* k_alt;
+  const uint16_t* v_alt;
+  int64_t alt_hs, alt_ss;
 };
 
 // Up to kMaxGroup independent (query chunk, KV chunk) pairs with the same head layout in
@@ -467,6 +473,14 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     qt = ap->n_qtiles - 1 - (rem - plan.qt_begin[pi]);
     qv = ap->q; kv = ap->k; vv = ap->v;
     q_hs = ap->q_hs; q_ss = ap->q_ss; k_hs = ap->k_hs; k_ss = ap->k_ss; v_hs = ap->v_hs; v_ss = ap->v_ss;
+    if constexpr (POS) {
+      // a key list found out of order: its sorted-row copies (one scalar load per workgroup)
+      if (ap->kv_sel != nullptr && __builtin_amdgcn_readfirstlane(*ap->kv_sel) != 0) {
+        kv = ap->k_alt; vv = ap->v_alt;
+        k_hs = v_hs = ap->alt_hs;
+        k_ss = v_ss = ap->alt_ss;
+      }
+    }
     lq = ap->lq;
     rep = ap->rep;
     causal = ap->causal;
@@ -905,6 +919,10 @@ struct GenArgs {
   float* fin_lse;
   int64_t fin_lse_hs;
   const int32_t* q_lim;
+  const int32_t* kv_sel;   // as BlockArgs
+  const void* k_alt;
+  const void* v_alt;
+  int64_t alt_hs, alt_ss;
 };
 
 constexpr int kGenRows = 64;
@@ -917,6 +935,11 @@ __global__ __launch_bounds__(kGenRows) void general_block_kernel(GenArgs a) {
   const int head = blockIdx.y;
   const int kvh = head / a.rep;
   const int row = blockIdx.x * kGenRows + threadIdx.x;
+  if (a.q_lim != nullptr && a.kv_sel != nullptr && *a.kv_sel != 0) {
+    a.k = a.k_alt; a.v = a.v_alt;
+    a.k_hs = a.v_hs = a.alt_hs;
+    a.k_ss = a.v_ss = a.alt_ss;
+  }
   const bool live = row < a.lq;
   const int d = a.d;
   float qv[DMAX], acc[DMAX];
@@ -1039,6 +1062,11 @@ static BlockArgs make_args(const BlockLaunch& L) {
   a.fin_out = L.fin_out; a.fin_dtype = L.fin_dtype; a.fin_hs = L.fin_hs; a.fin_ss = L.fin_ss;
   a.fin_lse = L.fin_lse; a.fin_lse_hs = L.fin_lse_hs;
   a.q_lim = L.causal ? L.q_lim : nullptr;
+  a.kv_sel = L.kv_sel;
+  a.k_alt = static_cast<const uint16_t*>(L.k_alt);
+  a.v_alt = static_cast<const uint16_t*>(L.v_alt);
+  a.alt_hs = L.alt_hs;
+  a.alt_ss = L.alt_ss;
   a.d = static_cast<int32_t>(L.d);
   const int g = heads_per_group(a.rep);
   a.n_qtiles = static_cast<int32_t>(ceil_div(L.lq, 32 * (kWaves / g)));
@@ -1051,7 +1079,10 @@ static BlockArgs make_args(const BlockLaunch& L) {
 template <int DT>
 static void launch_pingpong(BlockGroup& grp, hipStream_t stream) {
   const BlockArgs& a0 = grp.a[0];
-  for (int i = 0; i < grp.n; ++i) check_tile_bytes(grp.a[i].k_ss, grp.a[i].v_ss);
+  for (int i = 0; i < grp.n; ++i) {
+    check_tile_bytes(grp.a[i].k_ss, grp.a[i].v_ss);
+    if (grp.a[i].kv_sel != nullptr) check_tile_bytes(grp.a[i].alt_ss, grp.a[i].alt_ss);
+  }
   grp.qt_begin[0] = 0;
   for (int i = 0; i < grp.n; ++i) grp.qt_begin[i + 1] = grp.qt_begin[i] + grp.a[i].n_qtiles;
   const dim3 grid(static_cast<unsigned>(grp.qt_begin[grp.n] * a0.n_groups));
@@ -1098,6 +1129,11 @@ static void launch_general(const BlockLaunch& L, hipStream_t stream) {
   a.fin_out = L.fin_out; a.fin_dtype = L.fin_dtype; a.fin_hs = L.fin_hs; a.fin_ss = L.fin_ss;
   a.fin_lse = L.fin_lse; a.fin_lse_hs = L.fin_lse_hs;
   a.q_lim = L.causal ? L.q_lim : nullptr;
+  a.kv_sel = L.kv_sel;
+  a.k_alt = L.k_alt;
+  a.v_alt = L.v_alt;
+  a.alt_hs = L.alt_hs;
+  a.alt_ss = L.alt_ss;
   const dim3 grid(static_cast<unsigned>(ceil_div(L.lq, kGenRows)), static_cast<unsigned>(L.hq));
   if (L.d <= 64) general_block_kernel<DT, 64><<<grid, kGenRows, 0, stream>>>(a);
   else if (L.d <= 128) general_block_kernel<DT, 128><<<grid, kGenRows, 0, stream>>>(a);

@@ -358,7 +358,7 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
     check_view(v, "v", p.seq);
   }
   // Fused schedule: one launch over every domain's ring (vanilla positions, BF16/F16,
-  // head_dim a multiple of 8 up to 128 other than 64, 16-byte rows); AUTO takes it
+  // head_dim a multiple of 8 up to 128, 16-byte rows); AUTO takes it
   // wherever it applies.
   const bool fused_ok = !p.positioned && ring_fused_applies(d->dtype, d->head_dim) && mfma_layout_ok(q) &&
                         mfma_layout_ok(out) && (paged || (mfma_layout_ok(k) && mfma_layout_ok(v)));
@@ -491,6 +491,39 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
   }
 }
 
+// Workspace of the positioned block entry: the per-row key limits, then (causal) the
+// key-order flag, the two (key, row) sort buffers and the sorted-row K / V copies.
+struct PositionedWorkspace {
+  size_t lim = 0, flag = 0, key[2] = {0, 0}, row[2] = {0, 0}, kc = 0, vc = 0, total = 0;
+};
+
+PositionedWorkspace positioned_workspace(const hcp_ring_block_desc* d) {
+  PositionedWorkspace w;
+  size_t cur = 0;
+  w.lim = cur;
+  cur += align256(static_cast<size_t>(d->q_len) * sizeof(int32_t));
+  if (d->causal == 1 && d->kv_len > 0) {
+    const size_t n = static_cast<size_t>(d->kv_len);
+    w.flag = cur;
+    cur += 256;
+    for (int i = 0; i < 2; ++i) {
+      w.key[i] = cur;
+      cur += align256(n * sizeof(int64_t));
+    }
+    for (int i = 0; i < 2; ++i) {
+      w.row[i] = cur;
+      cur += align256(n * sizeof(int32_t));
+    }
+    const size_t copy = align256(static_cast<size_t>(d->num_kv_heads) * n * d->head_dim * elem_size(d->dtype));
+    w.kc = cur;
+    cur += copy;
+    w.vc = cur;
+    cur += copy;
+  }
+  w.total = cur;
+  return w;
+}
+
 }  // namespace
 
 int block_transport_guard(const char* fn, const std::function<void()>& body) { return guarded(fn, body); }
@@ -548,8 +581,13 @@ int hcp_ring_block_partial(const hcp_ring_block_desc* desc, hcp_ring_view q, hcp
 }
 
 size_t hcp_ring_block_partial_positioned_workspace_size(const hcp_ring_block_desc* desc) {
-  if (desc == nullptr || desc->q_len < 0) return 0;
-  return align256(static_cast<size_t>(desc->q_len) * sizeof(int32_t));
+  if (desc == nullptr || desc->q_len < 0 || desc->kv_len < 0 || desc->num_kv_heads <= 0 || desc->head_dim <= 0)
+    return 0;
+  try {
+    return positioned_workspace(desc).total;
+  } catch (...) {
+    return 0;  // unsupported dtype: the entry point itself reports it
+  }
 }
 
 int hcp_ring_block_partial_positioned(const hcp_ring_block_desc* desc, hcp_ring_view q, const int64_t* q_positions,
@@ -564,21 +602,59 @@ int hcp_ring_block_partial_positioned(const hcp_ring_block_desc* desc, hcp_ring_
     require(o != nullptr && lse != nullptr, "null o or lse");
     BlockLaunch L = make_launch(desc, q, k, v, o, lse);
     if (desc->causal) {
-      const size_t need = hcp_ring_block_partial_positioned_workspace_size(desc);
+      const PositionedWorkspace w = positioned_workspace(desc);
       require(q_positions != nullptr, "null q_positions");
       require(kv_positions != nullptr || desc->kv_len == 0, "null kv_positions");
-      require(workspace != nullptr && workspace_bytes >= need,
-              "workspace too small: need " + std::to_string(need) + " bytes");
+      require(workspace != nullptr && workspace_bytes >= w.total,
+              "workspace too small: need " + std::to_string(w.total) + " bytes");
+      char* base = static_cast<char*>(workspace);
+      const hipStream_t st = as_stream(stream);
       KeyLimitArgs la{};
       la.q_pos = q_positions;
       la.n_q = desc->q_len;
       la.k_pos = kv_positions;
       la.k_off[0] = 0;
       la.k_len[0] = desc->kv_len;
-      la.lim = static_cast<int32_t*>(workspace);
+      la.lim = reinterpret_cast<int32_t*>(base + w.lim);
       la.lim_stride = 0;
-      la.err = device_error_flags();
-      launch_key_limits(la, 1, desc->kv_len, as_stream(stream));
+      la.err = nullptr;  // keys in any order are handled below
+      if (desc->kv_len > 0) {
+        // A key list that is not non-decreasing is sorted with its rows, and K / V are
+        // read through the sorted order (device-side decision: nothing happens for a
+        // list already in order).  Attention over a set of keys does not depend on
+        // their order (ring.rs:249-273 masks key by key).
+        int* flag = reinterpret_cast<int*>(base + w.flag);
+        int64_t* const keys[2] = {reinterpret_cast<int64_t*>(base + w.key[0]),
+                                  reinterpret_cast<int64_t*>(base + w.key[1])};
+        int32_t* const rows[2] = {reinterpret_cast<int32_t*>(base + w.row[0]),
+                                  reinterpret_cast<int32_t*>(base + w.row[1])};
+        launch_key_sort(kv_positions, desc->kv_len, flag, keys, rows, st);
+        const int f = key_sort_passes(desc->kv_len) % 2;
+        const int es = elem_size(desc->dtype);
+        KvSortedGather g{};
+        g.flag = flag;
+        g.rows = rows[f];
+        g.n = desc->kv_len;
+        g.hkv = desc->num_kv_heads;
+        g.row_bytes = static_cast<int64_t>(desc->head_dim) * es;
+        g.k = static_cast<const char*>(k.data);
+        g.v = static_cast<const char*>(v.data);
+        g.k_hs_bytes = k.head_stride * es;
+        g.k_ss_bytes = k.seq_stride * es;
+        g.v_hs_bytes = v.head_stride * es;
+        g.v_ss_bytes = v.seq_stride * es;
+        g.kc = base + w.kc;
+        g.vc = base + w.vc;
+        launch_kv_sorted_gather(g, st);
+        la.sel = flag;
+        la.k_pos_sorted = keys[f];
+        L.kv_sel = flag;
+        L.k_alt = g.kc;
+        L.v_alt = g.vc;
+        L.alt_hs = desc->kv_len * desc->head_dim;
+        L.alt_ss = desc->head_dim;
+      }
+      launch_key_limits(la, 1, desc->kv_len, st);
       L.q_lim = la.lim;
     }
     launch_block_partial(L, as_stream(stream));

@@ -33,6 +33,13 @@ struct BlockLaunch {
   // Positions mode (causal only, q_lim != nullptr): row i of the query chunk sees keys
   // [0, q_lim[i]) of the KV chunk instead of those with k_off + j <= q_off + i.
   const int32_t* q_lim = nullptr;
+  // Positions mode with keys in any order: when kv_sel is non-null and *kv_sel != 0 (a
+  // device flag), the kernels read K / V from the sorted-row copies k_alt / v_alt
+  // ([hkv, lk, d] contiguous, strides alt_hs / alt_ss) instead of k / v.
+  const int* kv_sel = nullptr;
+  const void* k_alt = nullptr;
+  const void* v_alt = nullptr;
+  int64_t alt_hs = 0, alt_ss = 0;
 };
 
 bool block_uses_mfma(int dtype, int d);
@@ -101,7 +108,9 @@ __host__ __device__ int64_t strategy_position(const StrategySpec& s, int d, int6
 void launch_domain_positions(const StrategySpec& s, int64_t seq, int64_t* out, hipStream_t stream);
 
 // lim[src * lim_stride + r] = #{j < k_len[src] : k_pos[k_off[src] + j] <= q_pos[r]} for
-// r < n_q; sets error bit 1 when a key list is not non-decreasing.
+// r < n_q, by binary search over a non-decreasing key list: k_pos, or k_pos_sorted when
+// sel is non-null and *sel != 0 (a list launch_key_sort found out of order).  With err
+// non-null, sets error bit 1 when the searched list is not non-decreasing.
 struct KeyLimitArgs {
   const int64_t* q_pos;
   int64_t n_q;
@@ -111,8 +120,33 @@ struct KeyLimitArgs {
   int32_t* lim;
   int64_t lim_stride;
   int* err;
+  const int* sel;
+  const int64_t* k_pos_sorted;
 };
 void launch_key_limits(const KeyLimitArgs& a, int n_src, int64_t max_k_len, hipStream_t stream);
+
+// Keys in any order (positions.hip): *flag = 1 iff k[0 .. n) is not non-decreasing;
+// then (and only then) the (key, row) pairs are sorted into key[f] / row[f] with
+// f = key_sort_passes(n) % 2 (key[1 - f] / row[1 - f] are scratch).  Stream-ordered,
+// no host synchronisation.
+int key_sort_passes(int64_t n);
+void launch_key_sort(const int64_t* k, int64_t n, int* flag, int64_t* const key[2], int32_t* const row[2],
+                     hipStream_t stream);
+// When *flag != 0: kc / vc [hkv, n, row_bytes] (contiguous) get row rows[r] of the K / V
+// views for every head (byte strides); nothing otherwise.
+struct KvSortedGather {
+  const int* flag;
+  const int32_t* rows;
+  int64_t n;
+  int32_t hkv;
+  int64_t row_bytes;
+  const char* k;
+  const char* v;
+  int64_t k_hs_bytes, k_ss_bytes, v_hs_bytes, v_ss_bytes;
+  char* kc;
+  char* vc;
+};
+void launch_kv_sorted_gather(const KvSortedGather& g, hipStream_t stream);
 
 // Wire frames (wire.hip): fp32 payload segments <-> strided storage views, the
 // serde_json-compatible headers and a reader for them.

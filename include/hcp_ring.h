@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define HCP_RING_ABI_VERSION 2
+#define HCP_RING_ABI_VERSION 3
 
 enum hcp_ring_status {
   HCP_RING_OK = 0,
@@ -99,7 +99,9 @@ int hcp_ring_last_path(void);
 /*
  * Reads and clears the sticky device-side error flags of the current device
  * (bit 0: a paged block id outside [0, num_blocks) was met and that row skipped;
- * bit 1: a list of key positions given to the positions mode was not non-decreasing;
+ * bit 1: a replay's generated key positions were not non-decreasing (an internal
+ *        consistency check; hcp_ring_block_partial_positioned takes keys in any order
+ *        and never sets it);
  * bit 2: a RoPE position outside the cos / sin table).
  * Synchronises `stream`.
  */
@@ -153,11 +155,16 @@ int hcp_ring_block_partial(const hcp_ring_block_desc* desc, hcp_ring_view q, hcp
  * As (1), with desc->q_offset / kv_offset ignored: query i has global position
  * q_positions[i], key j has kv_positions[j] (DEVICE int64 arrays, the reference's
  * Int64 position tensors), and with causal=1 a key is visible iff
- * kv_positions[j] <= q_positions[i].  kv_positions must be non-decreasing (as every
- * strategy's local order is, strategy.rs:114-121, and any slice of it); otherwise
- * device error bit 1 is set.  q_positions may be in any order.  The workspace
- * (hcp_ring_block_partial_positioned_workspace_size bytes) holds one int32 per query
- * row.  With causal=0 positions are not read.
+ * kv_positions[j] <= q_positions[i] (ring.rs:249-273, key by key).  Both lists may be
+ * in any order.  A key list that is not non-decreasing (the committed-KV slab appends
+ * positions in arrival order, self_driving.rs:180-224; the reference's own test passes
+ * [0, 4, 3, 5], ring.rs:2343) is sorted on the device together with its K / V rows
+ * into the workspace, and the fold reads them in that order; the decision is taken on
+ * the device, so a list already in order costs a few empty launches and no copy.  The
+ * workspace (hcp_ring_block_partial_positioned_workspace_size bytes) holds one int32 per
+ * query row and, with causal=1, the sort buffers (12 bytes per key, twice) and the
+ * sorted K / V copies (2 * num_kv_heads * kv_len * head_dim elements).  With causal=0
+ * positions are not read.
  * ------------------------------------------------------------------------------- */
 size_t hcp_ring_block_partial_positioned_workspace_size(const hcp_ring_block_desc* desc);
 

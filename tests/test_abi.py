@@ -20,7 +20,23 @@ def test_library_exports_every_header_function(hcp):
 
 
 def test_abi_version(hcp):
-    assert hcp.lib().hcp_ring_abi_version() == 2
+    import re
+    header = open(hcp.HEADER).read()
+    want = int(re.search(r"#define HCP_RING_ABI_VERSION (\d+)", header).group(1))
+    assert hcp.lib().hcp_ring_abi_version() == want == hcp.ABI_VERSION == 3
+
+
+def test_positioned_workspace_size_covers_the_key_sort(hcp):
+    # lim int32 per query row; with causal=1 the flag, two (int64 key, int32 row) sort
+    # buffers and the sorted K / V copies [Hkv, Lk, D] -- each region 256-byte aligned.
+    a = lambda x: (x + 255) // 256 * 256
+    d = hcp.BlockDesc(2, 16, 4, 128, 300, 1500, 0, 0, 1, 0, 0.1)
+    want = a(300 * 4) + 256 + 2 * a(1500 * 8) + 2 * a(1500 * 4) + 2 * a(4 * 1500 * 128 * 2)
+    assert hcp.lib().hcp_ring_block_partial_positioned_workspace_size(ctypes.byref(d)) == want
+    d.causal = 0
+    assert hcp.lib().hcp_ring_block_partial_positioned_workspace_size(ctypes.byref(d)) == a(300 * 4)
+    d.causal, d.dtype = 1, 99
+    assert hcp.lib().hcp_ring_block_partial_positioned_workspace_size(ctypes.byref(d)) == 0
 
 
 def test_null_descriptor_is_invalid(hcp):

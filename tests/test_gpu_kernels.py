@@ -55,13 +55,13 @@ BLOCK_CASES = [
     ("fp32_general_d64", 150, 150, 8, 8, 64, 0, 0, True, torch.float32),
     ("gqa2_long_noncausal", 160, 1000, 8, 4, 128, 0, 0, False, torch.bfloat16),
     ("gqa2_causal_long_past", 300, 1500, 4, 2, 128, 1200, 0, True, torch.bfloat16),
-    # head dims other than 64 and 128 run in the head-dim-128 kernel, zero-padded
+    # head dims below 128 run in the head-dim-128 kernel, zero-padded
     ("d96_padded_gqa4", 200, 300, 8, 2, 96, 0, 0, True, torch.bfloat16),
     ("d112_f16_noncausal", 150, 260, 4, 4, 112, 0, 0, False, torch.float16),
     ("d48_full_past", 130, 250, 4, 2, 48, 300, 0, True, torch.bfloat16),
     ("d8_diag", 70, 90, 2, 1, 8, 20, 0, True, torch.bfloat16),
     # GQA ratios that are not powers of two: Qwen2-0.5B (14 q / 2 kv heads, D=64: one
-    # head per workgroup in the head-dim-64 kernel) and 6 at D=128 (two per workgroup)
+    # head per workgroup) and 6 at D=128 (two per workgroup)
     ("qwen2_0p5b_rep7_d64", 150, 300, 14, 2, 64, 150, 0, True, torch.bfloat16),
     ("gqa6_d128", 120, 260, 12, 2, 128, 140, 0, True, torch.bfloat16),
 ]
@@ -338,7 +338,7 @@ RING_CASES = [
     ("d80_f16", [150, 260], 4, 4, 80, torch.float16, 59),
     ("d32_gqa4", [200, 100, 64], 8, 2, 32, torch.bfloat16, 60),
     # the reference's own model shape (Qwen2-0.5B: 14 q / 2 kv heads, D=64, GQA 7) and a
-    # D=64 fp16 multi-head case, both on the head-dim-64 block kernel
+    # D=64 fp16 multi-head case
     ("qwen2_0p5b_d64", [320, 200, 136], 14, 2, 64, torch.bfloat16, 61),
     ("mha_d64_f16", [257, 190], 6, 6, 64, torch.float16, 62),
 ]
@@ -586,6 +586,13 @@ POSITIONED_CASES = [
     ("gaps_unsorted_q_d128", 257, 333, 16, 2, 128, torch.bfloat16, "gaps"),
     ("striped_d64_f16", 200, 300, 4, 4, 64, torch.float16, "striped_rev"),
     ("gaps_fp32_general", 150, 190, 4, 2, 64, torch.float32, "gaps"),
+    # keys in any order (ring.rs:249-273 masks key by key; the committed-KV slab appends
+    # positions in arrival order, self_driving.rs:180-224): sorted on the device first
+    ("shuffled_gqa4_d128", 300, 1500, 16, 4, 128, torch.bfloat16, "shuffled"),        # one sort tile
+    ("shuffled_5k_merge_passes", 200, 5000, 8, 2, 128, torch.bfloat16, "shuffled"),  # 3 tiles, 2 merge passes
+    ("arrival_runs_9k", 256, 9000, 8, 1, 128, torch.bfloat16, "runs"),               # 5 tiles, 3 passes
+    ("shuffled_ties_d64_f16", 180, 1200, 4, 2, 64, torch.float16, "ties"),
+    ("shuffled_fp32_general", 150, 1100, 4, 2, 64, torch.float32, "shuffled"),
 ]
 
 
@@ -601,6 +608,14 @@ def _positions(pattern, lq, lk, seed):
         pos, _ = _strategy_rows([lq, 2 * lq, lq], "zigzag")
         return np.array(pos[0]), np.array(pos[0])
     qp = rng.choice(4 * (lq + lk), size=lq, replace=False)          # any order
+    if pattern == "shuffled":       # keys in any order
+        return qp, rng.choice(4 * (lq + lk), size=lk, replace=False)
+    if pattern == "ties":           # any order, many equal key positions
+        return qp, rng.integers(0, 2 * (lq + lk), size=lk)
+    if pattern == "runs":           # sorted runs concatenated in arrival order, overlapping ranges
+        cuts = np.sort(rng.choice(np.arange(1, lk), size=6, replace=False))
+        return qp, np.concatenate([np.sort(r) for r in np.split(rng.choice(4 * (lq + lk), size=lk,
+                                                                           replace=False), cuts)])
     kp = np.sort(rng.choice(4 * (lq + lk), size=lk, replace=False))  # non-decreasing
     return qp, kp
 
@@ -633,9 +648,69 @@ def test_block_partial_positioned_matches_closed_form(gpu, case):
     assert np.abs(o - to[0].numpy()).max() <= tol, name
 
 
+@pytest.mark.parametrize("dt,d", [(torch.float32, 4), (torch.bfloat16, 128)])
+def test_positioned_partial_committed_kv_positions(gpu, dt, d):
+    # The reference's own case (ring.rs:2247-2370, ring_forward_uses_independent_query_and_
+    # committed_kv_positions): queries at positions [3, 5] against committed keys at
+    # [0, 4, 3, 5] -- key 4 lies in query 3's future although it precedes key 3 in the
+    # list.  fp32 head dim 4 (the test's shape, general kernel) and bf16 head dim 128.
+    qp, kp = np.array([3, 5]), np.array([0, 4, 3, 5])
+    (q, k, v), (q32, k32, v32) = draw(2343 + d, [(2, 1, d), (4, 1, d), (4, 1, d)], dt)
+    scale = 1 / math.sqrt(d)
+    t = lambda a: torch.tensor(a, dtype=torch.int64, device="cuda")
+    o, lse = H.positioned_local_compact_partial(q.permute(1, 0, 2), t(qp), k.permute(1, 0, 2), v.permute(1, 0, 2),
+                                                t(kp))
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, qp, kp, scale)
+    tol_o, tol_l = (1e-5, 1e-5) if dt == torch.float32 else (OUT_TOL, LSE_TOL)
+    assert np.abs(o.cpu().numpy() - ref_o.transpose(1, 0, 2)).max() <= tol_o
+    assert np.abs(lse.cpu().numpy() - ref_l.T).max() <= tol_l
+    # a prefix reading of the list (keys [0, 4, 3] for query 3) differs from the answer
+    wrong_o, _ = C.attention_f64(q32[:1], k32[:3], v32[:3], qp[:1], np.array([0, 3, 3]), scale)
+    assert np.abs(wrong_o[0] - ref_o[0]).max() > 10 * tol_o
+    to, tl = T.positioned_local_compact_partial(scale, bhsd(q32), torch.from_numpy(qp), bhsd(k32), bhsd(v32),
+                                                torch.from_numpy(kp))
+    assert np.abs(o.cpu().numpy() - to[0].numpy()).max() <= tol_o
+    assert np.abs(lse.cpu().numpy() - tl[0].numpy()).max() <= tol_l
+
+
+def test_positioned_merge_keys_in_any_order(gpu):
+    # positioned_merge_compact_partial (ring.rs:574-603) with shuffled keys on both
+    # sides: local partial over one half of a shuffled 2000-key list, merged with the
+    # other half, equals attention over the whole list (GQA 4, D=128, bf16).
+    lq, lk, hq, hkv, d = 260, 2000, 16, 4, 128
+    rng = np.random.default_rng(7)
+    qp = rng.choice(3 * lk, size=lq, replace=False)
+    kp = rng.choice(3 * lk, size=lk, replace=False)
+    (q, k, v), (q32, k32, v32) = draw(2024, [(lq, hq, d), (lk, hkv, d), (lk, hkv, d)], torch.bfloat16)
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    t = lambda a: torch.tensor(a, dtype=torch.int64, device="cuda")
+    h = 1100
+    o, l = H.positioned_local_compact_partial(qh, t(qp), kh[:, :h], vh[:, :h], t(kp[:h]))
+    o, l = H.positioned_merge_compact_partial(qh, t(qp), o, l, kh[:, h:], vh[:, h:], t(kp[h:]))
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    scale = 1 / math.sqrt(d)
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, qp, kp, scale)
+    fin = np.isfinite(ref_l.T)
+    o, l = o.cpu().numpy(), l.cpu().numpy()
+    assert np.array_equal(np.isneginf(l), ~fin)
+    assert np.abs(o - ref_o.transpose(1, 0, 2)).max() <= OUT_TOL
+    assert np.abs(l[fin] - ref_l.T[fin]).max() <= LSE_TOL
+    # the restatement's merge re-entry on the same halves (state in fp32 upcasts)
+    ex = lambda a: T.repeat_kv_heads(bhsd(a), hq // hkv)
+    tq, tqp = bhsd(q32), torch.from_numpy(qp)
+    to, tl = T.positioned_local_compact_partial(scale, tq, tqp, ex(k32[:h]), ex(v32[:h]), torch.from_numpy(kp[:h]))
+    to, tl = T.positioned_merge_compact_partial(scale, tq, tqp, to, tl, ex(k32[h:]), ex(v32[h:]),
+                                                torch.from_numpy(kp[h:]))
+    assert np.abs(o - to[0].numpy()).max() <= OUT_TOL
+
+
 def test_block_partial_positioned_merge_and_flag(gpu):
     # positioned_merge_compact_partial with positions (ring.rs:574-603): a striped
-    # target merged with two sources; then a non-monotone key list raises flag bit 1.
+    # target merged with two sources; then the same source with its key list reversed
+    # gives the same partial and raises no flag (keys in any order are sorted first).
     pos, _ = _strategy_rows([160, 96, 64], "striped")
     (q, k, v), (q32, k32, v32) = draw(91, [(320, 8, 128), (320, 2, 128), (320, 2, 128)], torch.bfloat16)
     qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
@@ -650,9 +725,15 @@ def test_block_partial_positioned_merge_and_flag(gpu):
     assert np.abs(o.cpu().numpy() - ref_o.transpose(1, 0, 2)).max() <= OUT_TOL
     assert np.abs(l.cpu().numpy() - ref_l.T).max() <= LSE_TOL
     assert H.fetch_device_errors() == 0
-    bad = t(pos[1][::-1].copy())
-    H.positioned_local_compact_partial(qh[:, :160], t(pos[0]), kh[:, 160:256], vh[:, 160:256], bad)
-    assert H.fetch_device_errors() & 2
+    o1, l1 = H.positioned_local_compact_partial(qh[:, :160], t(pos[0]), kh[:, 160:256], vh[:, 160:256], t(pos[1]))
+    rev = t(pos[1][::-1].copy())
+    o2, l2 = H.positioned_local_compact_partial(qh[:, :160], t(pos[0]), kh[:, 160:256].flip(1),
+                                                vh[:, 160:256].flip(1).contiguous(), rev)
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    assert torch.equal(torch.isneginf(l1), torch.isneginf(l2))
+    fin = torch.isfinite(l1)
+    assert (o1 - o2).abs().max().item() <= 1e-5 and (l1[fin] - l2[fin]).abs().max().item() <= 1e-5
 
 
 STRATEGY_RING_CASES = [
