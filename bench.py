@@ -155,6 +155,53 @@ def bench_prefill(H, torch, steps: int, warmup: int, c=None, schedule: str = "au
                 alg_bytes_per_launch=blk_bytes * steps // blk_n, tensors=tensors, out=out, lse=lse)
 
 
+def trace_summary(H, torch, c, tensors, launches: int):
+    """Traced fused launches of a prefill config (hcp_ring_trace_attach): per launch the
+    library's statistics, and over all launches a least-squares fit of workgroup
+    duration against the 128-key tiles it folds (intercept = the fixed cost of a work
+    item, slope = the cost of one tile), plus the shader clock from s_memtime."""
+    import numpy as np
+
+    q, k, v = tensors
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    n = len(c["chunks"])
+    need = H.trace_record_bytes(torch.bfloat16, c["hq"], c["hkv"], c["d"], c["chunks"])
+    buf = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    stride = 16 + 2 * n
+    durs, tiles, clocks, per_launch = [], [], [], []
+    H.trace_attach(buf)
+    try:
+        for _ in range(launches):
+            H.ring_attention_replay(qh, kh, vh, c["chunks"])
+            doms, launch = H.trace_read()
+            per_launch.append(launch)
+            rec = buf.view(torch.int32).cpu().numpy().view(np.uint32).reshape(-1, stride).astype(np.uint64)
+            t0 = rec[:, 0] | (rec[:, 1] << 32)
+            t1 = rec[:, 2] | (rec[:, 3] << 32)
+            c0 = rec[:, 4] | (rec[:, 5] << 32)
+            c1 = rec[:, 6] | (rec[:, 7] << 32)
+            durs.append((t1 - t0).astype(np.float64) / 100.0)  # us (100 MHz ticks)
+            tiles.append(rec[:, 12].astype(np.float64))
+            clocks.append(100.0 * (c1 - c0).astype(np.float64) / (t1 - t0).astype(np.float64))
+    finally:
+        H.trace_attach(None)
+    dur, til, clk = np.concatenate(durs), np.concatenate(tiles), np.concatenate(clocks)
+    slope, icpt = np.polyfit(til, dur, 1)
+    resid = dur - (icpt + slope * til)
+    keys = ["span_ms", "busy_cu_ms", "idle_gap_cu_ms", "tail_cu_ms", "head_cu_ms", "clock_mhz", "wg_ms_mean"]
+    mean = {k: round(float(np.mean([x[k] for x in per_launch])), 4) for k in keys}
+    return {"launches": launches, "workgroups": int(per_launch[0]["workgroups"]), "cus": int(per_launch[0]["cus"]),
+            "mean_per_launch": mean,
+            "span_ms_per_launch": [round(x["span_ms"], 4) for x in per_launch],
+            "fit_us": {"per_item": round(float(icpt), 2), "per_key_tile": round(float(slope), 3),
+                       "resid_rms": round(float(np.sqrt(np.mean(resid ** 2))), 2)},
+            "wg_us": {"min": round(float(dur.min()), 1), "mean": round(float(dur.mean()), 1),
+                      "max": round(float(dur.max()), 1)},
+            "key_tiles_per_wg": {"min": int(til.min()), "mean": round(float(til.mean()), 2), "max": int(til.max())},
+            "clock_mhz": {"p10": round(float(np.percentile(clk, 10)), 1), "median": round(float(np.median(clk)), 1),
+                          "p90": round(float(np.percentile(clk, 90)), 1)}}
+
+
 def prefill_summary(r):
     """JSON object of a prefill leg (TFLOP/s of the whole step, and of the block kernel
     from its own launch times)."""
@@ -569,8 +616,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
-    ap.add_argument("--leg", choices=["c2"], default=None,
-                    help="run one extra leg alone and print its JSON object (profiling)")
+    ap.add_argument("--leg", choices=["c2", "c3"], default=None,
+                    help="run one prefill leg alone and print its JSON object (profiling)")
+    ap.add_argument("--trace", action="store_true",
+                    help="with --leg: also run traced launches (per-workgroup records) and summarise them")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three plain 1 GiB device copies (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -589,8 +638,13 @@ def main():
     H = load_pkg()
     torch.cuda.set_device(0)
     log(f"device {torch.cuda.get_device_name(0)}")
-    if args.leg == "c2":
-        print(json.dumps({"c2_prefill": bench_c2(H, torch, args.steps, args.warmup)}), flush=True)
+    if args.leg is not None:
+        c = C2 if args.leg == "c2" else C3
+        r = bench_prefill(H, torch, args.steps, args.warmup, c)
+        out = {"leg": args.leg, **prefill_summary(r)}
+        if args.trace:
+            out["trace"] = trace_summary(H, torch, c, r["tensors"], launches=args.steps)
+        print(json.dumps(out), flush=True)
         return
     pre = bench_prefill(H, torch, args.steps, args.warmup)
     log(f"c3 prefill {pre['tflops']:.1f} TFLOP/s ({pre['ms_step']:.3f} ms/step, {pre['path']})")

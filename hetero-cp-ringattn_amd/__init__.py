@@ -99,6 +99,21 @@ class ReplayDesc(ctypes.Structure):
                 ("strategy", ctypes.c_int32), ("schedule", ctypes.c_int32)]
 
 
+class TraceDomain(ctypes.Structure):
+    _fields_ = [("domain", ctypes.c_int32), ("workgroups", ctypes.c_int32), ("key_tiles", ctypes.c_int64),
+                ("peer_chunks", ctypes.c_int64), ("kv_recv_bytes", ctypes.c_int64), ("kv_sent_bytes", ctypes.c_int64),
+                ("span_ms", ctypes.c_double), ("local_cu_ms", ctypes.c_double), ("peer_cu_ms", ctypes.c_double),
+                ("local_compute_ms", ctypes.c_double), ("peer_compute_ms", ctypes.c_double),
+                ("clock_mhz", ctypes.c_double)]
+
+
+class TraceLaunch(ctypes.Structure):
+    _fields_ = [("workgroups", ctypes.c_int64), ("cus", ctypes.c_int32), ("reserved0", ctypes.c_int32),
+                ("span_ms", ctypes.c_double), ("busy_cu_ms", ctypes.c_double), ("idle_gap_cu_ms", ctypes.c_double),
+                ("tail_cu_ms", ctypes.c_double), ("head_cu_ms", ctypes.c_double), ("clock_mhz", ctypes.c_double),
+                ("wg_ms_min", ctypes.c_double), ("wg_ms_mean", ctypes.c_double), ("wg_ms_max", ctypes.c_double)]
+
+
 BLOCK_AGENT_MAX = 64
 BLOCK_META_MAX = 256
 
@@ -260,6 +275,11 @@ def lib() -> ctypes.CDLL:
         "hcp_block_poll_transfers": ([vp, ctypes.POINTER(BlockCompletionC), ctypes.c_size_t,
                                       ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
         "hcp_block_wire_bytes": ([vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+        "hcp_ring_trace_attach": ([vp, ctypes.c_size_t], ctypes.c_int),
+        "hcp_ring_trace_record_bytes": ([ctypes.POINTER(ReplayDesc)], ctypes.c_size_t),
+        "hcp_ring_trace_read": ([vp, ctypes.POINTER(TraceDomain), i32, ctypes.POINTER(i32),
+                                 ctypes.POINTER(TraceLaunch)], ctypes.c_int),
+        "hcp_ring_trace_perf_log": ([vp, i32, ctypes.c_char_p], ctypes.c_int),
         "hcp_ring_replay_timing": ([i32], ctypes.c_int),
         "hcp_ring_replay_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)],
                                         ctypes.c_int),
@@ -924,6 +944,40 @@ def synth_normals(seed: int, offset: int, count: int, out, stream=None):
     _check(lib().hcp_synth_normals(ctypes.c_uint64(seed), offset, count, dtype_code(out.dtype),
                                    _ptr(out), _stream(stream)))
     return out
+
+
+def trace_record_bytes(dtype, hq, hkv, d, chunks, causal=True) -> int:
+    """Bytes of trace records one fused replay of this shape writes."""
+    desc, _arr = replay_desc(dtype, hq, hkv, d, chunks, causal)
+    return lib().hcp_ring_trace_record_bytes(ctypes.byref(desc))
+
+
+def trace_attach(buffer) -> None:
+    """Trace every later fused replay on this thread into ``buffer`` (a device tensor,
+    kept referenced by the caller); ``None`` detaches."""
+    if buffer is None:
+        _check(lib().hcp_ring_trace_attach(None, 0))
+    else:
+        _check(lib().hcp_ring_trace_attach(_ptr(buffer), buffer.numel() * buffer.element_size()))
+
+
+def _struct_dict(x) -> dict:
+    return {name: getattr(x, name) for name, _ in x._fields_ if not name.startswith("reserved")}
+
+
+def trace_read(stream=None):
+    """(per-domain statistics, launch statistics) of the last traced replay."""
+    doms = (TraceDomain * 64)()
+    n = ctypes.c_int32(0)
+    launch = TraceLaunch()
+    _check(lib().hcp_ring_trace_read(_stream(stream), doms, 64, ctypes.byref(n), ctypes.byref(launch)))
+    return [_struct_dict(doms[i]) for i in range(n.value)], _struct_dict(launch)
+
+
+def trace_perf_log(layer_idx: int, path: str | None = None, stream=None) -> None:
+    """Append the last traced replay's ring_attention events (JSONL) to ``path`` or
+    to $HCP_PERF_LOG (ring.rs:820-844)."""
+    _check(lib().hcp_ring_trace_perf_log(_stream(stream), layer_idx, path.encode() if path else None))
 
 
 def replay_timing(enable: bool) -> None:

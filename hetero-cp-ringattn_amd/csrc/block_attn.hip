@@ -406,10 +406,20 @@ struct RingPlan {
   float scale_log2;
   int32_t off[kMaxDomains], len[kMaxDomains];   // rows (= global positions) of each domain
   int32_t qt_begin[kMaxDomains + 1];            // query tiles of slot s (domain n-1-s)
+  uint32_t* trace;                              // trace records (the TRACE kernels only)
+  int32_t trace_stride;                         // 32-bit words per record
 };
 static_assert(sizeof(RingPlan) <= 4096, "kernel arguments are limited to 4 KiB");
 
-template <int DT, int G, bool POS, int BK, bool RING, class P>
+// Trace record of one workgroup of a traced fused ring (hcp_ring_trace_attach), 32-bit
+// words: [0, 2) s_memrealtime at entry (100 MHz), [2, 4) at the end, [4, 6) / [6, 8)
+// s_memtime (shader clock) at entry / end, 8 HW_ID, 9 XCC_ID, 10 target domain |
+// head group << 16, 11 query tile, 12 key tiles folded, [13, 16) zero, then for ring
+// position s (0 = the local chunk, s = source (t - s) mod N) the s_memrealtime at which
+// the workgroup moved past that source, two words each (0: never visited).
+constexpr int kTraceHeaderWords = 16;
+
+template <int DT, int G, bool POS, int BK, bool RING, class P, bool TRACE = false>
 __device__ __forceinline__ void pingpong_body(const P& plan) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
@@ -433,6 +443,11 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   int* const lim_red = reinterpret_cast<int*>(v_lds + (NBV - 1) * BK * D);
   int* const simd_of = lim_red + kWaves;
 
+  [[maybe_unused]] uint64_t trace_t0 = 0, trace_c0 = 0;
+  if constexpr (TRACE) {
+    trace_t0 = __builtin_amdgcn_s_memrealtime();
+    trace_c0 = __builtin_amdgcn_s_memtime();
+  }
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -862,9 +877,30 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     issue(1);
     if (live(0)) xphase(0);
   }
+  // Trace: wave 0 stamps the time at which its tiles move from one source to the next
+  // (a tile belongs to the source of its top row; ring position (t - d) mod N).
+  [[maybe_unused]] int trace_slot = 0;
+  [[maybe_unused]] uint32_t* trace_rec = nullptr;
+  auto trace_tile = [&](int t) __attribute__((always_inline)) {
+    if constexpr (TRACE && RING) {
+      if (wave != 0 || t < nt0) return;
+      int kr, ke;
+      tile_rows(t, kr, ke);
+      int dom = 0;
+      while (dom + 1 < plan.n && ke - 1 >= plan.off[dom + 1]) ++dom;
+      const int slot = (t_dom - dom + plan.n) % plan.n;
+      if (slot != trace_slot) {
+        const uint64_t now = __builtin_amdgcn_s_memrealtime();
+        if (lane == 0) *reinterpret_cast<uint64_t*>(trace_rec + kTraceHeaderWords + 2 * trace_slot) = now;
+        trace_slot = slot;
+      }
+    }
+  };
+  if constexpr (TRACE && RING) trace_rec = plan.trace + static_cast<int64_t>(blockIdx.x) * plan.trace_stride;
   const int lag = lead ? 0 : 1;
   int u = 1, rk = 1 % NBK, rv = 0;
   for (; u <= hot; ++u, rk = next(rk, NBK), rv = next(rv, NBV)) {
+    if constexpr (TRACE) trace_tile(u);
     m_full(rk, rv);
     if (!lead) settle(u);
     issue(u + lag);
@@ -884,6 +920,26 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     write_final_row<D>(plan.out, plan.dtype, head * plan.out_hs + row * plan.out_ss,
                        plan.lse != nullptr ? plan.lse + head * plan.lse_hs + row : nullptr, lhalf, oacc, m_run,
                        sum_xor32(l_run), dn);
+    if constexpr (TRACE) {
+      if (wave == 0) {  // wave 0 always holds rows (a query tile's first 32 rows exist)
+        const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+        const uint64_t c1 = __builtin_amdgcn_s_memtime();
+        uint32_t hw, xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        if (lane == 0) {
+          uint64_t* r64 = reinterpret_cast<uint64_t*>(trace_rec);
+          r64[0] = trace_t0;
+          r64[1] = t1;
+          r64[2] = trace_c0;
+          r64[3] = c1;
+          *reinterpret_cast<u32x4*>(trace_rec + 8) =
+              u32x4{hw, xcc, static_cast<uint32_t>(t_dom) | (static_cast<uint32_t>(hg) << 16), static_cast<uint32_t>(qt)};
+          *reinterpret_cast<u32x4*>(trace_rec + 12) = u32x4{static_cast<uint32_t>(n_tiles), 0u, 0u, 0u};
+          r64[kTraceHeaderWords / 2 + trace_slot] = t1;
+        }
+      }
+    }
   } else {
     write_row<D>(*ap, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run), dn);
   }
@@ -894,9 +950,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(Block
   pingpong_body<DT, G, POS, BK, false>(grp);
 }
 
-template <int DT, int G, int BK>
+template <int DT, int G, int BK, bool TRACE>
 __global__ __launch_bounds__(kThreads, 1) void flash_ring_kernel(RingPlan plan) {
-  pingpong_body<DT, G, false, BK, true>(plan);
+  pingpong_body<DT, G, false, BK, true, RingPlan, TRACE>(plan);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1207,6 +1263,25 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
   HCP_HIP(hipGetLastError());
 }
 
+template <bool TRACE>
+static void launch_ring_kernel(int dtype, int g, dim3 grid, const RingPlan& p, hipStream_t stream) {
+  if (dtype == kBF16) {
+    switch (g) {
+      case 8: flash_ring_kernel<kBF16, 8, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+      case 4: flash_ring_kernel<kBF16, 4, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+      case 2: flash_ring_kernel<kBF16, 2, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+      default: flash_ring_kernel<kBF16, 1, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+    }
+  } else {
+    switch (g) {
+      case 8: flash_ring_kernel<kF16, 8, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+      case 4: flash_ring_kernel<kF16, 4, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+      case 2: flash_ring_kernel<kF16, 2, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+      default: flash_ring_kernel<kF16, 1, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+    }
+  }
+}
+
 bool ring_fused_applies(int dtype, int d) { return (dtype == kBF16 || dtype == kF16) && padded_d_ok(d); }
 
 void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
@@ -1243,23 +1318,24 @@ void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
   for (int s = 0; s < L.n; ++s) p.qt_begin[s + 1] = p.qt_begin[s] + static_cast<int32_t>(ceil_div(p.len[L.n - 1 - s], tq));
   const int64_t blocks = static_cast<int64_t>(p.qt_begin[L.n]) * p.n_groups;
   require(blocks <= INT32_MAX, "fused ring: too many workgroups");
+  require(blocks == ring_fused_workgroups(L.hq, L.hkv, L.n, L.len), "fused ring: workgroup count");
+  p.trace = L.trace;
+  p.trace_stride = L.trace_stride;
+  if (L.trace != nullptr) require(L.trace_stride >= kTraceHeaderWords + 2 * L.n, "fused ring: trace stride");
   const dim3 grid(static_cast<unsigned>(blocks));
-  if (L.dtype == kBF16) {
-    switch (g) {
-      case 8: flash_ring_kernel<kBF16, 8, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
-      case 4: flash_ring_kernel<kBF16, 4, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
-      case 2: flash_ring_kernel<kBF16, 2, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
-      default: flash_ring_kernel<kBF16, 1, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
-    }
-  } else {
-    switch (g) {
-      case 8: flash_ring_kernel<kF16, 8, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
-      case 4: flash_ring_kernel<kF16, 4, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
-      case 2: flash_ring_kernel<kF16, 2, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
-      default: flash_ring_kernel<kF16, 1, kBK3><<<grid, kThreads, 0, stream>>>(p); break;
-    }
-  }
+  if (L.trace != nullptr) launch_ring_kernel<true>(L.dtype, g, grid, p, stream);
+  else launch_ring_kernel<false>(L.dtype, g, grid, p, stream);
   HCP_HIP(hipGetLastError());
 }
+
+int64_t ring_fused_workgroups(int hq, int hkv, int n, const int64_t* len) {
+  const int g = heads_per_group(hq / hkv);
+  const int tq = 32 * (kWaves / g);
+  int64_t tiles = 0;
+  for (int i = 0; i < n; ++i) tiles += ceil_div(len[i], tq);
+  return tiles * (hq / g);
+}
+
+int ring_trace_words(int n) { return kTraceHeaderWords + 2 * n; }
 
 }  // namespace hcp

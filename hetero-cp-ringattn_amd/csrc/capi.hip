@@ -6,7 +6,12 @@
 // (rust_bridge.cc:19-27,614-644).  The C++ ring-replay driver (the single-GPU
 // counterpart of HcpRingAttentionBackend::ring_attention, ring.rs:861-1398) lives here
 // too; it only enqueues kernels.
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <map>
 #include <functional>
 #include <mutex>
 #include <string>
@@ -305,6 +310,20 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
   return p;
 }
 
+// Trace of fused replays (hcp_ring_trace_attach): the caller's device buffer and the
+// geometry of the last traced replay, per thread like the rest of the call state.
+struct TraceState {
+  void* buf = nullptr;
+  size_t bytes = 0;
+  bool have = false;  // a traced replay ran since the buffer was attached
+  int n = 0, hkv = 0, d = 0, es = 0;
+  std::vector<int64_t> len;
+  std::vector<std::vector<int>> sources;  // per target, ring order
+  int64_t blocks = 0;
+  int stride = 0;
+};
+thread_local TraceState g_trace;
+
 // Whole replay as one fused-ring launch (HCP_SCHEDULE_FUSED): q / k / v / out are the
 // whole-sequence views.
 void run_replay_fused(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ring_view q, hcp_ring_view k,
@@ -327,8 +346,114 @@ void run_replay_fused(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ri
   L.lse = lse_out;
   L.lse_hs = p.seq;
   L.len = p.len.data();
+  if (g_trace.buf != nullptr) {
+    const int64_t blocks = ring_fused_workgroups(L.hq, L.hkv, p.n, p.len.data());
+    const int stride = ring_trace_words(p.n);
+    const size_t need = static_cast<size_t>(blocks) * stride * sizeof(uint32_t);
+    require(g_trace.bytes >= need, "trace buffer too small: need " + std::to_string(need) + " bytes");
+    L.trace = static_cast<uint32_t*>(g_trace.buf);
+    L.trace_stride = stride;
+    g_trace.have = true;
+    g_trace.n = p.n;
+    g_trace.hkv = d->num_kv_heads;
+    g_trace.d = d->head_dim;
+    g_trace.es = elem_size(d->dtype);
+    g_trace.len = p.len;
+    g_trace.sources = p.sources;
+    g_trace.blocks = blocks;
+    g_trace.stride = stride;
+  }
   timed(kTimedBlock, stream, [&] { launch_ring_fused(L, stream); });
   g_last_path = HCP_PATH_RING_FUSED;
+}
+
+// Per-domain and per-launch statistics of the last traced replay (layout of the
+// records: include/hcp_ring.h, hcp_ring_trace_attach).
+void trace_stats(hipStream_t stream, std::vector<hcp_ring_trace_domain>& doms, hcp_ring_trace_launch& L) {
+  const TraceState& t = g_trace;
+  require(t.buf != nullptr, "no trace buffer attached");
+  require(t.have, "no traced replay since the trace buffer was attached");
+  HCP_HIP(hipStreamSynchronize(stream));
+  std::vector<uint32_t> w(static_cast<size_t>(t.blocks) * t.stride);
+  HCP_HIP(hipMemcpy(w.data(), t.buf, w.size() * sizeof(uint32_t), hipMemcpyDeviceToHost));
+  auto u64 = [&](int64_t rec, int word) {
+    const uint32_t* r = w.data() + rec * t.stride + word;
+    return static_cast<uint64_t>(r[0]) | (static_cast<uint64_t>(r[1]) << 32);
+  };
+  constexpr double kTicksPerMs = 1e5;  // s_memrealtime runs at 100 MHz
+  doms.assign(t.n, hcp_ring_trace_domain{});
+  std::vector<uint64_t> d_first(t.n, UINT64_MAX), d_last(t.n, 0), d_ticks(t.n, 0), d_clk(t.n, 0);
+  std::map<uint32_t, std::vector<std::pair<uint64_t, uint64_t>>> per_cu;
+  L = hcp_ring_trace_launch{};
+  uint64_t first = UINT64_MAX, last = 0, busy = 0, clk = 0, wmin = UINT64_MAX, wmax = 0;
+  for (int64_t r = 0; r < t.blocks; ++r) {
+    const uint64_t t0 = u64(r, 0), t1 = u64(r, 2), c0 = u64(r, 4), c1 = u64(r, 6);
+    const uint32_t* hdr = w.data() + r * t.stride;
+    const int dom = static_cast<int>(hdr[10] & 0xffffu);
+    require(t1 > t0 && dom < t.n, "incomplete trace record " + std::to_string(r));
+    hcp_ring_trace_domain& D = doms[dom];
+    D.workgroups += 1;
+    D.key_tiles += hdr[12];
+    uint64_t prev = t0, local = 0, peer = 0;
+    for (int s = 0; s < t.n; ++s) {
+      const uint64_t st = u64(r, 16 + 2 * s);
+      if (st == 0) continue;
+      const uint64_t seg = st > prev ? st - prev : 0;
+      (s == 0 ? local : peer) += seg;
+      prev = std::max(prev, st);
+    }
+    D.local_cu_ms += local / kTicksPerMs;
+    D.peer_cu_ms += peer / kTicksPerMs;
+    d_first[dom] = std::min(d_first[dom], t0);
+    d_last[dom] = std::max(d_last[dom], t1);
+    d_ticks[dom] += t1 - t0;
+    d_clk[dom] += c1 - c0;
+    per_cu[(hdr[9] << 16) | ((hdr[8] >> 8) & 0xffu)].push_back({t0, t1});
+    first = std::min(first, t0);
+    last = std::max(last, t1);
+    busy += t1 - t0;
+    clk += c1 - c0;
+    wmin = std::min(wmin, t1 - t0);
+    wmax = std::max(wmax, t1 - t0);
+  }
+  L.workgroups = t.blocks;
+  L.cus = static_cast<int32_t>(per_cu.size());
+  L.span_ms = (last - first) / kTicksPerMs;
+  L.busy_cu_ms = busy / kTicksPerMs;
+  L.clock_mhz = busy > 0 ? 100.0 * clk / busy : 0.0;
+  L.wg_ms_min = wmin / kTicksPerMs;
+  L.wg_ms_max = wmax / kTicksPerMs;
+  L.wg_ms_mean = t.blocks > 0 ? L.busy_cu_ms / t.blocks : 0.0;
+  for (auto& kv : per_cu) {
+    auto& v = kv.second;
+    std::sort(v.begin(), v.end());
+    L.head_cu_ms += (v.front().first - first) / kTicksPerMs;
+    L.tail_cu_ms += (last - v.back().second) / kTicksPerMs;
+    uint64_t end = v.front().second;
+    for (size_t i = 1; i < v.size(); ++i) {
+      if (v[i].first > end) L.idle_gap_cu_ms += (v[i].first - end) / kTicksPerMs;
+      end = std::max(end, v[i].second);
+    }
+  }
+  const double cus = std::max(1, L.cus);
+  const int64_t row_bytes = static_cast<int64_t>(t.hkv) * t.d * t.es * 2;  // K and V of one token
+  for (int dom = 0; dom < t.n; ++dom) {
+    hcp_ring_trace_domain& D = doms[dom];
+    D.domain = dom;
+    D.span_ms = d_last[dom] > d_first[dom] ? (d_last[dom] - d_first[dom]) / kTicksPerMs : 0.0;
+    D.local_compute_ms = D.local_cu_ms / cus;
+    D.peer_compute_ms = D.peer_cu_ms / cus;
+    D.clock_mhz = d_ticks[dom] > 0 ? 100.0 * d_clk[dom] / d_ticks[dom] : 0.0;
+    for (int src : t.sources[dom])
+      if (src != dom) {
+        D.peer_chunks += 1;
+        D.kv_recv_bytes += t.len[src] * row_bytes;
+      }
+    for (int tgt = 0; tgt < t.n; ++tgt)
+      if (tgt != dom)
+        for (int src : t.sources[tgt])
+          if (src == dom) D.kv_sent_bytes += t.len[dom] * row_bytes;
+  }
 }
 
 void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k, hcp_ring_view v,
@@ -1455,6 +1580,76 @@ int hcp_ring_prefill_replay_paged(const hcp_ring_replay_desc* desc, hcp_ring_vie
     hcp_ring_view none{nullptr, 0, 1};
     run_replay(desc, q, none, none, pool, block_table, table_len, out, lse_out, workspace, workspace_bytes,
                as_stream(stream));
+  });
+}
+
+int hcp_ring_trace_attach(void* buffer, size_t bytes) {
+  return guarded(__func__, [&] {
+    require(buffer == nullptr || bytes > 0, "empty trace buffer");
+    require(reinterpret_cast<uintptr_t>(buffer) % 8 == 0, "trace buffer must be 8-byte aligned");
+    g_trace = TraceState{};
+    g_trace.buf = buffer;
+    g_trace.bytes = buffer != nullptr ? bytes : 0;
+  });
+}
+
+size_t hcp_ring_trace_record_bytes(const hcp_ring_replay_desc* desc) {
+  try {
+    const ReplayPlan p = plan_replay(desc, false);
+    return static_cast<size_t>(ring_fused_workgroups(desc->num_q_heads, desc->num_kv_heads, p.n, p.len.data())) *
+           ring_trace_words(p.n) * sizeof(uint32_t);
+  } catch (...) {
+    return 0;
+  }
+}
+
+int hcp_ring_trace_read(void* stream, hcp_ring_trace_domain* out, int32_t capacity, int32_t* num_domains,
+                        hcp_ring_trace_launch* launch) {
+  return guarded(__func__, [&] {
+    require(out != nullptr && num_domains != nullptr, "null output");
+    std::vector<hcp_ring_trace_domain> doms;
+    hcp_ring_trace_launch L;
+    trace_stats(as_stream(stream), doms, L);
+    require(capacity >= static_cast<int32_t>(doms.size()), "capacity below the number of domains");
+    std::copy(doms.begin(), doms.end(), out);
+    *num_domains = static_cast<int32_t>(doms.size());
+    if (launch != nullptr) *launch = L;
+  });
+}
+
+int hcp_ring_trace_perf_log(void* stream, int32_t layer_idx, const char* path) {
+  return guarded(__func__, [&] {
+    const char* target = path != nullptr ? path : std::getenv("HCP_PERF_LOG");
+    if (target == nullptr || *target == 0) return;
+    std::vector<hcp_ring_trace_domain> doms;
+    hcp_ring_trace_launch L;
+    trace_stats(as_stream(stream), doms, L);
+    const auto now = std::chrono::system_clock::now().time_since_epoch();
+    const long long ms_total = std::chrono::duration_cast<std::chrono::milliseconds>(now).count();
+    char ts[48];
+    std::snprintf(ts, sizeof ts, "%lld.%03lldZ", ms_total / 1000, ms_total % 1000);
+    std::string lines;
+    for (const auto& D : doms) {
+      char buf[1024];
+      std::snprintf(buf, sizeof buf,
+                    "{\"ts\":\"%s\",\"event\":\"ring_attention\",\"domain\":%d,\"layer\":%d,\"total_ms\":%.3f,"
+                    "\"local_compute_ms\":%.3f,\"peer_compute_ms\":%.3f,\"recv_ms\":0.000,\"send_ms\":0.000,"
+                    "\"forward_ms\":0.000,\"flush_ms\":0.000,\"kv_sent_bytes\":%lld,\"kv_recv_bytes\":%lld,"
+                    "\"wire_sent_bytes\":0,\"wire_recv_bytes\":0,\"micro_blocks\":%lld,\"num_domains\":%d,"
+                    "\"seq_len\":%lld,\"overlap\":1,\"workgroups\":%d,\"key_tiles\":%lld,\"local_cu_ms\":%.3f,"
+                    "\"peer_cu_ms\":%.3f,\"clock_mhz\":%.1f,\"schedule\":\"fused\"}\n",
+                    ts, D.domain, layer_idx, D.span_ms, D.local_compute_ms, D.peer_compute_ms,
+                    static_cast<long long>(D.kv_sent_bytes), static_cast<long long>(D.kv_recv_bytes),
+                    static_cast<long long>(D.peer_chunks), g_trace.n,
+                    static_cast<long long>(g_trace.len[D.domain]), D.workgroups,
+                    static_cast<long long>(D.key_tiles), D.local_cu_ms, D.peer_cu_ms, D.clock_mhz);
+      lines += buf;
+    }
+    FILE* f = std::fopen(target, "a");
+    require(f != nullptr, std::string("cannot open perf log ") + target);
+    const size_t wrote = std::fwrite(lines.data(), 1, lines.size(), f);
+    std::fclose(f);
+    require(wrote == lines.size(), std::string("short write to perf log ") + target);
   });
 }
 

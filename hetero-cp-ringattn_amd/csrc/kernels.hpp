@@ -61,9 +61,17 @@ struct RingLaunch {
   float* lse;
   int64_t lse_hs;
   const int64_t* len;  // HOST array of n chunk lengths
+  // Traced launch (non-null): one record of trace_stride >= ring_trace_words(n) 32-bit
+  // words per workgroup (layout in block_attn.hip, kTraceHeaderWords).
+  uint32_t* trace = nullptr;
+  int trace_stride = 0;
 };
 bool ring_fused_applies(int dtype, int d);
 void launch_ring_fused(const RingLaunch& L, hipStream_t stream);
+// Workgroups of the fused ring launch for this head layout and chunk list.
+int64_t ring_fused_workgroups(int hq, int hkv, int n, const int64_t* len);
+// 32-bit words of one trace record of an n-domain fused ring.
+int ring_trace_words(int n);
 
 void launch_lse_merge(int n, const float* const* o_parts, const float* const* lse_parts, int heads,
                       int64_t q_len, int d, int out_dtype, void* out, int64_t out_hs, int64_t out_ss,

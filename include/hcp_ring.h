@@ -673,6 +673,80 @@ int hcp_ring_replay_timing(int32_t enable);
 int hcp_ring_replay_timing_read(double* ms, int64_t* launches);
 
 /* ---------------------------------------------------------------------------------
+ * Per-ring-call trace and perf events (the JSONL perf log of ring.rs:820-844 and the
+ * ring_attention event of ring.rs:1376-1395, HCP_PERF_LOG).
+ *
+ * hcp_ring_trace_attach: every later fused-schedule replay on the calling thread
+ * (hcp_ring_prefill_replay / _paged taking the fused path) runs the traced build of
+ * the fused ring kernel, which writes one record per workgroup into `buffer` (caller-
+ * owned DEVICE memory of `bytes`; null detaches).  A replay needs
+ * hcp_ring_trace_record_bytes(desc) bytes (-6 if the buffer is smaller).  Records are
+ * 16 + 2 * num_domains 32-bit words: [0,2) s_memrealtime (100 MHz) at workgroup entry,
+ * [2,4) at its end, [4,6) / [6,8) s_memtime (shader clock) at entry / end, 8 HW_ID,
+ * 9 XCC_ID, 10 target domain | head group << 16, 11 query tile, 12 128-key tiles
+ * folded, 13-15 zero, then per ring position s (0 = own chunk, s = source (t - s) mod N)
+ * the s_memrealtime at which the workgroup moved past that source (0: not visited).
+ * Each traced replay overwrites the records of the previous one.
+ *
+ * hcp_ring_trace_read: waits for `stream`, reads the last traced replay's records and
+ * aggregates them per target domain (out[0 .. num_domains), capacity >= num_domains)
+ * and for the whole launch (*launch, may be null).  compute_ms fields are CU-time
+ * divided by the CUs the launch used (the time the domain's share would take with
+ * the GPU to itself); span_ms is wall time from the first workgroup's start to the
+ * last one's end.
+ *
+ * hcp_ring_trace_perf_log: the same statistics appended as one JSON line per domain
+ * to `path` (null: the HCP_PERF_LOG environment variable; neither set: nothing is
+ * written and 0 is returned), in the reference's ring_attention event shape:
+ * {"ts","event":"ring_attention","domain","layer","total_ms","local_compute_ms",
+ * "peer_compute_ms","recv_ms","send_ms","forward_ms","flush_ms","kv_sent_bytes",
+ * "kv_recv_bytes","wire_sent_bytes","wire_recv_bytes","micro_blocks","num_domains",
+ * "seq_len","overlap"} plus "workgroups","key_tiles","local_cu_ms","peer_cu_ms",
+ * "clock_mhz","schedule".  Transfer times and wire bytes are 0 (the ring is replayed in
+ * HBM); kv_recv_bytes are the peer chunks' K/V bytes the domain folded and
+ * kv_sent_bytes its own chunk's bytes times the domains that folded it (Hkv layout, as
+ * a multi-GPU ring would move them); micro_blocks counts the peer chunks folded.
+ * ------------------------------------------------------------------------------- */
+typedef struct hcp_ring_trace_domain {
+  int32_t domain;
+  int32_t workgroups;
+  int64_t key_tiles;         /* 128-key tiles folded by the domain's workgroups */
+  int64_t peer_chunks;       /* peer sources folded */
+  int64_t kv_recv_bytes;
+  int64_t kv_sent_bytes;
+  double span_ms;
+  double local_cu_ms;        /* CU-milliseconds on the domain's own chunk */
+  double peer_cu_ms;         /* CU-milliseconds on peer chunks */
+  double local_compute_ms;   /* local_cu_ms / cus */
+  double peer_compute_ms;    /* peer_cu_ms / cus */
+  double clock_mhz;          /* mean shader clock over the domain's workgroups */
+} hcp_ring_trace_domain;
+
+typedef struct hcp_ring_trace_launch {
+  int64_t workgroups;
+  int32_t cus;               /* distinct CUs that ran a workgroup */
+  int32_t reserved0;
+  double span_ms;            /* first workgroup start to last workgroup end */
+  double busy_cu_ms;         /* sum of workgroup durations */
+  double idle_gap_cu_ms;     /* sum over CUs of the gaps between consecutive workgroups */
+  double tail_cu_ms;         /* sum over CUs of (launch end - the CU's last workgroup end) */
+  double head_cu_ms;         /* sum over CUs of (the CU's first start - launch start) */
+  double clock_mhz;          /* busy-time-weighted mean shader clock */
+  double wg_ms_min;          /* shortest, mean and longest workgroup */
+  double wg_ms_mean;
+  double wg_ms_max;
+} hcp_ring_trace_launch;
+
+int hcp_ring_trace_attach(void* buffer, size_t bytes);
+
+size_t hcp_ring_trace_record_bytes(const hcp_ring_replay_desc* desc);
+
+int hcp_ring_trace_read(void* stream, hcp_ring_trace_domain* out, int32_t capacity, int32_t* num_domains,
+                        hcp_ring_trace_launch* launch);
+
+int hcp_ring_trace_perf_log(void* stream, int32_t layer_idx, const char* path);
+
+/* ---------------------------------------------------------------------------------
  * Synthetic inputs (no reference counterpart; used by the benchmark).
  *
  * Writes normals n = offset .. offset+count-1 of the LCG + Box-Muller stream of

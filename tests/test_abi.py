@@ -255,3 +255,32 @@ def test_block_transport_metadata_without_a_gpu(hcp):
     finally:
         a.destroy()
         b.destroy()
+
+
+def test_trace_entry_points_validate_without_gpu(hcp):
+    # Reading with nothing attached, or with nothing traced yet, is refused before any
+    # device work; the record size follows the fused launch geometry.
+    assert hcp.lib().hcp_ring_trace_attach(None, 0) == 0
+    n = ctypes.c_int32(0)
+    doms = (hcp.TraceDomain * 4)()
+    assert hcp.lib().hcp_ring_trace_read(None, doms, 4, ctypes.byref(n), None) == -6
+    assert "no trace buffer attached" in hcp.last_error()
+    assert hcp.lib().hcp_ring_trace_attach(ctypes.c_void_p(4), 64) == -6  # misaligned
+    assert hcp.lib().hcp_ring_trace_attach(ctypes.c_void_p(256), 64) == 0
+    assert hcp.lib().hcp_ring_trace_read(None, doms, 4, ctypes.byref(n), None) == -6
+    assert "no traced replay" in hcp.last_error()
+    assert hcp.lib().hcp_ring_trace_attach(None, 0) == 0
+    # c3: 4 domains, G = 4 (64 query rows per workgroup), 8 head groups
+    chunks = [12288, 8192, 8192, 4096]
+    wgs = sum((c + 63) // 64 for c in chunks) * 8
+    assert hcp.trace_record_bytes(torch.bfloat16, 32, 8, 128, chunks) == wgs * (16 + 2 * 4) * 4
+    # c2: G = 8 (32 rows), 2 head groups
+    assert hcp.trace_record_bytes(torch.bfloat16, 16, 2, 128, [4096, 2560, 1536]) == 512 * (16 + 6) * 4
+    # perf log with no path and no HCP_PERF_LOG is a no-op, even without a trace
+    import os
+    old = os.environ.pop("HCP_PERF_LOG", None)
+    try:
+        assert hcp.lib().hcp_ring_trace_perf_log(None, 0, None) == 0
+    finally:
+        if old is not None:
+            os.environ["HCP_PERF_LOG"] = old

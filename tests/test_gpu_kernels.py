@@ -1123,3 +1123,74 @@ def test_block_transport_carries_a_kv_wire_frame(gpu):
     finally:
         a.destroy()
         b.destroy()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_traced_fused_replay_statistics_and_perf_log(gpu, causal, tmp_path):
+    # The traced fused ring (per-ring-call timing, ring.rs:820-844,1376-1395) computes
+    # the same bits as the untraced one, and its per-domain statistics follow the ring's
+    # geometry: workgroups per domain, 128-key tiles folded, peer chunks and their K/V
+    # bytes; the JSONL events carry the reference's ring_attention fields.
+    import json
+    chunks, hq, hkv, d = [900, 300, 500, 348], 8, 2, 128
+    s = sum(chunks)
+    (q, k, v), _ = draw(71, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    ref_o, ref_l = H.ring_attention_replay(qh, kh, vh, chunks, causal=causal)
+    need = H.trace_record_bytes(torch.bfloat16, hq, hkv, d, chunks, causal)
+    small = torch.zeros(need // 2, dtype=torch.uint8, device="cuda")
+    H.trace_attach(small)
+    with pytest.raises(H.HcpRingError, match="trace buffer too small"):
+        H.ring_attention_replay(qh, kh, vh, chunks, causal=causal)
+    buf = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    H.trace_attach(buf)
+    try:
+        o, l = H.ring_attention_replay(qh, kh, vh, chunks, causal=causal)
+        assert H.last_path() == "ring_fused"
+        doms, launch = H.trace_read()
+        log = tmp_path / "perf.jsonl"
+        H.trace_perf_log(3, str(log))
+    finally:
+        H.trace_attach(None)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref_o) and torch.equal(l, ref_l)
+    n = len(chunks)
+    offs = [sum(chunks[:i]) for i in range(n)]
+    tq, groups = 32 * 8 // 4, hq // 4           # G = 4 query heads per workgroup
+    row_bytes = hkv * d * 2 * 2
+    assert [x["domain"] for x in doms] == list(range(n))
+    total_tiles = 0
+    for t, x in enumerate(doms):
+        assert x["workgroups"] == -(-chunks[t] // tq) * groups
+        tiles = 0
+        for qt in range(-(-chunks[t] // tq)):
+            q_end = min(chunks[t], (qt + 1) * tq)
+            local = -(-(q_end if causal else chunks[t]) // 128)
+            below = -(-offs[t] // 128)
+            above = 0 if causal else -(-(s - offs[t] - chunks[t]) // 128)
+            tiles += local + below + above
+        assert x["key_tiles"] == tiles * groups
+        total_tiles += tiles * groups
+        srcs = list(range(t)) if causal else [j for j in range(n) if j != t]
+        assert x["peer_chunks"] == len(srcs)
+        assert x["kv_recv_bytes"] == sum(chunks[j] for j in srcs) * row_bytes
+        users = (n - 1 - t) if causal else (n - 1)
+        assert x["kv_sent_bytes"] == chunks[t] * row_bytes * users
+        assert x["local_cu_ms"] > 0 and x["span_ms"] > 0
+        assert (x["peer_cu_ms"] > 0) == (len(srcs) > 0)
+        assert 300 < x["clock_mhz"] < 3000
+    assert launch["workgroups"] == sum(x["workgroups"] for x in doms)
+    assert 1 <= launch["cus"] <= 256 and launch["span_ms"] > 0
+    assert launch["wg_ms_min"] <= launch["wg_ms_mean"] <= launch["wg_ms_max"]
+    cu_ms = sum(x["local_cu_ms"] + x["peer_cu_ms"] for x in doms)
+    assert cu_ms <= launch["busy_cu_ms"] * 1.0001
+    lines = [json.loads(x) for x in log.read_text().splitlines()]
+    assert [e["domain"] for e in lines] == list(range(n))
+    for e, x in zip(lines, doms):
+        assert e["event"] == "ring_attention" and e["layer"] == 3 and e["num_domains"] == n
+        assert e["seq_len"] == chunks[e["domain"]] and e["overlap"] == 1
+        assert e["kv_recv_bytes"] == x["kv_recv_bytes"] and e["micro_blocks"] == x["peer_chunks"]
+        assert abs(e["local_compute_ms"] - round(x["local_compute_ms"], 3)) < 2e-3
+        for key in ("total_ms", "peer_compute_ms", "recv_ms", "send_ms", "forward_ms", "flush_ms",
+                    "kv_sent_bytes", "wire_sent_bytes", "wire_recv_bytes", "ts"):
+            assert key in e

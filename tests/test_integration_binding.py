@@ -187,6 +187,7 @@ CTYPES_MIRRORS = {
     "ReplayDesc": "hcp_ring_replay_desc", "BlockDescC": "hcp_block_desc",
     "RemoteBlockDescC": "hcp_remote_block_desc", "BlockCompletionC": "hcp_block_completion",
     "KvFrameDesc": "hcp_kv_frame_desc", "PacketFrameDesc": "hcp_packet_frame_desc", "QkvDesc": "hcp_qkv_desc",
+    "TraceDomain": "hcp_ring_trace_domain", "TraceLaunch": "hcp_ring_trace_launch",
 }
 
 
