@@ -41,6 +41,9 @@ C4 = dict(batch=64, hq=32, hkv=8, d=128, bs=16, ctx=16384, chunks=[8192, 5120, 3
           pool_blocks=65536, seed=45)
 C5 = dict(chunks=[21504, 13312, 18432, 23552, 24576, 9216, 8192, 12288], hq=32, hkv=8, d=128,
           bs=16, seed=46)
+# The reference's own model (Qwen2-0.5B: 14 q / 2 kv heads, head dim 64,
+# docs/2domain_mps_hip_scale_matrix.md) on c3's 32k 4-domain split.
+QWEN64 = dict(name="qwen2_0p5b_d64", chunks=[12288, 8192, 8192, 4096], hq=14, hkv=2, d=64, seed=47)
 
 
 def log(msg: str) -> None:
@@ -221,6 +224,24 @@ def bench_c2(H, torch, steps: int, warmup: int):
            **prefill_summary(fused), "per_step": prefill_summary(per),
            "max_abs_diff_schedules": round((fused["out"].float() - per["out"].float()).abs().max().item(), 5)}
     del fused, per
+    return res
+
+
+def bench_qwen_d64(H, torch, steps: int, warmup: int):
+    """32k 4-domain ring with Qwen2-0.5B heads (14 q / 2 kv, D=64), bf16, causal, fused
+    schedule: K/V token-major (adjacent KV heads: paired head-dim-64 kernels), and the
+    same tensors head-major (KV heads apart: zero-padded to 128) in the same run."""
+    c = QWEN64
+    paired = bench_prefill(H, torch, steps, warmup, c)
+    q, k, v = paired["tensors"]
+    padded = bench_prefill(H, torch, steps, warmup, c,
+                           tensors=(q, k.permute(1, 0, 2).contiguous().permute(1, 0, 2),
+                                    v.permute(1, 0, 2).contiguous().permute(1, 0, 2)))
+    log(f"qwen d64 {paired['tflops']:.1f} TFLOP/s paired, {padded['tflops']:.1f} zero-padded")
+    res = {"workload": "Qwen2-0.5B heads: S=32768 in [12288,8192,8192,4096], 14q/2kv heads, D=64, bf16, causal",
+           **prefill_summary(paired), "zero_padded": prefill_summary(padded),
+           "max_abs_diff_layouts": round((paired["out"].float() - padded["out"].float()).abs().max().item(), 5)}
+    del paired, padded
     return res
 
 
@@ -616,7 +637,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
-    ap.add_argument("--leg", choices=["c2", "c3"], default=None,
+    ap.add_argument("--leg", choices=["c2", "c3", "qwen64"], default=None,
                     help="run one prefill leg alone and print its JSON object (profiling)")
     ap.add_argument("--trace", action="store_true",
                     help="with --leg: also run traced launches (per-workgroup records) and summarise them")
@@ -638,8 +659,11 @@ def main():
     H = load_pkg()
     torch.cuda.set_device(0)
     log(f"device {torch.cuda.get_device_name(0)}")
+    if args.leg == "qwen64" and not args.trace:
+        print(json.dumps({"qwen2_0p5b_d64_32k": bench_qwen_d64(H, torch, args.steps, args.warmup)}), flush=True)
+        return
     if args.leg is not None:
-        c = C2 if args.leg == "c2" else C3
+        c = {"c2": C2, "c3": C3, "qwen64": QWEN64}[args.leg]
         r = bench_prefill(H, torch, args.steps, args.warmup, c)
         out = {"leg": args.leg, **prefill_summary(r)}
         if args.trace:
@@ -659,6 +683,7 @@ def main():
                                                        5))
         del per
         c2 = bench_c2(H, torch, args.steps, args.warmup)
+        qwen = bench_qwen_d64(H, torch, args.steps, args.warmup)
         dec = bench_decode(H, torch, args.steps, args.warmup)
         log(f"c4 decode {dec['gbs']:.1f} GB/s")
         stg = bench_staged(H, torch, args.steps, args.warmup)
@@ -692,6 +717,7 @@ def main():
                                  "sampled_max_abs_err_out": stg.get("sampled_err_out"),
                                  "sampled_max_abs_err_lse": stg.get("sampled_err_lse")},
             c2_prefill=c2,
+            qwen2_0p5b_d64_32k=qwen,
             c3_per_step=c3_per_step,
             lse_merge={"workload": "c3 ring partials of the 4 target domains (10 x [32, L, 128] fp32 + LSE) "
                                    "-> bf16 rows + fp32 LSE, one hcp_ring_lse_merge per domain",

@@ -33,6 +33,7 @@
 // General path (fp32, or any head_dim <= 256): one thread per (query row, head), K/V
 // tiles staged in LDS as fp32.  Used for the fp32 CPU-smoke config.
 #include <algorithm>
+#include <cstdlib>
 #include <vector>
 
 #include "kernels.hpp"
@@ -419,15 +420,23 @@ static_assert(sizeof(RingPlan) <= 4096, "kernel arguments are limited to 4 KiB")
 // the workgroup moved past that source, two words each (0: never visited).
 constexpr int kTraceHeaderWords = 16;
 
-template <int DT, int G, bool POS, int BK, bool RING, class P, bool TRACE = false>
+template <int DT, int G, bool POS, int BK, bool RING, class P, bool TRACE = false, bool PAIR = false>
 __device__ __forceinline__ void pingpong_body(const P& plan) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
+  // D: the LDS row of a K / V tile (128 dims).  PAIR (head dim 64): the row holds two
+  // adjacent KV heads, waves 0-3 fold query heads of the first from its left half and
+  // waves 4-7 those of the second from its right half, each with the MFMA work and
+  // fragment reads of a 64-dim head; tiles, DMA, swizzles and transposing reads are
+  // those of the 128-dim layout.
   constexpr int D = kD3;
-  constexpr int TB = kWaves / G;
+  constexpr int DW = PAIR ? kD3 / 2 : kD3;       // head dims a wave folds
+  constexpr int WPH = PAIR ? kWaves / 2 : kWaves;  // waves per KV head of a workgroup
+  static_assert(WPH % G == 0, "heads per group must divide the waves per KV head");
+  constexpr int TB = WPH / G;
   constexpr int TQ = 32 * TB;
-  constexpr int KS = D / 16;
-  constexpr int DB = D / 32;
+  constexpr int KS = DW / 16;
+  constexpr int DB = DW / 32;
   constexpr int kDmaPerWave = BK / 4 / kWaves;  // 1 KiB DMA instructions per wave per tile (K or V)
   constexpr int kTile = BK * D * 2;              // bytes of one K or V tile
   constexpr int NKB = BK / 32;                   // 32-key blocks of S^T per tile
@@ -503,10 +512,20 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     dn = ap->d;
   }
 
-  const int head = hg * G + (wave % G);
-  const int kvh = (hg * G) / rep;
+  const int wave_h = PAIR ? wave % WPH : wave;  // wave index among its KV head's waves
+  const int half = PAIR ? wave / WPH : 0;         // which KV head of the pair (its LDS half)
+  int head, kvh;  // this wave's query head; the (first) KV head whose rows the tiles hold
+  if constexpr (PAIR) {
+    const int per_kv = rep / G;  // head groups per KV head
+    const int pair = hg / per_kv;
+    kvh = 2 * pair;
+    head = (kvh + half) * rep + (hg - pair * per_kv) * G + (wave_h % G);
+  } else {
+    head = hg * G + (wave % G);
+    kvh = (hg * G) / rep;
+  }
   const int tq0 = qt * TQ;
-  const int wq0 = tq0 + (wave / G) * 32;
+  const int wq0 = tq0 + (wave_h / G) * 32;
   const int my_q = wq0 + lcol;
   const int q_end = min(lq, tq0 + TQ);
 
@@ -565,6 +584,7 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   const uint32_t k_lds0 = lds_offset(k_lds) + wave * (kDmaPerWave * 1024);
   const uint32_t v_lds0 = lds_offset(v_lds) + wave * (kDmaPerWave * 1024);
   uint32_t k_voff[kDmaPerWave], v_voff[kDmaPerWave];
+  const int dn_row = PAIR ? 2 * dn : dn;  // dims of a tile row read from the views
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
     const int r = (wave * kDmaPerWave + j) * 4 + (lane >> 4);
@@ -572,8 +592,8 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     // global chunk p ^ swz(r) of row r; chunks past the head dim get an offset beyond any
     // tile's records (tiles stay below 2^31 bytes), so the DMA writes zeros there
     const int kc = p ^ (r & 15), vc = p ^ (4 * (r & 3));
-    k_voff[j] = kc * 8 < dn ? static_cast<uint32_t>(r * k_ss * 2 + (kc << 4)) : 0x80000000u;
-    v_voff[j] = vc * 8 < dn ? static_cast<uint32_t>(r * v_ss * 2 + (vc << 4)) : 0x80000000u;
+    k_voff[j] = kc * 8 < dn_row ? static_cast<uint32_t>(r * k_ss * 2 + (kc << 4)) : 0x80000000u;
+    v_voff[j] = vc * 8 < dn_row ? static_cast<uint32_t>(r * v_ss * 2 + (vc << 4)) : 0x80000000u;
   }
   // Buffer descriptors of a tile's rows [kr, ke): a few scalar instructions per tile
   // (every wave of the CU shares one scalar unit, and the DMA issue sits on the
@@ -638,13 +658,17 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   // K fragment s of a lane sits at k_rd0 ^ (s << 5) in a tile: (lhalf + 2s) ^ (krow & 15)
   // changes only bits 1-3 of the 16-byte column index with s, and tile bases are
   // 1 KiB-aligned, so the XOR commutes with adding the base.
-  const uint32_t k_rd0 = krow * (D * 2) + ((lhalf ^ (krow & 15)) << 4);
+  // (PAIR: k-steps 4 * half + s, the wave's half of the row: the XOR with 4 * half << 5
+  // sets bit 7 only, disjoint from the s << 5 of the loop)
+  const uint32_t k_rd0 = (krow * (D * 2) + ((lhalf ^ (krow & 15)) << 4)) ^ (PAIR ? (4u * half) << 5 : 0u);
   const int g16 = lane >> 4, sl = lane & 15;
   uint32_t v_rd[DB];
 #pragma unroll
-  for (int b = 0; b < DB; ++b)
-    v_rd[b] = (8 * (g16 >> 1) + (sl >> 2)) * (D * 2) +
-              ((4 * (b ^ (sl >> 2)) + 2 * (g16 & 1) + ((sl & 3) >> 1)) << 4) + 8 * (sl & 1);
+  for (int bb = 0; bb < DB; ++bb) {
+    const int b = (PAIR ? 2 * half : 0) + bb;  // 32-dim block of the LDS row
+    v_rd[bb] = (8 * (g16 >> 1) + (sl >> 2)) * (D * 2) +
+               ((4 * (b ^ (sl >> 2)) + 2 * (g16 & 1) + ((sl & 3) >> 1)) << 4) + 8 * (sl & 1);
+  }
   const uint32_t k_lds_off = lds_offset(k_lds);
   const char* v_lds_c = reinterpret_cast<const char*>(v_lds);
 
@@ -917,7 +941,7 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   if (my_q >= lq) return;
   if constexpr (RING) {
     const int64_t row = static_cast<int64_t>(plan.off[t_dom]) + my_q;
-    write_final_row<D>(plan.out, plan.dtype, head * plan.out_hs + row * plan.out_ss,
+    write_final_row<DW>(plan.out, plan.dtype, head * plan.out_hs + row * plan.out_ss,
                        plan.lse != nullptr ? plan.lse + head * plan.lse_hs + row : nullptr, lhalf, oacc, m_run,
                        sum_xor32(l_run), dn);
     if constexpr (TRACE) {
@@ -941,18 +965,18 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
       }
     }
   } else {
-    write_row<D>(*ap, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run), dn);
+    write_row<DW>(*ap, head, my_q, lhalf, oacc, m_run, sum_xor32(l_run), dn);
   }
 }
 
-template <int DT, int G, bool POS, int BK>
+template <int DT, int G, bool POS, int BK, bool PAIR>
 __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockGroup grp) {
-  pingpong_body<DT, G, POS, BK, false>(grp);
+  pingpong_body<DT, G, POS, BK, false, BlockGroup, false, PAIR>(grp);
 }
 
-template <int DT, int G, int BK, bool TRACE>
+template <int DT, int G, int BK, bool TRACE, bool PAIR>
 __global__ __launch_bounds__(kThreads, 1) void flash_ring_kernel(RingPlan plan) {
-  pingpong_body<DT, G, false, BK, true, RingPlan, TRACE>(plan);
+  pingpong_body<DT, G, false, BK, true, RingPlan, TRACE, PAIR>(plan);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1090,6 +1114,35 @@ static int heads_per_group(int rep) {
   return 1;
 }
 
+// Head dim 64 with adjacent KV heads (head stride = 64 elements, as in the token-major
+// [S, Hkv, 64] projection output) and an even KV head count: the paired
+// instantiations, which fold two KV heads per 128-dim tile row instead of zero-padding
+// one head to 128.  Other head-dim-64 layouts (head-major, odd Hkv) stay zero-padded.
+static bool pair_ok(int dtype, int d, int hkv, int64_t k_hs, int64_t v_hs) {
+  return (dtype == kBF16 || dtype == kF16) && d == kD3 / 2 && hkv % 2 == 0 && k_hs == kD3 / 2 && v_hs == kD3 / 2;
+}
+
+// Work decomposition of the matrix-core kernels: query heads per group (sharing a K/V
+// tile), query rows per workgroup and head groups per query tile.  Paired: up to 4
+// query heads of each of the two KV heads (4 waves per KV head).
+struct Geometry {
+  int g, tq, n_groups;
+};
+static Geometry geometry(int hq, int hkv, bool pair) {
+  const int rep = hq / hkv;
+  Geometry r;
+  if (pair) {
+    r.g = rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
+    r.tq = 32 * (kWaves / 2 / r.g);
+    r.n_groups = (hkv / 2) * (rep / r.g);
+  } else {
+    r.g = heads_per_group(rep);
+    r.tq = 32 * (kWaves / r.g);
+    r.n_groups = hq / r.g;
+  }
+  return r;
+}
+
 // The head-dim-128 kernels form buffer descriptors with 32-bit row arithmetic: a tile of
 // kBK3 rows of either view must stay below 2^31 bytes.
 static void check_tile_bytes(int64_t k_ss, int64_t v_ss) {
@@ -1097,7 +1150,7 @@ static void check_tile_bytes(int64_t k_ss, int64_t v_ss) {
           "k/v sequence strides too large for the matrix-core kernel");
 }
 
-static BlockArgs make_args(const BlockLaunch& L) {
+static BlockArgs make_args(const BlockLaunch& L, bool pair) {
   BlockArgs a;
   a.q = static_cast<const uint16_t*>(L.q);
   a.k = static_cast<const uint16_t*>(L.k);
@@ -1124,16 +1177,28 @@ static BlockArgs make_args(const BlockLaunch& L) {
   a.alt_hs = L.alt_hs;
   a.alt_ss = L.alt_ss;
   a.d = static_cast<int32_t>(L.d);
-  const int g = heads_per_group(a.rep);
-  a.n_qtiles = static_cast<int32_t>(ceil_div(L.lq, 32 * (kWaves / g)));
-  a.n_groups = L.hq / g;
+  const Geometry geo = geometry(L.hq, L.hkv, pair);
+  a.n_qtiles = static_cast<int32_t>(ceil_div(L.lq, geo.tq));
+  a.n_groups = geo.n_groups;
   return a;
+}
+
+static bool block_pair_ok(const BlockLaunch& L) {
+  if (!pair_ok(L.dtype, L.d, L.hkv, L.k_hs, L.v_hs)) return false;
+  // the sorted-row copies of a positioned call are head-major: not paired
+  return L.kv_sel == nullptr;
 }
 
 // One launch of the head-dim-128 kernel over grp.a[0 .. grp.n) (same dtype, heads, and
 // positions mode; every pair has at least one query tile).
+template <int DT, int G, bool PAIR>
+static void launch_pingpong_g(const BlockGroup& grp, bool pos, dim3 grid, hipStream_t stream) {
+  if (pos) flash_block_pingpong_kernel<DT, G, true, kBK3, PAIR><<<grid, kThreads, 0, stream>>>(grp);
+  else flash_block_pingpong_kernel<DT, G, false, kBK3, PAIR><<<grid, kThreads, 0, stream>>>(grp);
+}
+
 template <int DT>
-static void launch_pingpong(BlockGroup& grp, hipStream_t stream) {
+static void launch_pingpong(BlockGroup& grp, hipStream_t stream, bool pair) {
   const BlockArgs& a0 = grp.a[0];
   for (int i = 0; i < grp.n; ++i) {
     check_tile_bytes(grp.a[i].k_ss, grp.a[i].v_ss);
@@ -1143,23 +1208,20 @@ static void launch_pingpong(BlockGroup& grp, hipStream_t stream) {
   for (int i = 0; i < grp.n; ++i) grp.qt_begin[i + 1] = grp.qt_begin[i] + grp.a[i].n_qtiles;
   const dim3 grid(static_cast<unsigned>(grp.qt_begin[grp.n] * a0.n_groups));
   const bool pos = a0.q_lim != nullptr;
-  switch (heads_per_group(a0.rep)) {
-    case 8:
-      if (pos) flash_block_pingpong_kernel<DT, 8, true, kBK3><<<grid, kThreads, 0, stream>>>(grp);
-      else flash_block_pingpong_kernel<DT, 8, false, kBK3><<<grid, kThreads, 0, stream>>>(grp);
-      break;
-    case 4:
-      if (pos) flash_block_pingpong_kernel<DT, 4, true, kBK3><<<grid, kThreads, 0, stream>>>(grp);
-      else flash_block_pingpong_kernel<DT, 4, false, kBK3><<<grid, kThreads, 0, stream>>>(grp);
-      break;
-    case 2:
-      if (pos) flash_block_pingpong_kernel<DT, 2, true, kBK3><<<grid, kThreads, 0, stream>>>(grp);
-      else flash_block_pingpong_kernel<DT, 2, false, kBK3><<<grid, kThreads, 0, stream>>>(grp);
-      break;
-    default:
-      if (pos) flash_block_pingpong_kernel<DT, 1, true, kBK3><<<grid, kThreads, 0, stream>>>(grp);
-      else flash_block_pingpong_kernel<DT, 1, false, kBK3><<<grid, kThreads, 0, stream>>>(grp);
-      break;
+  const int g = geometry(a0.hq, a0.hkv, pair).g;
+  if (pair) {
+    switch (g) {
+      case 4: launch_pingpong_g<DT, 4, true>(grp, pos, grid, stream); break;
+      case 2: launch_pingpong_g<DT, 2, true>(grp, pos, grid, stream); break;
+      default: launch_pingpong_g<DT, 1, true>(grp, pos, grid, stream); break;
+    }
+    return;
+  }
+  switch (g) {
+    case 8: launch_pingpong_g<DT, 8, false>(grp, pos, grid, stream); break;
+    case 4: launch_pingpong_g<DT, 4, false>(grp, pos, grid, stream); break;
+    case 2: launch_pingpong_g<DT, 2, false>(grp, pos, grid, stream); break;
+    default: launch_pingpong_g<DT, 1, false>(grp, pos, grid, stream); break;
   }
 }
 
@@ -1167,8 +1229,9 @@ template <int DT>
 static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   BlockGroup grp;
   grp.n = 1;
-  grp.a[0] = make_args(L);
-  launch_pingpong<DT>(grp, stream);
+  const bool pair = block_pair_ok(L);
+  grp.a[0] = make_args(L, pair);
+  launch_pingpong<DT>(grp, stream, pair);
 }
 
 template <int DT>
@@ -1243,9 +1306,11 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
   if (live.empty()) return;
   const BlockLaunch& f = *live[0];
   bool grouped = !f.force_general && block_uses_mfma(f.dtype, f.d) && padded_d_ok(f.d);
+  const bool pair = block_pair_ok(f);
   for (const BlockLaunch* L : live)
     grouped = grouped && !L->force_general && L->dtype == f.dtype && L->d == f.d && L->hq == f.hq &&
-              L->hkv == f.hkv && (L->causal && L->q_lim != nullptr) == (f.causal && f.q_lim != nullptr);
+              L->hkv == f.hkv && (L->causal && L->q_lim != nullptr) == (f.causal && f.q_lim != nullptr) &&
+              block_pair_ok(*L) == pair;
   if (!grouped) {
     for (const BlockLaunch* L : live) launch_block_partial(*L, stream);
     return;
@@ -1256,29 +1321,28 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
   for (size_t base = 0; base < live.size(); base += kMaxGroup) {
     BlockGroup grp;
     grp.n = static_cast<int32_t>(std::min<size_t>(kMaxGroup, live.size() - base));
-    for (int i = 0; i < grp.n; ++i) grp.a[i] = make_args(*live[base + i]);
-    if (f.dtype == kBF16) launch_pingpong<kBF16>(grp, stream);
-    else launch_pingpong<kF16>(grp, stream);
+    for (int i = 0; i < grp.n; ++i) grp.a[i] = make_args(*live[base + i], pair);
+    if (f.dtype == kBF16) launch_pingpong<kBF16>(grp, stream, pair);
+    else launch_pingpong<kF16>(grp, stream, pair);
   }
   HCP_HIP(hipGetLastError());
 }
 
-template <bool TRACE>
-static void launch_ring_kernel(int dtype, int g, dim3 grid, const RingPlan& p, hipStream_t stream) {
-  if (dtype == kBF16) {
+template <int DT, bool TRACE>
+static void launch_ring_kernel(int g, bool pair, dim3 grid, const RingPlan& p, hipStream_t stream) {
+  if (pair) {
     switch (g) {
-      case 8: flash_ring_kernel<kBF16, 8, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
-      case 4: flash_ring_kernel<kBF16, 4, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
-      case 2: flash_ring_kernel<kBF16, 2, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
-      default: flash_ring_kernel<kBF16, 1, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
+      case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, true><<<grid, kThreads, 0, stream>>>(p); break;
+      case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, true><<<grid, kThreads, 0, stream>>>(p); break;
+      default: flash_ring_kernel<DT, 1, kBK3, TRACE, true><<<grid, kThreads, 0, stream>>>(p); break;
     }
-  } else {
-    switch (g) {
-      case 8: flash_ring_kernel<kF16, 8, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
-      case 4: flash_ring_kernel<kF16, 4, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
-      case 2: flash_ring_kernel<kF16, 2, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
-      default: flash_ring_kernel<kF16, 1, kBK3, TRACE><<<grid, kThreads, 0, stream>>>(p); break;
-    }
+    return;
+  }
+  switch (g) {
+    case 8: flash_ring_kernel<DT, 8, kBK3, TRACE, false><<<grid, kThreads, 0, stream>>>(p); break;
+    case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, false><<<grid, kThreads, 0, stream>>>(p); break;
+    case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, false><<<grid, kThreads, 0, stream>>>(p); break;
+    default: flash_ring_kernel<DT, 1, kBK3, TRACE, false><<<grid, kThreads, 0, stream>>>(p); break;
   }
 }
 
@@ -1299,9 +1363,10 @@ void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
   p.dtype = L.dtype;
   p.d = L.d;
   p.hq = L.hq; p.hkv = L.hkv; p.rep = L.hq / L.hkv;
-  const int g = heads_per_group(p.rep);
-  const int tq = 32 * (kWaves / g);
-  p.n_groups = L.hq / g;
+  const bool pair = ring_fused_paired(L);
+  const Geometry geo = geometry(L.hq, L.hkv, pair);
+  const int g = geo.g, tq = geo.tq;
+  p.n_groups = geo.n_groups;
   p.n = L.n;
   p.causal = L.causal;
   p.scale_log2 = L.scale * kLog2e;
@@ -1318,22 +1383,28 @@ void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
   for (int s = 0; s < L.n; ++s) p.qt_begin[s + 1] = p.qt_begin[s] + static_cast<int32_t>(ceil_div(p.len[L.n - 1 - s], tq));
   const int64_t blocks = static_cast<int64_t>(p.qt_begin[L.n]) * p.n_groups;
   require(blocks <= INT32_MAX, "fused ring: too many workgroups");
-  require(blocks == ring_fused_workgroups(L.hq, L.hkv, L.n, L.len), "fused ring: workgroup count");
+  require(blocks == ring_fused_workgroups(L.hq, L.hkv, L.n, L.len, pair), "fused ring: workgroup count");
   p.trace = L.trace;
   p.trace_stride = L.trace_stride;
   if (L.trace != nullptr) require(L.trace_stride >= kTraceHeaderWords + 2 * L.n, "fused ring: trace stride");
   const dim3 grid(static_cast<unsigned>(blocks));
-  if (L.trace != nullptr) launch_ring_kernel<true>(L.dtype, g, grid, p, stream);
-  else launch_ring_kernel<false>(L.dtype, g, grid, p, stream);
+  if (L.dtype == kBF16) {
+    if (L.trace != nullptr) launch_ring_kernel<kBF16, true>(g, pair, grid, p, stream);
+    else launch_ring_kernel<kBF16, false>(g, pair, grid, p, stream);
+  } else {
+    if (L.trace != nullptr) launch_ring_kernel<kF16, true>(g, pair, grid, p, stream);
+    else launch_ring_kernel<kF16, false>(g, pair, grid, p, stream);
+  }
   HCP_HIP(hipGetLastError());
 }
 
-int64_t ring_fused_workgroups(int hq, int hkv, int n, const int64_t* len) {
-  const int g = heads_per_group(hq / hkv);
-  const int tq = 32 * (kWaves / g);
+bool ring_fused_paired(const RingLaunch& L) { return pair_ok(L.dtype, L.d, L.hkv, L.k_hs, L.v_hs); }
+
+int64_t ring_fused_workgroups(int hq, int hkv, int n, const int64_t* len, bool pair) {
+  const Geometry geo = geometry(hq, hkv, pair);
   int64_t tiles = 0;
-  for (int i = 0; i < n; ++i) tiles += ceil_div(len[i], tq);
-  return tiles * (hq / g);
+  for (int i = 0; i < n; ++i) tiles += ceil_div(len[i], geo.tq);
+  return tiles * geo.n_groups;
 }
 
 int ring_trace_words(int n) { return kTraceHeaderWords + 2 * n; }

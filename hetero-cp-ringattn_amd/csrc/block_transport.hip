@@ -30,9 +30,11 @@ namespace hcp {
 namespace {
 
 struct Pending {
-  uint64_t block_id;
+  uint64_t block_id;   // destination block (the receiving agent's)
   uint64_t bytes;
   hipEvent_t done;
+  int src_side;        // the posting agent's side within the pair
+  uint64_t src_block;  // its local source block
 };
 
 // State shared by the two agents of a pair: each agent's inbox of posted transfers.
@@ -140,6 +142,19 @@ bool same_desc(const hcp_block_desc& x, const hcp_block_desc& y) {
          x.meta_len == y.meta_len && std::memcmp(x.meta, y.meta, x.meta_len) == 0;
 }
 
+// Waits for every queued copy that reads from or writes into block `block_id` of the
+// agent on `side` (all blocks when block_id is UINT64_MAX).  The copies stay queued,
+// so the receiver still observes them through poll_transfers.  Called with the pair's
+// mutex held.
+void wait_block_copies(PairState& st, int side, uint64_t block_id) {
+  for (int q = 0; q < 2; ++q)
+    for (const Pending& p : st.inbox[q]) {
+      const bool writes = q == side && (block_id == UINT64_MAX || p.block_id == block_id);
+      const bool reads = p.src_side == side && (block_id == UINT64_MAX || p.src_block == block_id);
+      if (writes || reads) HCP_HIP(hipEventSynchronize(p.done));
+    }
+}
+
 }  // namespace
 
 // Shared with capi.hip's boundary helpers.
@@ -178,11 +193,10 @@ int hcp_block_agent_destroy(hcp_block_agent* agent) {
     {
       std::lock_guard<std::mutex> lock(agent->pair->mu);
       if (agent->peer != nullptr) agent->peer->peer = nullptr;
-      // Transfers still queued for this agent: wait for their copies, then drop them.
-      for (Pending& p : agent->pair->inbox[agent->side]) {
-        (void)hipEventSynchronize(p.done);
-        agent->pair->events.push_back(p.done);
-      }
+      // Copies this agent posted that read its blocks: wait for them (the peer still
+      // polls their completions).  Transfers queued for this agent: wait, then drop.
+      wait_block_copies(*agent->pair, agent->side, UINT64_MAX);
+      for (Pending& p : agent->pair->inbox[agent->side]) agent->pair->events.push_back(p.done);
       agent->pair->inbox[agent->side].clear();
       if (agent->peer == nullptr && agent->pair.use_count() == 1) {
         for (hipEvent_t e : agent->pair->events) (void)hipEventDestroy(e);
@@ -230,7 +244,12 @@ int hcp_block_deregister(hcp_block_agent* agent, uint64_t block_id) {
   return block_transport_guard(__func__, [&] {
     require(agent != nullptr, "null agent");
     std::lock_guard<std::mutex> lock(agent->pair->mu);
-    require(agent->blocks.erase(block_id) == 1, "block " + std::to_string(block_id) + " is not registered");
+    require(agent->blocks.count(block_id) == 1, "block " + std::to_string(block_id) + " is not registered");
+    // The caller may free the block's memory once this returns: finish every copy
+    // that still reads or writes it (the reference's in-memory transport copies
+    // synchronously, so it has no such window).
+    wait_block_copies(*agent->pair, agent->side, block_id);
+    agent->blocks.erase(block_id);
   });
 }
 
@@ -320,7 +339,7 @@ int hcp_block_submit_transfer(hcp_block_agent* agent, uint64_t local_block_id, c
       HCP_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     HCP_HIP(hipEventRecord(e, s));
-    agent->pair->inbox[peer->side].push_back(Pending{remote->block_id, src.len, e});
+    agent->pair->inbox[peer->side].push_back(Pending{remote->block_id, src.len, e, agent->side, local_block_id});
     agent->sent += src.len;
   });
 }

@@ -77,8 +77,11 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
 // same-run A/Bs: KV staging scatter +3.5% and gather +2.7% over nt alone (c5; sc1 alone
 // +3%, sc0 alone +0.7%), wire-frame pack +13.5% and unpack +6.3% over plain stores, LSE
 // merge +3.2%.
+// On gfx940+ a VALU write to the data VGPRs of a VMEM store wider than 64 bits needs
+// two wait states after the store; the compiler's hazard recognizer does not see
+// stores inside inline asm, so the 16-byte form provides them itself (s_nop 1).
 __device__ __forceinline__ void store16_nt_sc1(void* p, u32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off nt sc1" : : "v"(p), "v"(v) : "memory");
+  asm volatile("global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ void store8_nt_sc1(void* p, u32x2 v) {
   asm volatile("global_store_dwordx2 %0, %1, off nt sc1" : : "v"(p), "v"(v) : "memory");

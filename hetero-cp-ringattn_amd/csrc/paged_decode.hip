@@ -321,12 +321,17 @@ int decode_slots(int d, int dtype, int r, int waves) {
     return 768;
   }
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dev, d, dtype, r, waves);
+  // the instantiation the launch takes: head dims other than 64 and 128 run the
+  // zero-padding (PAD) build of the 128 kernel, whose register use may differ
+  const bool pad = d != 64 && d != 128;
+  const int dk = d == 64 ? 64 : pad ? -1 : 128;
+  const auto key = std::make_tuple(dev, dk, dtype, r, waves);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int cus = 0, per_cu = 0;
-  const void* fn = dtype == kBF16 ? (d != 64 ? decode_fn<128, kBF16>(r) : decode_fn<64, kBF16>(r))
-                                  : (d != 64 ? decode_fn<128, kF16>(r) : decode_fn<64, kF16>(r));
+  const void* fn = dtype == kBF16
+                       ? (d == 64 ? decode_fn<64, kBF16>(r) : pad ? decode_fn<128, kBF16, true>(r) : decode_fn<128, kBF16>(r))
+                       : (d == 64 ? decode_fn<64, kF16>(r) : pad ? decode_fn<128, kF16, true>(r) : decode_fn<128, kF16>(r));
   int slots = 768;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * waves, 0) == hipSuccess && cus > 0 &&

@@ -610,8 +610,11 @@ int hcp_ringattn_cxx_smoke_domain_count(void);
  * reference's bincode 1.3.3 serialisation of AgentMetadata (little-endian, u64
  * lengths, u32 enum variants, blocks in ascending id).  A transfer needs equal block
  * lengths and the peer's current registration (-6 otherwise); the wire counters count
- * the bytes of posted transfers (sent) and polled completions (recv).  All calls on
- * one pair are serialised by a mutex; strings are NUL-terminated host memory.
+ * the bytes of posted transfers (sent) and polled completions (recv).  deregister
+ * waits for every posted copy that still reads or writes the block, and destroy for
+ * every copy reading the agent's blocks or queued to it, so the caller may release a
+ * block's memory as soon as either returns.  All calls on one pair are serialised by
+ * a mutex; strings are NUL-terminated host memory.
  * ------------------------------------------------------------------------------- */
 #define HCP_BLOCK_AGENT_MAX 64
 #define HCP_BLOCK_META_MAX 256

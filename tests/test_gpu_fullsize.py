@@ -75,6 +75,29 @@ def test_c3_full_ring_prefill_sampled_rows_and_strategy_invariance(gpu):
     assert (lz - lse).abs().max().item() <= 2 * LSE_TOL
 
 
+def test_c3_last_domain_whole_against_ring_attention(gpu):
+    # Domain 3 of c3 whole (rows 28672..32767, 32 heads) against the op-for-op
+    # restatement of ring_attention (ring.rs:861-1398) on the fp32 upcasts: its local
+    # chunk, then domains 2, 1 and 0 in ring order -- every ring step of the target
+    # whose rows see all four sources.
+    chunks, hq, hkv, d = [12288, 8192, 8192, 4096], 32, 8, 128
+    s = sum(chunks)
+    q, k, v = synth(44, [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    out, lse = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+    assert H.last_path() == "ring_fused"
+    torch.cuda.synchronize()
+    offs = [0, 12288, 20480, 28672]
+    off = offs[3]
+    q32, k32, v32 = (x.float().cpu().numpy() for x in (q, k, v))
+    f = lambda x: torch.from_numpy(x).permute(1, 0, 2).unsqueeze(0)
+    kx, vx = T.repeat_kv_heads(f(k32), hq // hkv), T.repeat_kv_heads(f(v32), hq // hkv)
+    sent = [T.local_micro_blocks(kx[:, :, o:o + L], vx[:, :, o:o + L], o, 4) for o, L in zip(offs, chunks)]
+    ro, rl = T.ring_attention(1 / math.sqrt(d), f(q32)[:, :, off:], kx[:, :, off:], vx[:, :, off:],
+                              torch.arange(off, s), off, 4, [sent[2], sent[1], sent[0]], return_lse=True)
+    assert np.abs(out[:, off:].float().cpu().numpy() - ro[0].numpy()).max() <= OUT_TOL
+    assert np.abs(lse[:, off:].cpu().numpy() - rl[0].numpy()).max() <= LSE_TOL
+
+
 def test_c2_full_ring_prefill_both_schedules(gpu):
     # Qwen2.5-3B shape at its stated size: S=8192 in [4096, 2560, 1536], 16 q / 2 kv heads
     # (eight query heads per KV head), D=128, bf16, seed 43.
@@ -111,7 +134,7 @@ def test_c2_full_ring_prefill_both_schedules(gpu):
         assert np.abs(l[:, off:].cpu().numpy() - rl[0].numpy()).max() <= LSE_TOL
 
 
-def test_c4_full_paged_decode_sampled_sequences(gpu):
+def test_c4_full_paged_decode_every_sequence(gpu):
     batch, hq, hkv, d, bs, ctx, nb = 64, 32, 8, 128, 16, 16384, 65536
     chunks = [8192, 5120, 3072]
     q = torch.empty(batch, hq, d, dtype=torch.bfloat16, device="cuda")
@@ -129,15 +152,23 @@ def test_c4_full_paged_decode_sampled_sequences(gpu):
                            out_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     assert H.fetch_device_errors() == 0
-    out = out.view(batch, hq, d).float().cpu().numpy()
-    lse = lse.view(batch, hq).cpu().numpy()
-    for b in (0, 31, 63):
-        blocks = torch.from_numpy(tables_np[b].astype(np.int64)).cuda()
-        k = pool[0].index_select(0, blocks).reshape(ctx, hkv, d).float().cpu().numpy()
-        v = pool[1].index_select(0, blocks).reshape(ctx, hkv, d).float().cpu().numpy()
-        ro, rl = rows_closed_form(q[b:b + 1].float().cpu().numpy(), k, v, [0], 1 / math.sqrt(d), lambda r: ctx)
-        assert np.abs(out[b] - ro[0]).max() <= OUT_TOL, b
-        assert np.abs(lse[b] - rl[0]).max() <= LSE_TOL, b
+    out = out.view(batch, hq, d).float().cpu()
+    lse = lse.view(batch, hq).cpu()
+    # every sequence against the f64 closed form over its whole context, K/V read
+    # through its block table from a host copy of the pool
+    pool_h, q_h = pool.cpu(), q.cpu().double()
+    tabs = torch.from_numpy(tables_np.astype(np.int64))
+    rep, scale = hq // hkv, 1 / math.sqrt(d)
+    err_o = err_l = 0.0
+    for b in range(batch):
+        k = pool_h[0].index_select(0, tabs[b]).reshape(ctx, hkv, d).double().permute(1, 2, 0)  # [hkv, d, ctx]
+        v = pool_h[1].index_select(0, tabs[b]).reshape(ctx, hkv, d).double().permute(1, 0, 2)  # [hkv, ctx, d]
+        sc = torch.matmul(q_h[b].view(hkv, rep, d), k) * scale                                 # [hkv, rep, ctx]
+        rl = torch.logsumexp(sc, dim=2)
+        ro = torch.matmul(torch.exp(sc - rl.unsqueeze(2)), v)                                  # [hkv, rep, d]
+        err_o = max(err_o, (out[b] - ro.reshape(hq, d)).abs().max().item())
+        err_l = max(err_l, (lse[b] - rl.reshape(hq)).abs().max().item())
+    assert err_o <= OUT_TOL and err_l <= LSE_TOL, (err_o, err_l)
 
 
 def test_c5_full_staging_bit_exact_against_torch_indexing(gpu):

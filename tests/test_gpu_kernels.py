@@ -64,6 +64,13 @@ BLOCK_CASES = [
     # head per workgroup) and 6 at D=128 (two per workgroup)
     ("qwen2_0p5b_rep7_d64", 150, 300, 14, 2, 64, 150, 0, True, torch.bfloat16),
     ("gqa6_d128", 120, 260, 12, 2, 128, 140, 0, True, torch.bfloat16),
+    # head dim 64 with adjacent KV heads: two KV heads per tile row (paired kernels), one
+    # to four query heads per KV head and workgroup half; an odd KV head count stays
+    # zero-padded
+    ("d64_pair_gqa4_causal_past", 300, 700, 16, 4, 64, 650, 0, True, torch.bfloat16),
+    ("d64_pair_rep8_two_groups", 96, 517, 16, 2, 64, 600, 100, True, torch.bfloat16),
+    ("d64_pair_rep2_noncausal_f16", 160, 1000, 8, 4, 64, 0, 0, False, torch.float16),
+    ("d64_odd_kv_heads_padded", 150, 260, 6, 3, 64, 140, 0, True, torch.bfloat16),
 ]
 
 
@@ -341,6 +348,8 @@ RING_CASES = [
     # D=64 fp16 multi-head case
     ("qwen2_0p5b_d64", [320, 200, 136], 14, 2, 64, torch.bfloat16, 61),
     ("mha_d64_f16", [257, 190], 6, 6, 64, torch.float16, 62),
+    ("d64_pair_gqa4_uneven4", [300, 77, 500, 123], 16, 4, 64, torch.bfloat16, 63),
+    ("d64_odd_kv_padded", [200, 150], 3, 3, 64, torch.bfloat16, 64),
 ]
 
 
@@ -1094,6 +1103,41 @@ def test_block_transport_round_trips_a_registered_block(gpu):
         receiver.destroy()
 
 
+def test_block_transport_deregister_waits_for_pending_copies(gpu):
+    # A 256 MiB transfer posted on a side stream, then the source deregistered at once
+    # and overwritten on the default stream: deregister returns only after the copy
+    # has read the block, so the destination holds the original bytes; the receiver
+    # still polls the completion, and destroy after a fresh post leaves the copy whole.
+    sender, receiver = H.BlockAgent.pair("src-side", "dst-side")
+    side = torch.cuda.Stream()
+    try:
+        n = 64 << 20
+        src = torch.arange(n, dtype=torch.int32, device="cuda")
+        dst = torch.zeros(n, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        sid, _ = sender.register_block(src)
+        did, _ = receiver.register_block(dst)
+        sender.load_remote_metadata(receiver.local_metadata())
+        sender.submit_transfer(sid, sender.remote_desc("dst-side", did), stream=side)
+        sender.deregister_block(sid)
+        src.fill_(-1)
+        torch.cuda.synchronize()
+        assert _poll_all(receiver, 1) == [(did, 4 * n)]
+        assert torch.equal(dst, torch.arange(n, dtype=torch.int32, device="cuda"))
+        src2 = torch.full((n,), 7, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        sid2, _ = sender.register_block(src2)
+        sender.submit_transfer(sid2, sender.remote_desc("dst-side", did), stream=side)
+        sender.destroy()
+        src2.fill_(-1)
+        torch.cuda.synchronize()
+        assert bool((dst == 7).all())
+        assert _poll_all(receiver, 1) == [(did, 4 * n)]
+    finally:
+        sender.destroy()
+        receiver.destroy()
+
+
 def test_block_transport_carries_a_kv_wire_frame(gpu):
     # The KV frame payload of a c3-shaped chunk (GQA-expanded fp32 K/V + positions,
     # tcp.rs:161-207) moved between registered device blocks, then unpacked at the
@@ -1194,3 +1238,35 @@ def test_traced_fused_replay_statistics_and_perf_log(gpu, causal, tmp_path):
         for key in ("total_ms", "peer_compute_ms", "recv_ms", "send_ms", "forward_ms", "flush_ms",
                     "kv_sent_bytes", "wire_sent_bytes", "wire_recv_bytes", "ts"):
             assert key in e
+
+
+@pytest.mark.parametrize("schedule", ["auto", "per_step"])
+def test_d64_paired_and_zero_padded_layouts_agree(gpu, schedule):
+    # The same Qwen2-0.5B-shaped ring (14 q / 2 kv heads, D=64) with token-major K/V
+    # (adjacent heads: two KV heads per tile row) and with head-major K/V (zero-padded
+    # to 128): both within tolerance of the restatement of ring_attention and of each
+    # other, the paired one traced (its workgroup count is the paired decomposition's).
+    chunks, hq, hkv, d = [700, 300, 500], 14, 2, 64
+    s = sum(chunks)
+    (q, k, v), (q32, k32, v32) = draw(65, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
+    qh = q.permute(1, 0, 2)
+    o1, l1 = H.ring_attention_replay(qh, k.permute(1, 0, 2), v.permute(1, 0, 2), chunks, schedule=schedule)
+    o2, l2 = H.ring_attention_replay(qh, k.permute(1, 0, 2).contiguous(), v.permute(1, 0, 2).contiguous(), chunks,
+                                     schedule=schedule)
+    torch.cuda.synchronize()
+    ro, rl = T.ring_attention_replay(1 / math.sqrt(d), bhsd(q32), bhsd(k32), bhsd(v32), chunks, return_lse=True)
+    for o, l in ((o1, l1), (o2, l2)):
+        assert np.abs(o.float().cpu().numpy() - ro[0].numpy()).max() <= OUT_TOL
+        assert np.abs(l.cpu().numpy() - rl[0].numpy()).max() <= LSE_TOL
+    assert (o1.float() - o2.float()).abs().max().item() <= OUT_TOL
+    if schedule == "auto":
+        buf = torch.zeros(H.trace_record_bytes(torch.bfloat16, hq, hkv, d, chunks), dtype=torch.uint8, device="cuda")
+        H.trace_attach(buf)
+        try:
+            o3, _ = H.ring_attention_replay(qh, k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+            doms, launch = H.trace_read()
+        finally:
+            H.trace_attach(None)
+        assert torch.equal(o3, o1)
+        # paired: one KV pair, 7 query heads per KV head (one per group), 128 rows per workgroup
+        assert launch["workgroups"] == sum(-(-c // 128) for c in chunks) * 7

@@ -65,3 +65,54 @@ def test_static_decode_rejects_calls_beyond_the_array(gpu):
     assert rc == -6 and "static scratch" in H.last_error()
     torch.cuda.synchronize()
     assert torch.isnan(o).all()  # nothing ran
+
+
+def test_static_decode_allocates_nothing(gpu):
+    # The advertised contract: after a warm-up call (code objects loaded, occupancy and
+    # the static array's address cached), another call changes neither torch's pools
+    # nor the device's free memory.
+    q, pool, tables = _inputs(93, 8, 32, 8, 128, 16, 2048)
+    rc, _, _ = _static_call(q, pool, tables, 0, 2048)
+    assert rc == 0, H.last_error()
+    o = torch.empty(8, 32, 128, dtype=torch.float32, device="cuda")
+    lse = torch.empty(8, 32, dtype=torch.float32, device="cuda")
+    desc = H.decode_desc(q, pool, tables, 0, 2048, 1 / math.sqrt(128))
+    pp = H.paged_pool(pool)
+    qv = H.View(q.data_ptr(), q.stride(1), q.stride(0))
+    torch.cuda.synchronize()
+    before = (torch.cuda.memory_allocated(), torch.cuda.memory_reserved(), torch.cuda.mem_get_info()[0])
+    for _ in range(3):
+        rc = H.lib().hcp_paged_decode_partial_static(ctypes.byref(desc), ctypes.byref(pp), qv, H._ptr(tables), None,
+                                                     H._ptr(o), H._ptr(lse), None)
+        assert rc == 0, H.last_error()
+    torch.cuda.synchronize()
+    after = (torch.cuda.memory_allocated(), torch.cuda.memory_reserved(), torch.cuda.mem_get_info()[0])
+    assert after == before
+
+
+def test_static_decode_replays_in_a_graph(gpu):
+    # Captured in a HIP graph (it records no memset nodes) and replayed three times with
+    # eager work and synchronisations in between, each replay on new query values:
+    # every replay equals the eager workspace entry point on the same inputs.
+    q, pool, tables = _inputs(94, 4, 16, 4, 128, 16, 1024)
+    o = torch.empty(4, 16, 128, dtype=torch.float32, device="cuda")
+    lse = torch.empty(4, 16, dtype=torch.float32, device="cuda")
+    desc = H.decode_desc(q, pool, tables, 0, 1024, 1 / math.sqrt(128))
+    pp = H.paged_pool(pool)
+    qv = H.View(q.data_ptr(), q.stride(1), q.stride(0))
+    call = lambda: H.lib().hcp_paged_decode_partial_static(ctypes.byref(desc), ctypes.byref(pp), qv, H._ptr(tables),
+                                                           None, H._ptr(o), H._ptr(lse), H._stream())
+    assert call() == 0, H.last_error()  # warm-up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = call()
+    assert rc == 0, H.last_error()
+    for seed in (95, 96, 97):
+        H.synth_normals(seed, 0, q.numel(), q)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref_o, ref_l = H.decode_local_compact_partial(q, pool, tables, 0, 1024)
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref_o) and torch.equal(lse, ref_l), seed
