@@ -230,7 +230,10 @@ def bench_c2(H, torch, steps: int, warmup: int):
 def bench_qwen_d64(H, torch, steps: int, warmup: int):
     """32k 4-domain ring with Qwen2-0.5B heads (14 q / 2 kv, D=64), bf16, causal, fused
     schedule: K/V token-major (adjacent KV heads: paired head-dim-64 kernels), and the
-    same tensors head-major (KV heads apart: zero-padded to 128) in the same run."""
+    same tensors head-major (KV heads apart: zero-padded to 128) in the same run.
+
+    Not run: its first run ended with a GPU fault whose cause is not identified."""
+    raise RuntimeError("the head-dim-64 leg is disabled: its last run faulted the GPU (cause not identified)")
     c = QWEN64
     paired = bench_prefill(H, torch, steps, warmup, c)
     q, k, v = paired["tensors"]
@@ -659,11 +662,11 @@ def main():
     H = load_pkg()
     torch.cuda.set_device(0)
     log(f"device {torch.cuda.get_device_name(0)}")
-    if args.leg == "qwen64" and not args.trace:
+    if args.leg == "qwen64":
         print(json.dumps({"qwen2_0p5b_d64_32k": bench_qwen_d64(H, torch, args.steps, args.warmup)}), flush=True)
         return
     if args.leg is not None:
-        c = {"c2": C2, "c3": C3, "qwen64": QWEN64}[args.leg]
+        c = {"c2": C2, "c3": C3}[args.leg]
         r = bench_prefill(H, torch, args.steps, args.warmup, c)
         out = {"leg": args.leg, **prefill_summary(r)}
         if args.trace:
@@ -683,7 +686,6 @@ def main():
                                                        5))
         del per
         c2 = bench_c2(H, torch, args.steps, args.warmup)
-        qwen = bench_qwen_d64(H, torch, args.steps, args.warmup)
         dec = bench_decode(H, torch, args.steps, args.warmup)
         log(f"c4 decode {dec['gbs']:.1f} GB/s")
         stg = bench_staged(H, torch, args.steps, args.warmup)
@@ -717,7 +719,6 @@ def main():
                                  "sampled_max_abs_err_out": stg.get("sampled_err_out"),
                                  "sampled_max_abs_err_lse": stg.get("sampled_err_lse")},
             c2_prefill=c2,
-            qwen2_0p5b_d64_32k=qwen,
             c3_per_step=c3_per_step,
             lse_merge={"workload": "c3 ring partials of the 4 target domains (10 x [32, L, 128] fp32 + LSE) "
                                    "-> bf16 rows + fp32 LSE, one hcp_ring_lse_merge per domain",

@@ -1116,10 +1116,15 @@ static int heads_per_group(int rep) {
 
 // Head dim 64 with adjacent KV heads (head stride = 64 elements, as in the token-major
 // [S, Hkv, 64] projection output) and an even KV head count: the paired
-// instantiations, which fold two KV heads per 128-dim tile row instead of zero-padding
-// one head to 128.  Other head-dim-64 layouts (head-major, odd Hkv) stay zero-padded.
+// instantiations fold two KV heads per 128-dim tile row instead of zero-padding one
+// head to 128.  Switched off: a 32k run of the head-dim-64 benchmark leg (paired, then
+// zero-padded head-major) ended with a GPU fault whose cause is not identified (a host
+// model of every global access of both launches finds them in bounds), so head dim 64
+// takes the zero-padded kernels until that fault is explained.
+constexpr bool kPairedD64Enabled = false;
 static bool pair_ok(int dtype, int d, int hkv, int64_t k_hs, int64_t v_hs) {
-  return (dtype == kBF16 || dtype == kF16) && d == kD3 / 2 && hkv % 2 == 0 && k_hs == kD3 / 2 && v_hs == kD3 / 2;
+  return kPairedD64Enabled && (dtype == kBF16 || dtype == kF16) && d == kD3 / 2 && hkv % 2 == 0 &&
+         k_hs == kD3 / 2 && v_hs == kD3 / 2;
 }
 
 // Work decomposition of the matrix-core kernels: query heads per group (sharing a K/V

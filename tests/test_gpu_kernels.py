@@ -19,6 +19,9 @@ pytestmark = pytest.mark.gpu
 
 OUT_TOL = 2e-2
 LSE_TOL = 1e-3
+# The paired head-dim-64 kernels are switched off in the library (an unexplained GPU
+# fault in a 32k head-dim-64 run); their parity cases run the zero-padded kernels.
+PAIRED_D64 = False
 
 
 def dev_bits(bits: np.ndarray, dtype=torch.bfloat16):
@@ -1259,7 +1262,7 @@ def test_d64_paired_and_zero_padded_layouts_agree(gpu, schedule):
         assert np.abs(o.float().cpu().numpy() - ro[0].numpy()).max() <= OUT_TOL
         assert np.abs(l.cpu().numpy() - rl[0].numpy()).max() <= LSE_TOL
     assert (o1.float() - o2.float()).abs().max().item() <= OUT_TOL
-    if schedule == "auto":
+    if schedule == "auto" and PAIRED_D64:
         buf = torch.zeros(H.trace_record_bytes(torch.bfloat16, hq, hkv, d, chunks), dtype=torch.uint8, device="cuda")
         H.trace_attach(buf)
         try:
