@@ -171,7 +171,7 @@ def trace_summary(H, torch, c, tensors, launches: int):
     need = H.trace_record_bytes(torch.bfloat16, c["hq"], c["hkv"], c["d"], c["chunks"])
     buf = torch.zeros(need, dtype=torch.uint8, device="cuda")
     stride = 16 + 2 * n
-    durs, tiles, clocks, per_launch = [], [], [], []
+    durs, tiles, clocks, per_launch, home = [], [], [], [], []
     H.trace_attach(buf)
     try:
         for _ in range(launches):
@@ -186,6 +186,8 @@ def trace_summary(H, torch, c, tensors, launches: int):
             durs.append((t1 - t0).astype(np.float64) / 100.0)  # us (100 MHz ticks)
             tiles.append(rec[:, 12].astype(np.float64))
             clocks.append(100.0 * (c1 - c0).astype(np.float64) / (t1 - t0).astype(np.float64))
+            # record i is work item i; id mod 8 is the XCD whose L2 streams its head group
+            home.append(((rec[:, 9] & 15) % 8) == (np.arange(len(rec)) % 8))
     finally:
         H.trace_attach(None)
     dur, til, clk = np.concatenate(durs), np.concatenate(tiles), np.concatenate(clocks)
@@ -201,6 +203,7 @@ def trace_summary(H, torch, c, tensors, launches: int):
             "wg_us": {"min": round(float(dur.min()), 1), "mean": round(float(dur.mean()), 1),
                       "max": round(float(dur.max()), 1)},
             "key_tiles_per_wg": {"min": int(til.min()), "mean": round(float(til.mean()), 2), "max": int(til.max())},
+            "items_on_home_xcd": round(float(np.concatenate(home).mean()), 4),
             "clock_mhz": {"p10": round(float(np.percentile(clk, 10)), 1), "median": round(float(np.median(clk)), 1),
                           "p90": round(float(np.percentile(clk, 90)), 1)}}
 

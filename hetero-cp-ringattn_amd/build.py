@@ -48,7 +48,9 @@ def _compile(src: str) -> str:
 
 
 LLVM_BIN = os.environ.get("HCP_LLVM_BIN", "/opt/rocm/llvm/bin")
-M0_SEQ = re.compile(r"^s_mov_b32 m0, s\d+$")
+# the helper's scalar operand: any SGPR, including the named ones the allocator may
+# hand out under pressure (vcc_lo / vcc_hi)
+M0_SEQ = re.compile(r"^s_mov_b32 m0, (s\d+|vcc_lo|vcc_hi)$")
 # instructions that read or write M0 without naming it
 M0_IMPLICIT = re.compile(r"^(v_movrel|s_movrel|s_set_gpr_idx|s_sendmsg|ds_gws|ds_\w*addtid|v_interp|"
                          r"lds_param_load|lds_direct_load|global_load_lds|scratch_load_lds|s_ttracedata)")
