@@ -279,7 +279,9 @@ def block_launch_bytes(c):
 # ------------------------------------------------------------------ c3 merge ----
 def bench_strategies(H, torch, tensors, steps: int, warmup: int):
     """c3 ring prefill with Striped and ZigZag positions (strategy.rs:53-110): the same
-    causal FLOPs, rows in domain-major order, masks from the per-row key limits."""
+    causal FLOPs, rows in domain-major order.  "auto": K/V copied in position order,
+    then one positions-mode launch over the sequence (per-row key limits); "per_step":
+    one grouped launch per ring step with the running state in HBM."""
     c = C3
     seq = sum(c["chunks"])
     qh, kh, vh = (x.permute(1, 0, 2) for x in tensors)
@@ -287,23 +289,28 @@ def bench_strategies(H, torch, tensors, steps: int, warmup: int):
     lse = torch.empty(c["hq"], seq, dtype=torch.float32, device="cuda")
     res = {}
     for strat in ("striped", "zigzag"):
-        ws = torch.empty(H.replay_workspace_size(torch.bfloat16, c["hq"], c["hkv"], c["d"], c["chunks"],
-                                                 strategy=strat), dtype=torch.uint8, device="cuda")
-        step = lambda: H.ring_attention_replay(qh, kh, vh, c["chunks"], out=out, lse_out=lse, workspace=ws,
-                                               strategy=strat)
-        for _ in range(warmup):
-            step()
-        log(f"c3 prefill ({strat}) timed x{steps}")
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step()
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / steps
-        res[strat] = {"value": round(causal_flops(seq, c["hq"], c["d"]) / (ms * 1e-3) / 1e12, 1),
-                      "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
-                      "finite": bool(torch.isfinite(lse).all().item())}
-        del ws
+        for sched in ("auto", "per_step"):
+            ws = torch.empty(H.replay_workspace_size(torch.bfloat16, c["hq"], c["hkv"], c["d"], c["chunks"],
+                                                     strategy=strat, schedule=sched), dtype=torch.uint8,
+                             device="cuda")
+            step = lambda: H.ring_attention_replay(qh, kh, vh, c["chunks"], out=out, lse_out=lse, workspace=ws,
+                                                   strategy=strat, schedule=sched)
+            for _ in range(warmup):
+                step()
+            log(f"c3 prefill ({strat}, {sched}) timed x{steps}")
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3 / steps
+            r = {"value": round(causal_flops(seq, c["hq"], c["d"]) / (ms * 1e-3) / 1e12, 1),
+                 "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "finite": bool(torch.isfinite(lse).all().item())}
+            if sched == "auto":
+                res[strat] = r
+            else:
+                res[strat]["per_step"] = r
+            del ws
     return res
 
 
@@ -643,7 +650,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
-    ap.add_argument("--leg", choices=["c2", "c3", "qwen64"], default=None,
+    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "strategies"], default=None,
                     help="run one prefill leg alone and print its JSON object (profiling)")
     ap.add_argument("--trace", action="store_true",
                     help="with --leg: also run traced launches (per-workgroup records) and summarise them")
@@ -667,6 +674,11 @@ def main():
     log(f"device {torch.cuda.get_device_name(0)}")
     if args.leg == "qwen64":
         print(json.dumps({"qwen2_0p5b_d64_32k": bench_qwen_d64(H, torch, args.steps, args.warmup)}), flush=True)
+        return
+    if args.leg == "strategies":
+        tensors = synth_qkv(H, torch, sum(C3["chunks"]), C3["hq"], C3["hkv"], C3["d"], C3["seed"])
+        print(json.dumps({"leg": "strategies", **bench_strategies(H, torch, tensors, args.steps, args.warmup)}),
+              flush=True)
         return
     if args.leg is not None:
         c = {"c2": C2, "c3": C3}[args.leg]

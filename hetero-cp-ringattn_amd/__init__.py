@@ -612,7 +612,8 @@ def ring_attention_replay(q, k, v, chunks, causal=True, scale=None, out=None, ls
     Rows are in domain-major order (row r = position ``domain_positions(chunks,
     strategy)[r]``; the global order for "vanilla"); ``inverse_perm`` maps back.
     ``schedule``: "auto" (one fused launch where it applies), "per_step" (one grouped
-    launch per ring step) or "fused"."""
+    launch per ring step) or "fused".  Fused with "striped" / "zigzag" positions: K/V
+    copied in position order, then one positions-mode block over the whole sequence."""
     torch = _torch()
     hq, s, d = q.shape
     hkv = k.shape[0]
@@ -953,8 +954,8 @@ def trace_record_bytes(dtype, hq, hkv, d, chunks, causal=True) -> int:
 
 
 def trace_attach(buffer) -> None:
-    """Trace every later fused replay on this thread into ``buffer`` (a device tensor,
-    kept referenced by the caller); ``None`` detaches."""
+    """Trace every later fused replay with vanilla positions on this thread into
+    ``buffer`` (a device tensor, kept referenced by the caller); ``None`` detaches."""
     if buffer is None:
         _check(lib().hcp_ring_trace_attach(None, 0))
     else:

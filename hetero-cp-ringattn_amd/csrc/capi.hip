@@ -181,6 +181,11 @@ struct ReplayPlan {
   StrategySpec spec;
   int schedule = HCP_SCHEDULE_AUTO;
   size_t fused_stage_bytes = 0;           // fused paged replay: each of the K and V staging buffers [Hkv, S, D]
+  // Fused replay with explicit positions (after the paged staging): positions int64 [S],
+  // the key-order flag, the two (key, row) sort buffers, K / V in position order
+  // [Hkv, S, D] and the per-row key limits int32 [S].
+  size_t fp_pos = 0, fp_flag = 0, fp_key[2] = {0, 0}, fp_row[2] = {0, 0}, fp_kc = 0, fp_vc = 0, fp_lim = 0;
+  size_t fp_total = 0;
   bool positioned = false;                // causal with explicit positions (Striped / ZigZag)
   size_t pos_off = 0, lim_off = 0;        // workspace: positions int64 [S], key limits int32 [N, S]
   std::vector<int64_t> len, off, first, last;
@@ -303,9 +308,35 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
   // at the start of the workspace (the per-step layout's need covers it: its staging
   // alone holds N chunks of the longest length).
   p.fused_stage_bytes = align256(static_cast<size_t>(p.seq) * d->num_kv_heads * d->head_dim * es);
+  if (p.positioned) {
+    size_t c = paged ? 2 * p.fused_stage_bytes : 0;
+    const size_t n8 = align256(static_cast<size_t>(p.seq) * sizeof(int64_t));
+    const size_t n4 = align256(static_cast<size_t>(p.seq) * sizeof(int32_t));
+    p.fp_pos = c;
+    c += n8;
+    p.fp_flag = c;
+    c += 256;
+    for (int i = 0; i < 2; ++i) {
+      p.fp_key[i] = c;
+      c += n8;
+    }
+    for (int i = 0; i < 2; ++i) {
+      p.fp_row[i] = c;
+      c += n4;
+    }
+    p.fp_kc = c;
+    c += p.fused_stage_bytes;
+    p.fp_vc = c;
+    c += p.fused_stage_bytes;
+    p.fp_lim = c;
+    c += n4;
+    p.fp_total = c;
+  }
   if (d->schedule == HCP_SCHEDULE_FUSED) {
-    require(!p.positioned, "the fused schedule needs vanilla positions (or causal = 0)");
-    p.total = paged ? 2 * p.fused_stage_bytes : 0;
+    p.total = p.positioned ? p.fp_total : paged ? 2 * p.fused_stage_bytes : 0;
+  } else if (d->schedule == HCP_SCHEDULE_AUTO && p.positioned) {
+    // AUTO runs the fused layout where the views allow it, else the per-step one
+    p.total = std::max(p.total, p.fp_total);
   }
   return p;
 }
@@ -365,6 +396,83 @@ void run_replay_fused(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ri
   }
   timed(kTimedBlock, stream, [&] { launch_ring_fused(L, stream); });
   g_last_path = HCP_PATH_RING_FUSED;
+}
+
+// Whole replay with explicit positions (Striped / ZigZag) as one positions-mode launch
+// of the block kernel: attention over a set of keys does not depend on their order, so
+// with K / V put in position order every query row sees a prefix of the keys -- those
+// at positions up to its own (ring.rs:249-273 masks key by key) -- and the whole
+// sequence is one block of S query rows against S keys, its output rows and LSE written
+// directly, with no running state in HBM between ring steps.  q / k / v / out are the
+// whole-sequence views in domain-major order (rows [off_t, off_t + len_t) hold domain
+// t's tokens in ascending position order); k / v paged: the staged copies.
+void run_replay_fused_positioned(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ring_view q,
+                                 hcp_ring_view k, hcp_ring_view v, hcp_ring_view out, float* lse_out, char* base,
+                                 hipStream_t stream) {
+  const int es = elem_size(d->dtype);
+  int64_t* pos = reinterpret_cast<int64_t*>(base + p.fp_pos);
+  launch_domain_positions(p.spec, p.seq, pos, stream);
+  int* flag = reinterpret_cast<int*>(base + p.fp_flag);
+  int64_t* const keys[2] = {reinterpret_cast<int64_t*>(base + p.fp_key[0]),
+                            reinterpret_cast<int64_t*>(base + p.fp_key[1])};
+  int32_t* const rows[2] = {reinterpret_cast<int32_t*>(base + p.fp_row[0]),
+                            reinterpret_cast<int32_t*>(base + p.fp_row[1])};
+  launch_key_sort(pos, p.seq, flag, keys, rows, stream);
+  const int f = key_sort_passes(p.seq) % 2;
+  KvSortedGather g{};
+  g.flag = flag;
+  g.rows = rows[f];
+  g.n = p.seq;
+  g.hkv = d->num_kv_heads;
+  g.row_bytes = static_cast<int64_t>(d->head_dim) * es;
+  g.k = static_cast<const char*>(k.data);
+  g.v = static_cast<const char*>(v.data);
+  g.k_hs_bytes = k.head_stride * es;
+  g.k_ss_bytes = k.seq_stride * es;
+  g.v_hs_bytes = v.head_stride * es;
+  g.v_ss_bytes = v.seq_stride * es;
+  g.kc = base + p.fp_kc;
+  g.vc = base + p.fp_vc;
+  timed(kTimedGather, stream, [&] { launch_kv_sorted_gather(g, stream); });
+  KeyLimitArgs la{};
+  la.q_pos = pos;
+  la.n_q = p.seq;
+  la.k_pos = pos;
+  la.k_off[0] = 0;
+  la.k_len[0] = p.seq;
+  la.lim = reinterpret_cast<int32_t*>(base + p.fp_lim);
+  la.lim_stride = 0;
+  la.err = nullptr;  // the keys are read in sorted order whatever their order in the views
+  la.sel = flag;
+  la.k_pos_sorted = keys[f];
+  launch_key_limits(la, 1, p.seq, stream);
+  hcp_ring_block_desc bd;
+  bd.dtype = d->dtype;
+  bd.num_q_heads = d->num_q_heads;
+  bd.num_kv_heads = d->num_kv_heads;
+  bd.head_dim = d->head_dim;
+  bd.q_len = p.seq;
+  bd.kv_len = p.seq;
+  bd.q_offset = 0;
+  bd.kv_offset = 0;
+  bd.causal = 1;
+  bd.accumulate = 0;
+  bd.scale = d->scale;
+  BlockLaunch L = make_launch(&bd, q, k, v, nullptr, nullptr);
+  L.q_lim = la.lim;
+  L.kv_sel = flag;
+  L.k_alt = g.kc;
+  L.v_alt = g.vc;
+  L.alt_hs = p.seq * d->head_dim;
+  L.alt_ss = d->head_dim;
+  L.fin_out = out.data;
+  L.fin_dtype = d->dtype;
+  L.fin_hs = out.head_stride;
+  L.fin_ss = out.seq_stride;
+  L.fin_lse = lse_out;
+  L.fin_lse_hs = p.seq;
+  timed(kTimedBlock, stream, [&] { launch_block_partial(L, stream); });
+  g_last_path = block_path(L);
 }
 
 // Per-domain and per-launch statistics of the last traced replay (layout of the
@@ -482,11 +590,11 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
     check_view(k, "k", p.seq);
     check_view(v, "v", p.seq);
   }
-  // Fused schedule: one launch over every domain's ring (vanilla positions, BF16/F16,
-  // head_dim a multiple of 8 up to 128, 16-byte rows); AUTO takes it
-  // wherever it applies.
-  const bool fused_ok = !p.positioned && ring_fused_applies(d->dtype, d->head_dim) && mfma_layout_ok(q) &&
-                        mfma_layout_ok(out) && (paged || (mfma_layout_ok(k) && mfma_layout_ok(v)));
+  // Fused schedule: one matrix-core launch for the whole replay (BF16/F16, head_dim a
+  // multiple of 8 up to 128, 16-byte rows) -- the fused ring for vanilla positions, one
+  // positions-mode block over the sequence otherwise; AUTO takes it wherever it applies.
+  const bool fused_ok = ring_fused_applies(d->dtype, d->head_dim) && mfma_layout_ok(q) && mfma_layout_ok(out) &&
+                        (paged || (mfma_layout_ok(k) && mfma_layout_ok(v)));
   if (p.schedule == HCP_SCHEDULE_FUSED)
     require(fused_ok,
             "the fused schedule needs BF16/F16, head_dim a multiple of 8 up to 128 and 16-byte "
@@ -510,7 +618,8 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
                                 stream);
       });
     }
-    run_replay_fused(d, p, q, kk, vv, out, lse_out, stream);
+    if (p.positioned) run_replay_fused_positioned(d, p, q, kk, vv, out, lse_out, base, stream);
+    else run_replay_fused(d, p, q, kk, vv, out, lse_out, stream);
     return;
   }
   // Explicit positions: generate every domain's positions in HBM, then the key limits

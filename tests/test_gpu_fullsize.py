@@ -62,17 +62,20 @@ def test_c3_full_ring_prefill_sampled_rows_and_strategy_invariance(gpu):
     got_l = lse.cpu().numpy()[:, rows].T
     assert np.abs(got_o - ref_o).max() <= OUT_TOL
     assert np.abs(got_l - ref_l).max() <= LSE_TOL
-    # the same sequence under ZigZag positions (rows in domain-major order) agrees
+    # the same sequence under ZigZag and Striped positions (rows in domain-major order)
+    # agrees: the one-launch schedule AUTO takes, and ZigZag ring step by ring step
     from oracle import strategy as SP
-    a = SP.build_assignment(chunks, "zigzag")
-    order = torch.tensor(sum(SP.build_domain_positions(a), []), device="cuda")
-    inv = torch.tensor(SP.build_inverse_perm(a), device="cuda")
-    qz, kz, vz = (x.index_select(0, order).permute(1, 0, 2) for x in (q, k, v))
-    oz, lz = H.ring_attention_replay(qz, kz, vz, chunks, strategy="zigzag")
-    oz, lz = oz.index_select(1, inv), lz.index_select(1, inv)
-    torch.cuda.synchronize()
-    assert (oz.float() - out.float()).abs().max().item() <= 2 * OUT_TOL
-    assert (lz - lse).abs().max().item() <= 2 * LSE_TOL
+    for strategy, schedule in (("zigzag", "auto"), ("striped", "auto"), ("zigzag", "per_step")):
+        a = SP.build_assignment(chunks, strategy)
+        order = torch.tensor(sum(SP.build_domain_positions(a), []), device="cuda")
+        inv = torch.tensor(SP.build_inverse_perm(a), device="cuda")
+        qz, kz, vz = (x.index_select(0, order).permute(1, 0, 2) for x in (q, k, v))
+        oz, lz = H.ring_attention_replay(qz, kz, vz, chunks, strategy=strategy, schedule=schedule)
+        oz, lz = oz.index_select(1, inv), lz.index_select(1, inv)
+        torch.cuda.synchronize()
+        assert (oz.float() - out.float()).abs().max().item() <= 2 * OUT_TOL, (strategy, schedule)
+        assert (lz - lse).abs().max().item() <= 2 * LSE_TOL, (strategy, schedule)
+        del qz, kz, vz, oz, lz
 
 
 def test_c3_last_domain_whole_against_ring_attention(gpu):

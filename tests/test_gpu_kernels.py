@@ -464,9 +464,6 @@ def test_ring_replay_fused_rejects_what_it_cannot_run(gpu):
     s = sum(chunks)
     q = torch.zeros(8, s, d, dtype=torch.bfloat16, device="cuda")
     kv = torch.zeros(2, s, d, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(H.HcpRingError) as e:   # explicit positions
-        H.ring_attention_replay(q, kv, kv, chunks, strategy="zigzag", schedule="fused")
-    assert e.value.code == -6
     with pytest.raises(H.HcpRingError) as e:   # fp32
         H.ring_attention_replay(q.float(), kv.float(), kv.float(), chunks, schedule="fused")
     assert e.value.code == -6
@@ -757,9 +754,10 @@ STRATEGY_RING_CASES = [
 ]
 
 
+@pytest.mark.parametrize("schedule", ["auto", "per_step"])
 @pytest.mark.parametrize("strategy", ["striped", "zigzag"])
 @pytest.mark.parametrize("case", STRATEGY_RING_CASES, ids=[c[0] for c in STRATEGY_RING_CASES])
-def test_ring_replay_strategy_matches_full_attention(gpu, case, strategy):
+def test_ring_replay_strategy_matches_full_attention(gpu, case, strategy, schedule):
     name, chunks, hq, hkv, d, dt, seed = case
     s = sum(chunks)
     (q, k, v), (q32, k32, v32) = draw(seed, [(s, hq, d), (s, hkv, d), (s, hkv, d)], dt)
@@ -767,9 +765,19 @@ def test_ring_replay_strategy_matches_full_attention(gpu, case, strategy):
     rows = torch.tensor(sum(pos, []), device="cuda")
     # domain-major inputs: row r holds global position rows[r]
     qd, kd, vd = (x.index_select(0, rows).permute(1, 0, 2) for x in (q, k, v))
-    out, lse = H.ring_attention_replay(qd, kd, vd, chunks, strategy=strategy)
+    H.replay_timing(True)
+    H.replay_timing_read()
+    out, lse = H.ring_attention_replay(qd, kd, vd, chunks, strategy=strategy, schedule=schedule)
+    launches = H.replay_timing_read()["block"][1]
+    H.replay_timing(False)
     torch.cuda.synchronize()
     assert H.fetch_device_errors() == 0
+    # AUTO on the matrix cores: one positions-mode launch over the whole sequence against
+    # K / V in position order; per step (and fp32): launches per ring step
+    if schedule == "auto" and dt != torch.float32:
+        assert launches == 1, (name, launches)
+    else:
+        assert launches >= len(chunks), (name, launches)
     out = out.float().cpu().numpy()[:, inv]
     lse = lse.cpu().numpy()[:, inv]
     p = np.arange(s)
@@ -795,8 +803,12 @@ def test_ring_replay_paged_strategy_matches_unpaged(gpu):
     o1, l1 = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
                                      strategy="zigzag")
     o2, l2 = H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, chunks, strategy="zigzag")
+    # the fused schedule is what AUTO ran: the same single launch, bit for bit
+    o3, l3 = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
+                                     strategy="zigzag", schedule="fused")
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    assert torch.equal(o1, o3) and torch.equal(l1, l3)
 
 
 def _wire_cases():
