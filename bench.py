@@ -10,8 +10,8 @@ algorithmic FLOPs of causal pairs only: 2 GEMMs x 2 x D x Hq x S(S+1)/2.
 
 Also reported on the same line: paged decode GB/s (config c4), KV staging gather GB/s
 and the staged 128k prefill (config c5), the LSE merge GB/s, the c3 prefill with Striped
-and ZigZag positions, the KV wire-frame pack, the fused QKV + RoPE + KV append,
-a roofline object for the
+and ZigZag positions, the KV wire-frame pack, the fused QKV + RoPE + KV append, fp32 on
+the matrix cores (c1 and an 8k block), a roofline object for the
 dominant kernel (the flash block kernel, from HIP events recorded by the replay
 driver on its launch stream over the timed region) and the CPU baseline (the oracle's
 op-for-op libtorch restatement of ring.rs timed on this host on a bounded sample).
@@ -34,6 +34,7 @@ PKG_DIR = os.path.join(ROOT, "hetero-cp-ringattn_amd")
 METRIC = "ring-prefill TFLOP/s (% MFMA peak) at 32k; paged-decode GB/s (% HBM peak)"
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU (dense)
 PEAK_HBM_GBS = 8000.0
+PEAK_FP32_MFMA_TFLOPS = 157.3  # dense fp32 on the matrix cores
 
 C2 = dict(name="c2", chunks=[4096, 2560, 1536], hq=16, hkv=2, d=128, seed=43)
 C3 = dict(name="c3", chunks=[12288, 8192, 8192, 4096], hq=32, hkv=8, d=128, seed=44)
@@ -311,6 +312,55 @@ def bench_strategies(H, torch, tensors, steps: int, warmup: int):
             else:
                 res[strat]["per_step"] = r
             del ws
+    return res
+
+
+def bench_fp32(H, torch, steps: int, warmup: int):
+    """fp32, the reference's CPU dtype: c1 (seq 1024 in [640, 384], 8 heads, D=64,
+    causal) as a ring replay, and one causal 8192-token block (Llama-3-8B heads, 32 q /
+    8 kv, D=128) on the fp32 matrix-core kernel and on the scalar kernel (an output not
+    16-byte aligned sends it there), against the fp32 matrix-core peak."""
+    res = {}
+    chunks, hq, d = [640, 384], 8, 64
+    seq = sum(chunks)
+    g = torch.Generator(device="cuda").manual_seed(42)
+    q, k, v = (torch.randn(hq, seq, d, device="cuda", generator=g) for _ in range(3))
+    step = lambda: H.ring_attention_replay(q, k, v, chunks)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    res["c1_replay"] = {"ms_per_step": round(ms, 4), "path": H.last_path(),
+                        "value": round(causal_flops(seq, hq, d) / (ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s"}
+    lq, hq, hkv, d = 8192, 32, 8, 128
+    q = torch.randn(hq, lq, d, device="cuda", generator=g)
+    k, v = (torch.randn(hkv, lq, d, device="cuda", generator=g) for _ in range(2))
+    flops = causal_flops(lq, hq, d)
+    for aligned in (True, False):
+        buf = torch.empty(hq * lq * d + 4, dtype=torch.float32, device="cuda")
+        o = (buf[:hq * lq * d] if aligned else buf[1:1 + hq * lq * d]).view(hq, lq, d)
+        lse = torch.empty(hq, lq, dtype=torch.float32, device="cuda")
+        f = lambda: H.block_partial(q, k, v, 0, 0, o=o, lse=lse)
+        f()
+        torch.cuda.synchronize()
+        path = H.last_path()
+        n = max(steps // (1 if aligned else 5), 1)
+        log(f"fp32 8k block ({path}) timed x{n}")
+        t0 = time.perf_counter()
+        for _ in range(n):
+            f()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / n
+        tf = flops / (ms * 1e-3) / 1e12
+        res["block_8k_" + path] = {"ms": round(ms, 3), "value": round(tf, 2), "unit": "TFLOP/s",
+                                   "frac_fp32_mfma": round(tf / PEAK_FP32_MFMA_TFLOPS, 4)}
+        del buf, o, lse
+    res["workload"] = ("fp32: c1 ring replay; causal 8192-token block, 32 q / 8 kv heads, D=128, on the fp32 "
+                       "matrix-core kernel and the scalar kernel")
     return res
 
 
@@ -650,7 +700,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
-    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "strategies"], default=None,
+    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "strategies", "fp32"], default=None,
                     help="run one prefill leg alone and print its JSON object (profiling)")
     ap.add_argument("--trace", action="store_true",
                     help="with --leg: also run traced launches (per-workgroup records) and summarise them")
@@ -674,6 +724,9 @@ def main():
     log(f"device {torch.cuda.get_device_name(0)}")
     if args.leg == "qwen64":
         print(json.dumps({"qwen2_0p5b_d64_32k": bench_qwen_d64(H, torch, args.steps, args.warmup)}), flush=True)
+        return
+    if args.leg == "fp32":
+        print(json.dumps({"leg": "fp32", **bench_fp32(H, torch, args.steps, args.warmup)}), flush=True)
         return
     if args.leg == "strategies":
         tensors = synth_qkv(H, torch, sum(C3["chunks"]), C3["hq"], C3["hkv"], C3["d"], C3["seed"])
@@ -710,6 +763,8 @@ def main():
         log(f"wire {wire}")
         qkv = bench_qkv(H, torch, args.steps, args.warmup)
         log(f"qkv {qkv}")
+        f32 = bench_fp32(H, torch, args.steps, args.warmup)
+        log(f"fp32 {f32}")
         log(f"c3 strategies {strat}")
         log(f"c3 lse merge {mrg['merge_gbs']:.1f} GB/s")
         log(f"c5 gather {stg['gather_gbs']:.1f} GB/s, prefill {stg.get('prefill_tflops', 0):.1f} TFLOP/s")
@@ -742,6 +797,7 @@ def main():
             strategies=dict(workload="c3 ring prefill with Striped / ZigZag positions (same causal FLOPs)", **strat),
             kv_frame=wire,
             qkv_rope=qkv,
+            fp32=f32,
         )
     cpu = None
     if not args.no_cpu:

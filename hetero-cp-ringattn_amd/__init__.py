@@ -156,7 +156,7 @@ STRATEGIES = {"vanilla": 0, "striped": 1, "zigzag": 2}
 
 
 SCHEDULES = {"auto": 0, "per_step": 1, "fused": 2}
-PATHS = {0: "none", 1: "mfma", 2: "ring_fused", 3: "general"}
+PATHS = {0: "none", 1: "mfma", 2: "ring_fused", 3: "general", 4: "mfma_f32"}
 
 
 def schedule_code(schedule) -> int:

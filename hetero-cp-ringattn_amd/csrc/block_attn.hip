@@ -1103,6 +1103,244 @@ __global__ __launch_bounds__(kGenRows) void general_block_kernel(GenArgs a) {
 }
 
 // ----------------------------------------------------------------------------------
+// fp32 matrix-core kernel (v_mfma_f32_32x32x2f32): the reference's fp32 fold
+// (ring.rs:201-370, its CPU default and c1's dtype) with fp32 products on the matrix
+// cores.  A workgroup is 4 waves over 128 query rows of one head (32 rows a wave); K / V
+// tiles of 32 keys are staged in LDS as fp32, the next tile's loads in flight (in
+// registers) while the current one is folded.  Per tile a wave computes
+//   S^T (32 keys x 32 rows) = K Q^T  in DP/2 MFMAs, k-step s pairing dims (2s, 2s + 1)
+//                                    over the two lane halves;
+//   O^T (DP dims x 32 rows) += V^T P^T  in 16 MFMAs per 32 dims, k-step s pairing the
+//                                    keys a lane already holds as element s of S^T
+//                                    (8 (s / 4) + 4 half + s mod 4), so P needs no shuffle.
+// LDS layouts make each 16-byte read feed four k-steps: K rows hold the even dims, then
+// the odd ones ([key][half * DP/2 + s]); V is stored transposed ([dim][key]), where the
+// four keys of k-steps 4t .. 4t+3 of a lane half are adjacent.  Element i of a 32x32
+// accumulator holds row 8 (i / 4) + 4 half + (i mod 4), column lane mod 32 -- the
+// layout of the head-dim-128 kernel's O^T, whose epilogue indexing this one shares.
+// Masking, the online softmax (base 2, scale folded into the exponent), the running-
+// state merge (accumulate) and the final-row mode are those of general_block_kernel.
+// ----------------------------------------------------------------------------------
+constexpr int kF32Waves = 4;
+constexpr int kF32Threads = 64 * kF32Waves;
+constexpr int kF32Rows = 32 * kF32Waves;
+constexpr int kF32BK = 32;
+
+template <int DP>
+__global__ __launch_bounds__(kF32Threads) void mfma_f32_block_kernel(GenArgs a) {
+  static_assert(DP % 32 == 0 && DP <= 128, "padded head dim");
+  constexpr int DB = DP / 32;
+  constexpr int KS = DP / 2;
+  constexpr int KLS = DP + 4;          // K row stride (floats), 16-byte aligned
+  constexpr int VLS = kF32BK + 4;      // V^T row stride (floats), 16-byte aligned
+  constexpr int NV4 = kF32BK * DP / 4 / kF32Threads;  // float4 of K (and of V) per thread per tile
+  static_assert(NV4 >= 1 && kF32BK * DP % (4 * kF32Threads) == 0, "tile split");
+  __shared__ __attribute__((aligned(16))) float ks[kF32BK * KLS];
+  __shared__ __attribute__((aligned(16))) float vt[DP * VLS];
+  __shared__ int red[kF32Waves];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int lcol = lane & 31, half = lane >> 5;
+  const int head = blockIdx.y;
+  const int kvh = head / a.rep;
+  const int d = a.d;
+  if (a.q_lim != nullptr && a.kv_sel != nullptr && __builtin_amdgcn_readfirstlane(*a.kv_sel) != 0) {
+    a.k = a.k_alt; a.v = a.v_alt;
+    a.k_hs = a.v_hs = a.alt_hs;
+    a.k_ss = a.v_ss = a.alt_ss;
+  }
+  const float* kf = static_cast<const float*>(a.k) + kvh * a.k_hs;
+  const float* vf = static_cast<const float*>(a.v) + kvh * a.v_hs;
+  const int tq0 = blockIdx.x * kF32Rows;
+  const int row = tq0 + 32 * wave + lcol;
+  const bool live = row < a.lq;
+
+  // Q^T fragments: k-step s, this lane's row, dim 2s + half (zero past the head dim)
+  float qf[KS];
+  {
+    const float* qr = static_cast<const float*>(a.q) + head * a.q_hs + static_cast<int64_t>(row) * a.q_ss;
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2) qf[s2] = (live && 2 * s2 + half < d) ? qr[2 * s2 + half] : 0.f;
+  }
+  // Keys [0, row_lim) of the chunk are visible to this lane's row; n_kv bounds the tiles.
+  int64_t row_lim = a.lk;
+  int n_kv = a.lk;
+  if (a.causal) {
+    if (a.q_lim != nullptr) {
+      row_lim = live ? min(max(a.q_lim[row], 0), a.lk) : 0;
+      int hi = static_cast<int>(row_lim);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) hi = max(hi, __shfl_xor(hi, off));
+      if (lane == 0) red[wave] = hi;
+      __syncthreads();
+      hi = 0;
+#pragma unroll
+      for (int w = 0; w < kF32Waves; ++w) hi = max(hi, red[w]);
+      n_kv = hi;
+    } else {
+      row_lim = a.q_off + row + 1 - a.k_off;
+      const int last = min(a.lq, tq0 + kF32Rows) - 1;
+      const int64_t lim = a.q_off + last + 1 - a.k_off;
+      n_kv = static_cast<int>(lim <= 0 ? 0 : (lim < a.lk ? lim : a.lk));
+    }
+  }
+  row_lim = live ? min(row_lim, static_cast<int64_t>(a.lk)) : 0;
+  // the wave's last visible key + 1: tiles from there on are skipped by this wave
+  int wave_hi = static_cast<int>(max(row_lim, int64_t(0)));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) wave_hi = max(wave_hi, __shfl_xor(wave_hi, off));
+  wave_hi = __builtin_amdgcn_readfirstlane(wave_hi);
+
+  // Tile loads: float4 j of this thread is row e / (DP/4), dims 4 (e mod DP/4) .. +3 of
+  // the tile (e = tid + j * threads); zero past the chunk or the head dim.
+  float4 kr[NV4], vr[NV4];
+  auto load_tile = [&](int kv0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+      const int e = tid + j * kF32Threads;
+      const int r = e / (DP / 4), c4 = 4 * (e % (DP / 4));
+      const int kv = kv0 + r;
+      const bool in = kv < a.lk && c4 < d;
+      const float* kp = kf + static_cast<int64_t>(kv) * a.k_ss + c4;
+      const float* vp = vf + static_cast<int64_t>(kv) * a.v_ss + c4;
+      kr[j] = in ? make_float4(kp[0], kp[1], kp[2], kp[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      vr[j] = in ? make_float4(vp[0], vp[1], vp[2], vp[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto store_tile = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+      const int e = tid + j * kF32Threads;
+      const int r = e / (DP / 4), c4 = 4 * (e % (DP / 4));
+      // dims c4, c4 + 2 are even (k-steps c4 / 2, c4 / 2 + 1 of half 0), c4 + 1, c4 + 3 odd
+      *reinterpret_cast<float2*>(&ks[r * KLS + c4 / 2]) = make_float2(kr[j].x, kr[j].z);
+      *reinterpret_cast<float2*>(&ks[r * KLS + KS + c4 / 2]) = make_float2(kr[j].y, kr[j].w);
+      vt[(c4 + 0) * VLS + r] = vr[j].x;
+      vt[(c4 + 1) * VLS + r] = vr[j].y;
+      vt[(c4 + 2) * VLS + r] = vr[j].z;
+      vt[(c4 + 3) * VLS + r] = vr[j].w;
+    }
+  };
+
+  const float c = a.scale * kLog2e;
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  if (n_kv > 0) load_tile(0);
+  for (int kv0 = 0; kv0 < n_kv; kv0 += kF32BK) {
+    __syncthreads();  // the previous tile's reads are done
+    store_tile();
+    __syncthreads();
+    if (kv0 + kF32BK < n_kv) load_tile(kv0 + kF32BK);  // in flight while this tile is folded
+    if (kv0 >= wave_hi) continue;  // no key of this tile is visible to the wave's rows
+    // S^T in two accumulators (even / odd groups of four k-steps), summed after
+    f32x16 sa, sb;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sa[r] = sb[r] = 0.f;
+    const float* kl = &ks[lcol * KLS + half * KS];
+#pragma unroll
+    for (int u = 0; u < KS / 4; ++u) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kl + 4 * u);
+      f32x16& acc = (u & 1) ? sb : sa;
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.x, qf[4 * u + 0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.y, qf[4 * u + 1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.z, qf[4 * u + 2], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.w, qf[4 * u + 3], acc, 0, 0, 0);
+    }
+    // element i: key kv0 + 8 (i / 4) + 4 half + (i mod 4) of this lane's row
+    const int64_t vis = row_lim - kv0;  // keys of the tile visible to the row: [0, vis)
+    float p[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int j = 8 * (i >> 2) + 4 * half + (i & 3);
+      p[i] = j < vis ? (sa[i] + sb[i]) * c : -INFINITY;
+      mx = fmaxf(mx, p[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    // a row with no visible key so far keeps m = -inf, p = 0 and its (zero) state
+    const bool none = m_new == -INFINITY;
+    const float alpha = none ? 1.f : exp2f(m_run - m_new);
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      p[i] = none ? 0.f : exp2f(p[i] - m_new);
+      ls += p[i];
+    }
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+#pragma unroll
+    for (int b = 0; b < DB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
+    // O^T += V^T P^T: k-steps 4t .. 4t+3 take keys 8t + 4 half + 0..3, adjacent in V^T
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float4 v4[DB];
+#pragma unroll
+      for (int b = 0; b < DB; ++b)
+        v4[b] = *reinterpret_cast<const float4*>(&vt[(32 * b + lcol) * VLS + 8 * t + 4 * half]);
+#pragma unroll
+      for (int b = 0; b < DB; ++b) oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[b].x, p[4 * t + 0], oacc[b], 0, 0, 0);
+#pragma unroll
+      for (int b = 0; b < DB; ++b) oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[b].y, p[4 * t + 1], oacc[b], 0, 0, 0);
+#pragma unroll
+      for (int b = 0; b < DB; ++b) oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[b].z, p[4 * t + 2], oacc[b], 0, 0, 0);
+#pragma unroll
+      for (int b = 0; b < DB; ++b) oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[b].w, p[4 * t + 3], oacc[b], 0, 0, 0);
+    }
+  }
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (!live) return;
+  const bool any = l_tot > 0.f;
+  const float inv = any ? 1.f / l_tot : 0.f;
+  const float lse_new = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+  const int64_t orow = static_cast<int64_t>(head) * a.lq + row;
+  float c_old = 0.f, c_new = inv, lse_out = lse_new;
+  if (a.accumulate) {
+    const float lse_old = a.lse[orow];
+    const float mm = fmaxf(lse_old, lse_new);
+    const bool ok = mm != -INFINITY;
+    const float w_old = ok ? __expf(lse_old - mm) : 0.f;
+    const float w_new = ok ? __expf(lse_new - mm) : 0.f;
+    const float den = w_old + w_new;
+    const float rden = den > 0.f ? 1.f / den : 0.f;
+    c_old = w_old * rden;
+    c_new = w_new * rden * inv;
+    lse_out = ok ? mm + __logf(den) : -INFINITY;
+  }
+  const int64_t fin_row = head * a.fin_hs + static_cast<int64_t>(row) * a.fin_ss;
+#pragma unroll
+  for (int b = 0; b < DB; ++b)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int dcol = 32 * b + 8 * j + 4 * half;
+      if (dcol >= d) continue;  // head dims are multiples of 4: whole groups only
+      float x0 = c_new * oacc[b][4 * j], x1 = c_new * oacc[b][4 * j + 1];
+      float x2 = c_new * oacc[b][4 * j + 2], x3 = c_new * oacc[b][4 * j + 3];
+      if (a.accumulate) {
+        const float4 old = *reinterpret_cast<const float4*>(a.o + orow * d + dcol);
+        x0 += c_old * old.x; x1 += c_old * old.y; x2 += c_old * old.z; x3 += c_old * old.w;
+      }
+      if (a.fin_out) store4(a.fin_out, a.fin_dtype, fin_row + dcol, x0, x1, x2, x3);
+      else *reinterpret_cast<float4*>(a.o + orow * d + dcol) = make_float4(x0, x1, x2, x3);
+    }
+  if (half == 0) {
+    if (a.fin_out) {
+      if (a.fin_lse) a.fin_lse[head * a.fin_lse_hs + row] = lse_out;
+    } else {
+      a.lse[orow] = lse_out;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
 // Host launcher
 // ----------------------------------------------------------------------------------
 
@@ -1239,8 +1477,7 @@ static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   launch_pingpong<DT>(grp, stream, pair);
 }
 
-template <int DT>
-static void launch_general(const BlockLaunch& L, hipStream_t stream) {
+static GenArgs make_gen_args(const BlockLaunch& L) {
   GenArgs a;
   a.q = L.q; a.k = L.k; a.v = L.v;
   a.q_hs = L.q_hs; a.q_ss = L.q_ss; a.k_hs = L.k_hs; a.k_ss = L.k_ss; a.v_hs = L.v_hs; a.v_ss = L.v_ss;
@@ -1258,6 +1495,12 @@ static void launch_general(const BlockLaunch& L, hipStream_t stream) {
   a.v_alt = L.v_alt;
   a.alt_hs = L.alt_hs;
   a.alt_ss = L.alt_ss;
+  return a;
+}
+
+template <int DT>
+static void launch_general(const BlockLaunch& L, hipStream_t stream) {
+  const GenArgs a = make_gen_args(L);
   const dim3 grid(static_cast<unsigned>(ceil_div(L.lq, kGenRows)), static_cast<unsigned>(L.hq));
   if (L.d <= 64) general_block_kernel<DT, 64><<<grid, kGenRows, 0, stream>>>(a);
   else if (L.d <= 128) general_block_kernel<DT, 128><<<grid, kGenRows, 0, stream>>>(a);
@@ -1273,11 +1516,38 @@ static bool padded_d_ok(int d) { return d > 0 && d <= kD3 && d % 8 == 0; }
 // True when the matrix-core kernels handle this shape.
 bool block_uses_mfma(int dtype, int d) { return (dtype == kBF16 || dtype == kF16) && padded_d_ok(d); }
 
+// The fp32 matrix-core kernel: head dims that are multiples of 4 up to 128 (any view
+// layout: Q / K / V are read one element per lane), with the state and final rows it
+// writes four values at a time aligned for that (16-byte fp32, 8-byte 16-bit stores).
+bool block_uses_mfma_f32(const BlockLaunch& L) {
+  if (L.dtype != kF32 || L.d % 4 != 0 || L.d > kD3) return false;
+  auto aligned = [](const void* p, uintptr_t n) { return reinterpret_cast<uintptr_t>(p) % n == 0; };
+  if (L.fin_out != nullptr &&
+      (!aligned(L.fin_out, L.fin_dtype == kF32 ? 16 : 8) || L.fin_hs % 4 != 0 || L.fin_ss % 4 != 0))
+    return false;
+  if ((L.fin_out == nullptr || L.accumulate) && !aligned(L.o, 16)) return false;
+  return true;
+}
+
+static void launch_mfma_f32(const BlockLaunch& L, hipStream_t stream) {
+  const GenArgs a = make_gen_args(L);
+  const dim3 grid(static_cast<unsigned>(ceil_div(L.lq, kF32Rows)), static_cast<unsigned>(L.hq));
+  const dim3 block(kF32Threads);
+  switch ((L.d + 31) / 32) {
+    case 1: mfma_f32_block_kernel<32><<<grid, block, 0, stream>>>(a); break;
+    case 2: mfma_f32_block_kernel<64><<<grid, block, 0, stream>>>(a); break;
+    case 3: mfma_f32_block_kernel<96><<<grid, block, 0, stream>>>(a); break;
+    default: mfma_f32_block_kernel<128><<<grid, block, 0, stream>>>(a); break;
+  }
+}
+
 void launch_block_partial(const BlockLaunch& L, hipStream_t stream) {
   if (L.lq == 0) return;
   if (!L.force_general && block_uses_mfma(L.dtype, L.d)) {
     if (L.dtype == kBF16) launch_mfma<kBF16>(L, stream);
     else launch_mfma<kF16>(L, stream);
+  } else if (block_uses_mfma_f32(L)) {
+    launch_mfma_f32(L, stream);
   } else {
     switch (L.dtype) {
       case kF32: launch_general<kF32>(L, stream); break;

@@ -73,7 +73,8 @@ thread_local int g_last_path = HCP_PATH_NONE;
 
 // The kernel a block launch takes (see launch_block_partial / launch_block_group).
 int block_path(const BlockLaunch& L) {
-  return !L.force_general && block_uses_mfma(L.dtype, L.d) ? HCP_PATH_MFMA : HCP_PATH_GENERAL;
+  if (!L.force_general && block_uses_mfma(L.dtype, L.d)) return HCP_PATH_MFMA;
+  return block_uses_mfma_f32(L) ? HCP_PATH_MFMA_F32 : HCP_PATH_GENERAL;
 }
 
 int fail(int code, const std::string& msg) {

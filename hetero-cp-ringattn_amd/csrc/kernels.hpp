@@ -43,6 +43,8 @@ struct BlockLaunch {
 };
 
 bool block_uses_mfma(int dtype, int d);
+// Whether an fp32 block runs on the fp32 matrix-core kernel (else the scalar one).
+bool block_uses_mfma_f32(const BlockLaunch& L);
 void launch_block_partial(const BlockLaunch& L, hipStream_t stream);
 // Independent blocks (distinct outputs) in as few launches as the kernels allow: one
 // launch per up to 8 head-dim-128 MFMA blocks of the same head layout, else one each.

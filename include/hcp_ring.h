@@ -82,17 +82,20 @@ int hcp_ring_device_count(int* count);
 
 /*
  * Kernel path taken by the last successful attention call on this thread (block
- * partials, positioned partials, ring replays): lets a caller see that a view whose
- * rows or strides are not 16-byte multiples, an fp32 dtype or a head_dim that is not a
- * multiple of 8 up to 128 went to the scalar general kernel instead of the matrix
- * cores.  No
- * reference counterpart (the reference has one ATen path).
+ * partials, positioned partials, ring replays): lets a caller see which kernel ran --
+ * a 16-bit view whose rows or strides are not 16-byte multiples, or a head_dim that is
+ * not a multiple of 8 up to 128, goes to the scalar general kernel instead of the
+ * matrix cores; fp32 runs on the fp32 matrix-core kernel where its head_dim is a
+ * multiple of 4 up to 128 (and its outputs are aligned for 4-wide stores), else on the
+ * general kernel.  No reference counterpart (the reference has one ATen path).
  */
 enum hcp_ring_path {
   HCP_PATH_NONE = 0,        /* no attention call yet, or it launched nothing */
   HCP_PATH_MFMA = 1,        /* matrix-core block kernels (one launch per block or ring step) */
   HCP_PATH_RING_FUSED = 2,  /* the fused ring kernel (one launch per replay) */
-  HCP_PATH_GENERAL = 3      /* the scalar fp32 general kernel for at least one block */
+  HCP_PATH_GENERAL = 3,     /* the scalar fp32 general kernel for at least one block */
+  HCP_PATH_MFMA_F32 = 4     /* the fp32 matrix-core block kernel (fp32 views, head_dim a
+                               multiple of 4 up to 128) */
 };
 int hcp_ring_last_path(void);
 

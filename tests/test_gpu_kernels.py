@@ -55,7 +55,15 @@ BLOCK_CASES = [
     ("gqa8_qwen", 96, 517, 16, 2, 128, 600, 100, True, torch.bfloat16),
     ("mha_d64_f16", 300, 300, 4, 4, 64, 77, 77, True, torch.float16),
     ("diag_unaligned_offsets", 257, 260, 8, 8, 128, 1003, 1000, True, torch.bfloat16),
-    ("fp32_general_d64", 150, 150, 8, 8, 64, 0, 0, True, torch.float32),
+    # fp32: the fp32 matrix-core kernel (head dims multiples of 4 up to 128), else the
+    # scalar general kernel (head dim 136)
+    ("fp32_d64", 150, 150, 8, 8, 64, 0, 0, True, torch.float32),
+    ("fp32_gqa4_d128_past", 200, 300, 8, 2, 128, 100, 0, True, torch.float32),
+    ("fp32_d96_noncausal", 150, 260, 4, 4, 96, 0, 0, False, torch.float32),
+    ("fp32_d36_partly_future", 200, 100, 6, 2, 36, 0, 50, True, torch.float32),
+    ("fp32_d4_diag", 70, 90, 2, 1, 4, 20, 0, True, torch.float32),
+    ("fp32_wholly_future", 64, 64, 4, 1, 128, 0, 1000, True, torch.float32),
+    ("fp32_general_d136", 90, 120, 4, 2, 136, 30, 0, True, torch.float32),
     ("gqa2_long_noncausal", 160, 1000, 8, 4, 128, 0, 0, False, torch.bfloat16),
     ("gqa2_causal_long_past", 300, 1500, 4, 2, 128, 1200, 0, True, torch.bfloat16),
     # head dims below 128 run in the head-dim-128 kernel, zero-padded
@@ -85,6 +93,8 @@ def test_block_partial_matches_oracle(gpu, case):
     o, lse = H.block_partial(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), qo, ko,
                              causal=causal, scale=scale)
     torch.cuda.synchronize()
+    if dt == torch.float32:
+        assert H.last_path() == ("mfma_f32" if d % 4 == 0 and d <= 128 else "general"), name
     o, lse = o.cpu().numpy(), lse.cpu().numpy()
     ref_o, ref_l = C.attention_f64(q32, k32, v32, np.arange(qo, qo + lq), np.arange(ko, ko + lk), scale,
                                    causal=causal)
@@ -104,6 +114,37 @@ def test_block_partial_matches_oracle(gpu, case):
         assert np.abs(o - to[0].numpy()).max() <= tol
         if fin.any():
             assert np.abs(lse[fin] - tl[fin]).max() <= LSE_TOL
+
+
+@pytest.mark.parametrize("d,causal,accumulate", [(128, True, False), (64, False, False), (96, True, True),
+                                                (36, True, True)])
+def test_fp32_matrix_core_kernel_matches_scalar_kernel(gpu, d, causal, accumulate):
+    # The fp32 matrix-core kernel against the scalar general kernel on the same inputs:
+    # an output that is not 16-byte aligned sends a block to the scalar one.  Accumulate:
+    # both merge the same running state (a first source folded by the scalar kernel).
+    lq, lk, hq, hkv = 170, 290, 8, 2
+    (q, k, v), (q32, k32, v32) = draw(90 + d, [(lq, hq, d), (lk, hkv, d), (lk, hkv, d)], torch.float32)
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    outs = []
+    for aligned in (True, False):
+        buf = torch.empty(hq * lq * d + 4, dtype=torch.float32, device="cuda")
+        o = (buf[:hq * lq * d] if aligned else buf[1:1 + hq * lq * d]).view(hq, lq, d)
+        lse = torch.empty(hq, lq, dtype=torch.float32, device="cuda")
+        if accumulate:
+            H.block_partial(qh, kh[:, :100], vh[:, :100], 150, 0, causal=causal, o=o, lse=lse)
+            assert H.last_path() == ("mfma_f32" if aligned else "general")
+            H.block_partial(qh, kh[:, 100:], vh[:, 100:], 150, 100, causal=causal, o=o, lse=lse, accumulate=True)
+        else:
+            H.block_partial(qh, kh, vh, 150, 0, causal=causal, o=o, lse=lse)
+        assert H.last_path() == ("mfma_f32" if aligned else "general")
+        torch.cuda.synchronize()
+        outs.append((o.cpu().numpy(), lse.cpu().numpy()))
+    (o1, l1), (o2, l2) = outs
+    assert np.abs(o1 - o2).max() <= 1e-5 and np.abs(l1 - l2).max() <= 1e-5
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, np.arange(150, 150 + lq), np.arange(lk), 1 / math.sqrt(d),
+                                   causal=causal)
+    assert np.abs(o1 - ref_o.transpose(1, 0, 2)).max() <= 1e-4
+    assert np.abs(l1 - ref_l.T).max() <= 1e-4
 
 
 def test_block_partial_head_major_and_unaligned_views(gpu):
@@ -369,7 +410,7 @@ def test_ring_replay_matches_tch_blockwise(gpu, case, schedule):
     # BF16/F16 at head dims that are multiples of 8 up to 128 take the fused ring kernel
     # unless a per-step schedule is asked for
     fused = dt != torch.float32 and d % 8 == 0 and d <= 128 and schedule == "auto"
-    assert H.last_path() == ("ring_fused" if fused else "general" if dt == torch.float32 else "mfma")
+    assert H.last_path() == ("ring_fused" if fused else "mfma_f32" if dt == torch.float32 else "mfma")
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     # the reference driver on fp32 upcasts (ring.rs:861-1398 restated op for op)
@@ -594,14 +635,14 @@ POSITIONED_CASES = [
     ("zigzag_local_d128", 320, 320, 8, 2, 128, torch.bfloat16, "zigzag_local"),
     ("gaps_unsorted_q_d128", 257, 333, 16, 2, 128, torch.bfloat16, "gaps"),
     ("striped_d64_f16", 200, 300, 4, 4, 64, torch.float16, "striped_rev"),
-    ("gaps_fp32_general", 150, 190, 4, 2, 64, torch.float32, "gaps"),
+    ("gaps_fp32", 150, 190, 4, 2, 64, torch.float32, "gaps"),
     # keys in any order (ring.rs:249-273 masks key by key; the committed-KV slab appends
     # positions in arrival order, self_driving.rs:180-224): sorted on the device first
     ("shuffled_gqa4_d128", 300, 1500, 16, 4, 128, torch.bfloat16, "shuffled"),        # one sort tile
     ("shuffled_5k_merge_passes", 200, 5000, 8, 2, 128, torch.bfloat16, "shuffled"),  # 3 tiles, 2 merge passes
     ("arrival_runs_9k", 256, 9000, 8, 1, 128, torch.bfloat16, "runs"),               # 5 tiles, 3 passes
     ("shuffled_ties_d64_f16", 180, 1200, 4, 2, 64, torch.float16, "ties"),
-    ("shuffled_fp32_general", 150, 1100, 4, 2, 64, torch.float32, "shuffled"),
+    ("shuffled_fp32", 150, 1100, 4, 2, 64, torch.float32, "shuffled"),
 ]
 
 
@@ -662,7 +703,7 @@ def test_positioned_partial_committed_kv_positions(gpu, dt, d):
     # The reference's own case (ring.rs:2247-2370, ring_forward_uses_independent_query_and_
     # committed_kv_positions): queries at positions [3, 5] against committed keys at
     # [0, 4, 3, 5] -- key 4 lies in query 3's future although it precedes key 3 in the
-    # list.  fp32 head dim 4 (the test's shape, general kernel) and bf16 head dim 128.
+    # list.  fp32 head dim 4 (the test's shape, fp32 matrix-core kernel) and bf16 head dim 128.
     qp, kp = np.array([3, 5]), np.array([0, 4, 3, 5])
     (q, k, v), (q32, k32, v32) = draw(2343 + d, [(2, 1, d), (4, 1, d), (4, 1, d)], dt)
     scale = 1 / math.sqrt(d)
