@@ -183,9 +183,9 @@ struct ReplayPlan {
   int schedule = HCP_SCHEDULE_AUTO;
   size_t fused_stage_bytes = 0;           // fused paged replay: each of the K and V staging buffers [Hkv, S, D]
   // Fused replay with explicit positions (after the paged staging): positions int64 [S],
-  // the key-order flag, the two (key, row) sort buffers, K / V in position order
+  // the copy flag, the row of each position int32 [S], K / V in position order
   // [Hkv, S, D] and the per-row key limits int32 [S].
-  size_t fp_pos = 0, fp_flag = 0, fp_key[2] = {0, 0}, fp_row[2] = {0, 0}, fp_kc = 0, fp_vc = 0, fp_lim = 0;
+  size_t fp_pos = 0, fp_flag = 0, fp_rows = 0, fp_kc = 0, fp_vc = 0, fp_lim = 0;
   size_t fp_total = 0;
   bool positioned = false;                // causal with explicit positions (Striped / ZigZag)
   size_t pos_off = 0, lim_off = 0;        // workspace: positions int64 [S], key limits int32 [N, S]
@@ -317,14 +317,8 @@ ReplayPlan plan_replay(const hcp_ring_replay_desc* d, bool paged) {
     c += n8;
     p.fp_flag = c;
     c += 256;
-    for (int i = 0; i < 2; ++i) {
-      p.fp_key[i] = c;
-      c += n8;
-    }
-    for (int i = 0; i < 2; ++i) {
-      p.fp_row[i] = c;
-      c += n4;
-    }
+    p.fp_rows = c;
+    c += n4;
     p.fp_kc = c;
     c += p.fused_stage_bytes;
     p.fp_vc = c;
@@ -404,25 +398,24 @@ void run_replay_fused(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ri
 // with K / V put in position order every query row sees a prefix of the keys -- those
 // at positions up to its own (ring.rs:249-273 masks key by key) -- and the whole
 // sequence is one block of S query rows against S keys, its output rows and LSE written
-// directly, with no running state in HBM between ring steps.  q / k / v / out are the
-// whole-sequence views in domain-major order (rows [off_t, off_t + len_t) hold domain
-// t's tokens in ascending position order); k / v paged: the staged copies.
+// directly, with no running state in HBM between ring steps.  A strategy's positions
+// are a permutation of [0, S): the row of each position and each row's key limit
+// (position + 1) follow in one pass, with no sort.  q / k / v / out are the whole-
+// sequence views in domain-major order (rows [off_t, off_t + len_t) hold domain t's
+// tokens in ascending position order); k / v paged: the staged copies.
 void run_replay_fused_positioned(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ring_view q,
                                  hcp_ring_view k, hcp_ring_view v, hcp_ring_view out, float* lse_out, char* base,
                                  hipStream_t stream) {
   const int es = elem_size(d->dtype);
   int64_t* pos = reinterpret_cast<int64_t*>(base + p.fp_pos);
-  launch_domain_positions(p.spec, p.seq, pos, stream);
   int* flag = reinterpret_cast<int*>(base + p.fp_flag);
-  int64_t* const keys[2] = {reinterpret_cast<int64_t*>(base + p.fp_key[0]),
-                            reinterpret_cast<int64_t*>(base + p.fp_key[1])};
-  int32_t* const rows[2] = {reinterpret_cast<int32_t*>(base + p.fp_row[0]),
-                            reinterpret_cast<int32_t*>(base + p.fp_row[1])};
-  launch_key_sort(pos, p.seq, flag, keys, rows, stream);
-  const int f = key_sort_passes(p.seq) % 2;
+  int32_t* rows = reinterpret_cast<int32_t*>(base + p.fp_rows);
+  int32_t* lim = reinterpret_cast<int32_t*>(base + p.fp_lim);
+  launch_domain_positions(p.spec, p.seq, pos, stream);
+  launch_position_inverse(pos, p.seq, rows, lim, flag, device_error_flags(), stream);
   KvSortedGather g{};
   g.flag = flag;
-  g.rows = rows[f];
+  g.rows = rows;
   g.n = p.seq;
   g.hkv = d->num_kv_heads;
   g.row_bytes = static_cast<int64_t>(d->head_dim) * es;
@@ -435,18 +428,6 @@ void run_replay_fused_positioned(const hcp_ring_replay_desc* d, const ReplayPlan
   g.kc = base + p.fp_kc;
   g.vc = base + p.fp_vc;
   timed(kTimedGather, stream, [&] { launch_kv_sorted_gather(g, stream); });
-  KeyLimitArgs la{};
-  la.q_pos = pos;
-  la.n_q = p.seq;
-  la.k_pos = pos;
-  la.k_off[0] = 0;
-  la.k_len[0] = p.seq;
-  la.lim = reinterpret_cast<int32_t*>(base + p.fp_lim);
-  la.lim_stride = 0;
-  la.err = nullptr;  // the keys are read in sorted order whatever their order in the views
-  la.sel = flag;
-  la.k_pos_sorted = keys[f];
-  launch_key_limits(la, 1, p.seq, stream);
   hcp_ring_block_desc bd;
   bd.dtype = d->dtype;
   bd.num_q_heads = d->num_q_heads;
@@ -460,7 +441,7 @@ void run_replay_fused_positioned(const hcp_ring_replay_desc* d, const ReplayPlan
   bd.accumulate = 0;
   bd.scale = d->scale;
   BlockLaunch L = make_launch(&bd, q, k, v, nullptr, nullptr);
-  L.q_lim = la.lim;
+  L.q_lim = lim;
   L.kv_sel = flag;
   L.k_alt = g.kc;
   L.v_alt = g.vc;

@@ -118,6 +118,11 @@ struct StrategySpec {
 // Global position of the i-th token (local storage order) of domain d.
 __host__ __device__ int64_t strategy_position(const StrategySpec& s, int d, int64_t i);
 void launch_domain_positions(const StrategySpec& s, int64_t seq, int64_t* out, hipStream_t stream);
+// pos: a permutation of [0, n).  rows[pos[r]] = r, lim[r] = pos[r] + 1 (the keys of the
+// position-ordered list row r sees), *flag = 1; a position out of range sets bit 1 of
+// *err.
+void launch_position_inverse(const int64_t* pos, int64_t n, int32_t* rows, int32_t* lim, int* flag, int* err,
+                             hipStream_t stream);
 
 // lim[src * lim_stride + r] = #{j < k_len[src] : k_pos[k_off[src] + j] <= q_pos[r]} for
 // r < n_q, by binary search over a non-decreasing key list: k_pos, or k_pos_sorted when

@@ -258,6 +258,35 @@ void launch_domain_positions(const StrategySpec& s, int64_t seq, int64_t* out, h
   HCP_HIP(hipGetLastError());
 }
 
+namespace {
+// Positions that are a permutation of [0, n) (a replay's strategy positions): row
+// rows[p] holds position p, and row r sees the keys [0, pos[r] + 1) of the position-
+// ordered list.  *flag = 1 selects the position-ordered K / V copies.  A position out
+// of range (not produced by the strategy kernel) is skipped and flagged (error bit 1).
+__global__ __launch_bounds__(kPosThreads) void position_inverse_kernel(const int64_t* pos, int64_t n, int32_t* rows,
+                                                                       int32_t* lim, int* flag, int* err) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kPosThreads + threadIdx.x;
+  if (r == 0) *flag = 1;
+  if (r >= n) return;
+  const int64_t p = pos[r];
+  if (p < 0 || p >= n) {
+    atomicOr(err, 2);
+    lim[r] = 0;
+    return;
+  }
+  rows[p] = static_cast<int32_t>(r);
+  lim[r] = static_cast<int32_t>(p + 1);
+}
+}  // namespace
+
+void launch_position_inverse(const int64_t* pos, int64_t n, int32_t* rows, int32_t* lim, int* flag, int* err,
+                             hipStream_t stream) {
+  if (n <= 0) return;
+  position_inverse_kernel<<<static_cast<unsigned>(ceil_div(n, kPosThreads)), kPosThreads, 0, stream>>>(pos, n, rows,
+                                                                                                       lim, flag, err);
+  HCP_HIP(hipGetLastError());
+}
+
 void launch_key_limits(const KeyLimitArgs& a, int n_src, int64_t max_k_len, hipStream_t stream) {
   const int64_t rows = a.n_q > max_k_len ? a.n_q : max_k_len;
   if (rows <= 0 || n_src <= 0) return;

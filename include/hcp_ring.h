@@ -401,10 +401,11 @@ int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_po
  *                          directly (no fp32 state in HBM).  VANILLA positions (or
  *                          causal = 0): each workgroup folds all sources of its
  *                          domain's query tile in ring order.  Causal STRIPED /
- *                          ZIGZAG: K/V are first copied in position order (a device
- *                          sort of the positions and one gather), so every query row
- *                          sees a prefix of the keys, and the whole sequence runs as
- *                          one positions-mode block (1) of S rows against S keys.
+ *                          ZIGZAG: K/V are first copied in position order (the
+ *                          positions are a permutation of [0, S): one pass gives each
+ *                          position's row, then one gather), so every query row sees
+ *                          a prefix of the keys, and the whole sequence runs as one
+ *                          positions-mode block (1) of S rows against S keys.
  *                          Applies to BF16/F16, head_dim a multiple of 8 up to 128,
  *                          and q/k/v/out views with 16-byte aligned rows; -6
  *                          otherwise.  The paged form gathers every chunk once, in one
@@ -412,8 +413,8 @@ int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_po
  *   HCP_SCHEDULE_AUTO (0)  FUSED where it applies, else PER_STEP.
  * Workspace: hcp_ring_replay_workspace_size reports the need of the requested schedule
  * (AUTO: the larger of the two).  FUSED needs none unpaged with VANILLA positions; with
- * STRIPED / ZIGZAG it holds the positions, the sort buffers, K/V in position order
- * (2 * Hkv * S * head_dim elements) and the per-row key limits.
+ * STRIPED / ZIGZAG it holds the positions, the row of each position, K/V in position
+ * order (2 * Hkv * S * head_dim elements) and the per-row key limits.
  * ------------------------------------------------------------------------------- */
 enum hcp_ring_schedule {
   HCP_SCHEDULE_AUTO = 0,

@@ -79,15 +79,15 @@ def test_replay_workspace_size_matches_plan(hcp):
 
 @pytest.mark.parametrize("strategy", ["striped", "zigzag"])
 def test_positioned_replay_workspace_fused_and_auto(hcp, strategy):
-    # Fused with explicit positions: positions int64 [S], a 256-byte flag, two int64 and
-    # two int32 sort buffers [S], K and V in position order [Hkv, S, D] and the key
-    # limits int32 [S]; paged, the two staging buffers come first.  AUTO covers both
-    # the fused and the per-step layouts.
+    # Fused with explicit positions: positions int64 [S], a 256-byte flag, the row of
+    # each position int32 [S], K and V in position order [Hkv, S, D] and the key limits
+    # int32 [S]; paged, the two staging buffers come first.  AUTO covers both the fused
+    # and the per-step layouts.
     chunks, hq, hkv, d = [1000, 600, 424], 8, 2, 128
     s = sum(chunks)
     a = lambda n: (n + 255) // 256 * 256
     stage = a(s * hkv * d * 2)
-    fused = a(8 * s) + 256 + 2 * a(8 * s) + 2 * a(4 * s) + 2 * stage + a(4 * s)
+    fused = a(8 * s) + 256 + a(4 * s) + 2 * stage + a(4 * s)
     size = lambda **kw: hcp.replay_workspace_size(torch.bfloat16, hq, hkv, d, chunks, strategy=strategy, **kw)
     assert size(schedule="fused") == fused
     assert size(schedule="fused", paged=True) == fused + 2 * stage
