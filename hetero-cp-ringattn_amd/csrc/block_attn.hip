@@ -1108,14 +1108,15 @@ __global__ __launch_bounds__(kGenRows) void general_block_kernel(GenArgs a) {
 // cores.  A workgroup is 4 waves over 128 query rows of one head (32 rows a wave); K / V
 // tiles of 32 keys are staged in LDS as fp32, the next tile's loads in flight (in
 // registers) while the current one is folded.  Per tile a wave computes
-//   S^T (32 keys x 32 rows) = K Q^T  in DP/2 MFMAs, k-step s pairing dims (2s, 2s + 1)
-//                                    over the two lane halves;
+//   S^T (32 keys x 32 rows) = K Q^T  in DP/2 MFMAs, k-step s taking dim
+//                                    8 (s / 4) + 4 half + (s mod 4) in lane half `half`;
 //   O^T (DP dims x 32 rows) += V^T P^T  in 16 MFMAs per 32 dims, k-step s pairing the
 //                                    keys a lane already holds as element s of S^T
 //                                    (8 (s / 4) + 4 half + s mod 4), so P needs no shuffle.
-// LDS layouts make each 16-byte read feed four k-steps: K rows hold the even dims, then
-// the odd ones ([key][half * DP/2 + s]); V is stored transposed ([dim][key]), where the
-// four keys of k-steps 4t .. 4t+3 of a lane half are adjacent.  Element i of a 32x32
+// LDS layouts make each 16-byte read feed four k-steps: K rows in dim order ([key][dim],
+// a loaded 16-byte group stored as is), whose dims 8u + 4 half .. +3 are k-steps
+// 4u .. 4u+3 of a lane half; V stored transposed ([dim][key]), where the four keys of
+// k-steps 4t .. 4t+3 of a lane half are adjacent.  Element i of a 32x32
 // accumulator holds row 8 (i / 4) + 4 half + (i mod 4), column lane mod 32 -- the
 // layout of the head-dim-128 kernel's O^T, whose epilogue indexing this one shares.
 // Masking, the online softmax (base 2, scale folded into the exponent), the running-
@@ -1156,12 +1157,16 @@ __global__ __launch_bounds__(kF32Threads) void mfma_f32_block_kernel(GenArgs a) 
   const int row = tq0 + 32 * wave + lcol;
   const bool live = row < a.lq;
 
-  // Q^T fragments: k-step s, this lane's row, dim 2s + half (zero past the head dim)
+  // Q^T fragments: k-step s, this lane's row, dim 8 (s / 4) + 4 half + (s mod 4) (zero
+  // past the head dim)
   float qf[KS];
   {
     const float* qr = static_cast<const float*>(a.q) + head * a.q_hs + static_cast<int64_t>(row) * a.q_ss;
 #pragma unroll
-    for (int s2 = 0; s2 < KS; ++s2) qf[s2] = (live && 2 * s2 + half < d) ? qr[2 * s2 + half] : 0.f;
+    for (int s2 = 0; s2 < KS; ++s2) {
+      const int dim = 8 * (s2 >> 2) + 4 * half + (s2 & 3);
+      qf[s2] = (live && dim < d) ? qr[dim] : 0.f;
+    }
   }
   // Keys [0, row_lim) of the chunk are visible to this lane's row; n_kv bounds the tiles.
   int64_t row_lim = a.lk;
@@ -1213,9 +1218,7 @@ __global__ __launch_bounds__(kF32Threads) void mfma_f32_block_kernel(GenArgs a) 
     for (int j = 0; j < NV4; ++j) {
       const int e = tid + j * kF32Threads;
       const int r = e / (DP / 4), c4 = 4 * (e % (DP / 4));
-      // dims c4, c4 + 2 are even (k-steps c4 / 2, c4 / 2 + 1 of half 0), c4 + 1, c4 + 3 odd
-      *reinterpret_cast<float2*>(&ks[r * KLS + c4 / 2]) = make_float2(kr[j].x, kr[j].z);
-      *reinterpret_cast<float2*>(&ks[r * KLS + KS + c4 / 2]) = make_float2(kr[j].y, kr[j].w);
+      *reinterpret_cast<float4*>(&ks[r * KLS + c4]) = kr[j];
       vt[(c4 + 0) * VLS + r] = vr[j].x;
       vt[(c4 + 1) * VLS + r] = vr[j].y;
       vt[(c4 + 2) * VLS + r] = vr[j].z;
@@ -1242,16 +1245,24 @@ __global__ __launch_bounds__(kF32Threads) void mfma_f32_block_kernel(GenArgs a) 
     f32x16 sa, sb;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sa[r] = sb[r] = 0.f;
-    const float* kl = &ks[lcol * KLS + half * KS];
+    const float* kl = &ks[lcol * KLS + 4 * half];
 #pragma unroll
     for (int u = 0; u < KS / 4; ++u) {
-      const float4 k4 = *reinterpret_cast<const float4*>(kl + 4 * u);
+      const float4 k4 = *reinterpret_cast<const float4*>(kl + 8 * u);
       f32x16& acc = (u & 1) ? sb : sa;
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.x, qf[4 * u + 0], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.y, qf[4 * u + 1], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.z, qf[4 * u + 2], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.w, qf[4 * u + 3], acc, 0, 0, 0);
     }
+    // K reads two ahead of the MFMAs that use them (all 16 at once take 64 registers)
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int i = 0; i < KS / 4 - 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     // element i: key kv0 + 8 (i / 4) + 4 half + (i mod 4) of this lane's row
     const int64_t vis = row_lim - kv0;  // keys of the tile visible to the row: [0, vis)
     float p[16];
@@ -1274,11 +1285,16 @@ __global__ __launch_bounds__(kF32Threads) void mfma_f32_block_kernel(GenArgs a) 
       ls += p[i];
     }
     l_run = l_run * alpha + ls;
+    // alpha is exactly 1 where the running max did not grow: the accumulators are
+    // rescaled only when it grew in some lane of the wave (mostly the first tiles)
+    if (__any(m_new != m_run)) {
+      asm volatile("");  // a real branch: not turned into unconditional multiplies
+#pragma unroll
+      for (int b = 0; b < DB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
+    }
     m_run = m_new;
-#pragma unroll
-    for (int b = 0; b < DB; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
     // O^T += V^T P^T: k-steps 4t .. 4t+3 take keys 8t + 4 half + 0..3, adjacent in V^T
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -1295,6 +1311,14 @@ __global__ __launch_bounds__(kF32Threads) void mfma_f32_block_kernel(GenArgs a) 
 #pragma unroll
       for (int b = 0; b < DB; ++b) oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4[b].w, p[4 * t + 3], oacc[b], 0, 0, 0);
     }
+    // V^T reads one group (DB reads) ahead, then one per DB MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, DB, 1);
+#pragma unroll
+    for (int i = 0; i < 3 * DB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * DB, 1);
   }
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (!live) return;
