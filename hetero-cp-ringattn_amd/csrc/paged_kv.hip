@@ -211,7 +211,9 @@ __global__ __launch_bounds__(256) void paged_gather_lds_kernel(PagedCopyArgs a, 
 // Scatter through LDS, the mirror of the gather above: the lanes read an item's rows
 // from the head-major buffer in 1 KiB runs (head, token, chunk order) into LDS at
 // their pool positions, then write the pool block span in address order.  Slots before
-// t0 are left alone; slots from t1 on are zero-filled when zero_tail is set.
+// t0 are left alone; slots from t1 on are zero-filled when zero_tail is set.  The reads
+// do not depend on the block id, so they are issued before it is checked: the block-
+// table read overlaps them instead of preceding them.
 template <int P>
 __global__ __launch_bounds__(256) void paged_scatter_lds_kernel(PagedCopyArgs a, int item_bytes) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t stage[];
@@ -227,11 +229,7 @@ __global__ __launch_bounds__(256) void paged_scatter_lds_kernel(PagedCopyArgs a,
     const int ri = range_of(a, bid);
     const PagedRange& R = a.r[ri];
     const int64_t entry = R.first_entry + (bid - a.block_begin[ri]);
-    const int32_t blk = __builtin_amdgcn_readfirstlane(R.table[entry]);
-    if (blk < 0 || blk >= a.num_blocks) {
-      if (threadIdx.x == 0 && plane == 0 && part == 0) atomicOr(a.err, 1);
-      continue;
-    }
+    const int32_t blk_raw = R.table[entry];
     const uint8_t* src = plane ? R.v_buf : R.k_buf;
     const int64_t tok0 = R.table_seq_offset + entry * a.bs + static_cast<int64_t>(part) * slots;
     for (int c = threadIdx.x; c < total; c += 256) {
@@ -245,7 +243,12 @@ __global__ __launch_bounds__(256) void paged_scatter_lds_kernel(PagedCopyArgs a,
       const int64_t boff = h * R.head_stride_b + (tok - R.t0) * R.seq_stride_b + static_cast<int64_t>(cv) * 16;
       *reinterpret_cast<u32x4*>(&stage[pc]) = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + boff));
     }
+    const int32_t blk = __builtin_amdgcn_readfirstlane(blk_raw);
     __syncthreads();
+    if (blk < 0 || blk >= a.num_blocks) {  // uniform: every thread skips the stores
+      if (threadIdx.x == 0 && plane == 0 && part == 0) atomicOr(a.err, 1);
+      continue;  // the next item's LDS writes come after this item's barrier above
+    }
     uint8_t* dst = a.pool + plane * a.plane_bytes + static_cast<int64_t>(blk) * blk_bytes +
                    static_cast<int64_t>(part) * item_bytes;
     for (int c = threadIdx.x; c < total; c += 256) {
