@@ -1143,7 +1143,11 @@ __global__ __launch_bounds__(kF32Threads) void mfma_f32_block_kernel(GenArgs a) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int lcol = lane & 31, half = lane >> 5;
-  const int head = blockIdx.y;
+  // work item: heads innermost, query tiles from the last (the most keys under causal
+  // masking) to the first, so every head's heaviest tiles start first
+  const int n_qt = (a.lq + kF32Rows - 1) / kF32Rows;
+  const int head = blockIdx.x % a.hq;
+  const int qt = n_qt - 1 - static_cast<int>(blockIdx.x / a.hq);
   const int kvh = head / a.rep;
   const int d = a.d;
   if (a.q_lim != nullptr && a.kv_sel != nullptr && __builtin_amdgcn_readfirstlane(*a.kv_sel) != 0) {
@@ -1153,7 +1157,7 @@ __global__ __launch_bounds__(kF32Threads) void mfma_f32_block_kernel(GenArgs a) 
   }
   const float* kf = static_cast<const float*>(a.k) + kvh * a.k_hs;
   const float* vf = static_cast<const float*>(a.v) + kvh * a.v_hs;
-  const int tq0 = blockIdx.x * kF32Rows;
+  const int tq0 = qt * kF32Rows;
   const int row = tq0 + 32 * wave + lcol;
   const bool live = row < a.lq;
 
@@ -1555,7 +1559,9 @@ bool block_uses_mfma_f32(const BlockLaunch& L) {
 
 static void launch_mfma_f32(const BlockLaunch& L, hipStream_t stream) {
   const GenArgs a = make_gen_args(L);
-  const dim3 grid(static_cast<unsigned>(ceil_div(L.lq, kF32Rows)), static_cast<unsigned>(L.hq));
+  const int64_t items = ceil_div(L.lq, kF32Rows) * static_cast<int64_t>(L.hq);
+  require(items <= INT32_MAX, "fp32 block: too many work items");
+  const dim3 grid(static_cast<unsigned>(items));
   const dim3 block(kF32Threads);
   switch ((L.d + 31) / 32) {
     case 1: mfma_f32_block_kernel<32><<<grid, block, 0, stream>>>(a); break;
