@@ -30,8 +30,11 @@
 //     ring.rs:1024-1046, with non-decreasing key positions; a key list in any other
 //     order is read through sorted-row copies, see positions.hip).
 //
-// General path (fp32, or any head_dim <= 256): one thread per (query row, head), K/V
-// tiles staged in LDS as fp32.  Used for the fp32 CPU-smoke config.
+// fp32 matrix-core path (mfma_f32_block_kernel, head_dim a multiple of 4 up to 128):
+// v_mfma_f32_32x32x2f32 for both products, 4 waves over 128 query rows of one head.
+//
+// General path (any other shape, head_dim <= 256): one thread per (query row, head),
+// K/V tiles staged in LDS as fp32.
 #include <algorithm>
 #include <cstdlib>
 #include <vector>
