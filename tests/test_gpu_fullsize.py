@@ -242,6 +242,44 @@ def test_c5_full_staged_prefill_output(gpu):
     assert (lse_s - lse_p).abs().max().item() <= LSE_TOL
 
 
+def test_c5_full_paged_zigzag_one_launch(gpu):
+    # c5 (131072 tokens in 8 domains, Llama-3-8B heads) under ZigZag positions, K/V in a
+    # permuted bs=16 pool in domain-major order: the one-launch schedule (chunks staged,
+    # K/V gathered into position order, one positions-mode block) equals the unpaged
+    # replay bit for bit; sampled rows (the first and last rows of every domain, i.e.
+    # both ends of its two zigzag runs) match the f64 closed form over the keys at
+    # positions up to their own.
+    from oracle import strategy as SP
+    chunks = I.c5_chunks()
+    hq, hkv, d, bs = 32, 8, 128, 16
+    s = sum(chunks)
+    q, k, v = synth(48, [(s, hq, d), (s, hkv, d), (s, hkv, d)])  # position order
+    a = SP.build_assignment(chunks, "zigzag")
+    pos = sum(SP.build_domain_positions(a), [])                     # row r holds position pos[r]
+    order = torch.tensor(pos, device="cuda")
+    qd, kd, vd = (x.index_select(0, order).permute(1, 0, 2).contiguous() for x in (q, k, v))
+    nb = s // bs
+    table = torch.from_numpy(I.permuted_block_table(42, nb)).cuda()
+    pool = torch.zeros(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.paged_kv_scatter(pool, table, 0, 0, s, kd, vd)
+    out_p, lse_p = H.ring_attention_replay_paged(qd, pool, table, chunks, strategy="zigzag")
+    out_u, lse_u = H.ring_attention_replay(qd, kd, vd, chunks, strategy="zigzag")
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    assert torch.equal(out_p, out_u) and torch.equal(lse_p, lse_u)
+    offs = [sum(chunks[:i]) for i in range(len(chunks))]
+    rows = sorted({o for o in offs} | {o + L - 1 for o, L in zip(offs, chunks)} |
+                  {o + (L + 1) // 2 - 1 for o, L in zip(offs, chunks)} | {o + (L + 1) // 2 for o, L in zip(offs, chunks)})
+    p = [pos[r] for r in rows]
+    q32 = q[torch.tensor(p, device="cuda")].float().cpu().numpy()
+    k32, v32 = k.float().cpu().numpy(), v.float().cpu().numpy()
+    ref_o, ref_l = rows_closed_form(q32, k32, v32, list(range(len(rows))), 1 / math.sqrt(d), lambda i: p[i] + 1)
+    got_o = out_p.float().cpu().numpy()[:, rows].transpose(1, 0, 2)
+    got_l = lse_p.cpu().numpy()[:, rows].T
+    assert np.abs(got_o - ref_o).max() <= OUT_TOL
+    assert np.abs(got_l - ref_l).max() <= LSE_TOL
+
+
 @pytest.mark.parametrize("tokens", [4096, 2048, 12288, 12200])
 def test_llama3_8b_qkv_rope_sampled_tokens(gpu, tokens):
     # The Llama-3-8B projection (hidden 4096 -> 32 q / 8 kv heads of 128, RoPE theta 5e5)
