@@ -613,7 +613,8 @@ def ring_attention_replay(q, k, v, chunks, causal=True, scale=None, out=None, ls
     strategy)[r]``; the global order for "vanilla"); ``inverse_perm`` maps back.
     ``schedule``: "auto" (one fused launch where it applies), "per_step" (one grouped
     launch per ring step) or "fused".  Fused with "striped" / "zigzag" positions: K/V
-    copied in position order, then one positions-mode block over the whole sequence."""
+    copied in position order, then one positions-mode block over the whole sequence;
+    fused fp32: one block over the sequence on the fp32 matrix-core kernel."""
     torch = _torch()
     hq, s, d = q.shape
     hkv = k.shape[0]

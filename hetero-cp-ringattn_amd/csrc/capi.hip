@@ -393,6 +393,34 @@ void run_replay_fused(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ri
   g_last_path = HCP_PATH_RING_FUSED;
 }
 
+// One block over the whole sequence: S query rows against S keys (the domains' chunks
+// in domain-major order), the output rows and LSE written directly.  With vanilla
+// positions it is the whole causal (or full) attention of the replay; with explicit
+// positions the caller adds the row limits and the position-ordered K / V.
+BlockLaunch whole_sequence_launch(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ring_view q,
+                                  hcp_ring_view k, hcp_ring_view v, hcp_ring_view out, float* lse_out) {
+  hcp_ring_block_desc bd;
+  bd.dtype = d->dtype;
+  bd.num_q_heads = d->num_q_heads;
+  bd.num_kv_heads = d->num_kv_heads;
+  bd.head_dim = d->head_dim;
+  bd.q_len = p.seq;
+  bd.kv_len = p.seq;
+  bd.q_offset = 0;
+  bd.kv_offset = 0;
+  bd.causal = d->causal;
+  bd.accumulate = 0;
+  bd.scale = d->scale;
+  BlockLaunch L = make_launch(&bd, q, k, v, nullptr, nullptr);
+  L.fin_out = out.data;
+  L.fin_dtype = d->dtype;
+  L.fin_hs = out.head_stride;
+  L.fin_ss = out.seq_stride;
+  L.fin_lse = lse_out;
+  L.fin_lse_hs = p.seq;
+  return L;
+}
+
 // Whole replay with explicit positions (Striped / ZigZag) as one positions-mode launch
 // of the block kernel: attention over a set of keys does not depend on their order, so
 // with K / V put in position order every query row sees a prefix of the keys -- those
@@ -428,31 +456,13 @@ void run_replay_fused_positioned(const hcp_ring_replay_desc* d, const ReplayPlan
   g.kc = base + p.fp_kc;
   g.vc = base + p.fp_vc;
   timed(kTimedGather, stream, [&] { launch_kv_sorted_gather(g, stream); });
-  hcp_ring_block_desc bd;
-  bd.dtype = d->dtype;
-  bd.num_q_heads = d->num_q_heads;
-  bd.num_kv_heads = d->num_kv_heads;
-  bd.head_dim = d->head_dim;
-  bd.q_len = p.seq;
-  bd.kv_len = p.seq;
-  bd.q_offset = 0;
-  bd.kv_offset = 0;
-  bd.causal = 1;
-  bd.accumulate = 0;
-  bd.scale = d->scale;
-  BlockLaunch L = make_launch(&bd, q, k, v, nullptr, nullptr);
+  BlockLaunch L = whole_sequence_launch(d, p, q, k, v, out, lse_out);
   L.q_lim = lim;
   L.kv_sel = flag;
   L.k_alt = g.kc;
   L.v_alt = g.vc;
   L.alt_hs = p.seq * d->head_dim;
   L.alt_ss = d->head_dim;
-  L.fin_out = out.data;
-  L.fin_dtype = d->dtype;
-  L.fin_hs = out.head_stride;
-  L.fin_ss = out.seq_stride;
-  L.fin_lse = lse_out;
-  L.fin_lse_hs = p.seq;
   timed(kTimedBlock, stream, [&] { launch_block_partial(L, stream); });
   g_last_path = block_path(L);
 }
@@ -572,15 +582,21 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
     check_view(k, "k", p.seq);
     check_view(v, "v", p.seq);
   }
-  // Fused schedule: one matrix-core launch for the whole replay (BF16/F16, head_dim a
-  // multiple of 8 up to 128, 16-byte rows) -- the fused ring for vanilla positions, one
-  // positions-mode block over the sequence otherwise; AUTO takes it wherever it applies.
-  const bool fused_ok = ring_fused_applies(d->dtype, d->head_dim) && mfma_layout_ok(q) && mfma_layout_ok(out) &&
-                        (paged || (mfma_layout_ok(k) && mfma_layout_ok(v)));
+  // Fused schedule: one matrix-core launch for the whole replay -- BF16/F16 (head_dim a
+  // multiple of 8 up to 128, 16-byte rows): the fused ring for vanilla positions, one
+  // positions-mode block over the sequence otherwise; FP32 (head_dim a multiple of 4 up
+  // to 128, an output aligned for 16-byte stores): one block over the sequence on the
+  // fp32 matrix-core kernel.  AUTO takes it wherever it applies.
+  const bool f32 = d->dtype == kF32;
+  const bool fused_ok =
+      f32 ? block_uses_mfma_f32(whole_sequence_launch(d, p, q, k, v, out, lse_out))
+          : ring_fused_applies(d->dtype, d->head_dim) && mfma_layout_ok(q) && mfma_layout_ok(out) &&
+                (paged || (mfma_layout_ok(k) && mfma_layout_ok(v)));
   if (p.schedule == HCP_SCHEDULE_FUSED)
     require(fused_ok,
-            "the fused schedule needs BF16/F16, head_dim a multiple of 8 up to 128 and 16-byte "
-            "aligned rows and strides");
+            "the fused schedule needs BF16/F16 with head_dim a multiple of 8 up to 128 and 16-byte "
+            "aligned rows and strides, or FP32 with head_dim a multiple of 4 up to 128 and an output "
+            "aligned for 16-byte stores");
   if (fused_ok && p.schedule != HCP_SCHEDULE_PER_STEP) {
     hcp_ring_view kk = k, vv = v;
     if (paged) {
@@ -600,8 +616,15 @@ void run_replay(const hcp_ring_replay_desc* d, hcp_ring_view q, hcp_ring_view k,
                                 stream);
       });
     }
-    if (p.positioned) run_replay_fused_positioned(d, p, q, kk, vv, out, lse_out, base, stream);
-    else run_replay_fused(d, p, q, kk, vv, out, lse_out, stream);
+    if (p.positioned) {
+      run_replay_fused_positioned(d, p, q, kk, vv, out, lse_out, base, stream);
+    } else if (f32) {
+      const BlockLaunch L = whole_sequence_launch(d, p, q, kk, vv, out, lse_out);
+      timed(kTimedBlock, stream, [&] { launch_block_partial(L, stream); });
+      g_last_path = block_path(L);
+    } else {
+      run_replay_fused(d, p, q, kk, vv, out, lse_out, stream);
+    }
     return;
   }
   // Explicit positions: generate every domain's positions in HBM, then the key limits

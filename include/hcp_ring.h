@@ -407,9 +407,12 @@ int hcp_decode_ring_replay(const hcp_paged_decode_desc* desc, const hcp_paged_po
  *                          a prefix of the keys, and the whole sequence runs as one
  *                          positions-mode block (1) of S rows against S keys.
  *                          Applies to BF16/F16, head_dim a multiple of 8 up to 128,
- *                          and q/k/v/out views with 16-byte aligned rows; -6
- *                          otherwise.  The paged form gathers every chunk once, in one
- *                          batched launch, then runs it;
+ *                          and q/k/v/out views with 16-byte aligned rows, and to FP32
+ *                          with head_dim a multiple of 4 up to 128 and an output
+ *                          aligned for 16-byte stores (one block over the sequence on
+ *                          the fp32 matrix-core kernel, vanilla or explicit
+ *                          positions); -6 otherwise.  The paged form gathers every
+ *                          chunk once, in one batched launch, then runs it;
  *   HCP_SCHEDULE_AUTO (0)  FUSED where it applies, else PER_STEP.
  * Workspace: hcp_ring_replay_workspace_size reports the need of the requested schedule
  * (AUTO: the larger of the two).  FUSED needs none unpaged with VANILLA positions; with
@@ -690,10 +693,10 @@ int hcp_ring_replay_timing_read(double* ms, int64_t* launches);
  * Per-ring-call trace and perf events (the JSONL perf log of ring.rs:820-844 and the
  * ring_attention event of ring.rs:1376-1395, HCP_PERF_LOG).
  *
- * hcp_ring_trace_attach: every later fused-schedule replay with VANILLA positions (or
- * causal = 0) on the calling thread (hcp_ring_prefill_replay / _paged taking the fused
- * path; replays with explicit positions run untraced) runs the traced build of the
- * fused ring kernel, which writes one record per workgroup into `buffer` (caller-
+ * hcp_ring_trace_attach: every later BF16/F16 fused-schedule replay with VANILLA
+ * positions (or causal = 0) on the calling thread (hcp_ring_prefill_replay / _paged
+ * taking the fused ring; the one-block fused forms run untraced) runs the traced build
+ * of the fused ring kernel, which writes one record per workgroup into `buffer` (caller-
  * owned DEVICE memory of `bytes`; null detaches).  A replay needs
  * hcp_ring_trace_record_bytes(desc) bytes (-6 if the buffer is smaller).  Records are
  * 16 + 2 * num_domains 32-bit words: [0,2) s_memrealtime (100 MHz) at workgroup entry,

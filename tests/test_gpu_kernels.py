@@ -411,6 +411,13 @@ def test_ring_replay_matches_tch_blockwise(gpu, case, schedule):
     # unless a per-step schedule is asked for
     fused = dt != torch.float32 and d % 8 == 0 and d <= 128 and schedule == "auto"
     assert H.last_path() == ("ring_fused" if fused else "mfma_f32" if dt == torch.float32 else "mfma")
+    if dt == torch.float32 and schedule == "auto":
+        # fp32 (c1): the whole replay as one block on the fp32 matrix-core kernel
+        H.replay_timing(True)
+        H.replay_timing_read()
+        H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+        assert H.replay_timing_read()["block"][1] == 1
+        H.replay_timing(False)
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     # the reference driver on fp32 upcasts (ring.rs:861-1398 restated op for op)
@@ -505,8 +512,10 @@ def test_ring_replay_fused_rejects_what_it_cannot_run(gpu):
     s = sum(chunks)
     q = torch.zeros(8, s, d, dtype=torch.bfloat16, device="cuda")
     kv = torch.zeros(2, s, d, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(H.HcpRingError) as e:   # fp32
-        H.ring_attention_replay(q.float(), kv.float(), kv.float(), chunks, schedule="fused")
+    with pytest.raises(H.HcpRingError) as e:   # fp32 beyond the fp32 matrix-core kernel's head dims
+        q132 = torch.zeros(8, s, 132, device="cuda")
+        kv132 = torch.zeros(2, s, 132, device="cuda")
+        H.ring_attention_replay(q132, kv132, kv132, chunks, schedule="fused")
     assert e.value.code == -6
     with pytest.raises(H.HcpRingError) as e:   # rows not on 16-byte boundaries
         qq = torch.zeros(8, s, d + 4, dtype=torch.bfloat16, device="cuda")[:, :, 4:]
@@ -813,9 +822,9 @@ def test_ring_replay_strategy_matches_full_attention(gpu, case, strategy, schedu
     H.replay_timing(False)
     torch.cuda.synchronize()
     assert H.fetch_device_errors() == 0
-    # AUTO on the matrix cores: one positions-mode launch over the whole sequence against
-    # K / V in position order; per step (and fp32): launches per ring step
-    if schedule == "auto" and dt != torch.float32:
+    # AUTO: one positions-mode launch over the whole sequence against K / V in position
+    # order (fp32 on the fp32 matrix-core kernel); per step: launches per ring step
+    if schedule == "auto":
         assert launches == 1, (name, launches)
     else:
         assert launches >= len(chunks), (name, launches)
