@@ -842,6 +842,52 @@ def test_ring_replay_strategy_matches_full_attention(gpu, case, strategy, schedu
         assert np.abs(out - ro[0].numpy()).max() <= 1e-4
 
 
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
+def test_fp32_replay_one_launch(gpu, causal):
+    # fp32 (the reference's CPU dtype): AUTO runs the whole replay as one block on the
+    # fp32 matrix-core kernel, causal or not; it agrees with the per-step schedule and
+    # with the f64 closed form at the fp32 tier (1e-4).
+    chunks, hq, hkv, d = [300, 170, 250], 8, 2, 64
+    s = sum(chunks)
+    (q, k, v), (q32, k32, v32) = draw(97, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.float32)
+    args = (q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks)
+    H.replay_timing(True)
+    H.replay_timing_read()
+    o1, l1 = H.ring_attention_replay(*args, causal=causal)
+    launches = H.replay_timing_read()["block"][1]
+    H.replay_timing(False)
+    assert H.last_path() == "mfma_f32" and launches == 1
+    o2, l2 = H.ring_attention_replay(*args, causal=causal, schedule="per_step")
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    pos = np.arange(s)
+    ro, rl = C.attention_f64(q32, k32, v32, pos, pos, 1 / math.sqrt(d), causal=causal)
+    for o, l in ((o1, l1), (o2, l2)):
+        assert np.abs(o.cpu().numpy() - ro.transpose(1, 0, 2)).max() <= 1e-4
+        assert np.abs(l.cpu().numpy() - rl.T).max() <= 1e-4
+
+
+@pytest.mark.parametrize("strategy", ["vanilla", "zigzag"])
+def test_fp32_paged_replay_one_launch_matches_unpaged(gpu, strategy):
+    # fp32 K/V in a permuted paged pool: the one-launch schedule stages every chunk once
+    # (and, for ZigZag, copies K/V in position order), then runs the same block as the
+    # unpaged replay: bit for bit equal.
+    chunks = [256, 96, 160]
+    s, hq, hkv, d, bs = sum(chunks), 8, 2, 64, 16
+    (q, k, v), _ = draw(98, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.float32)
+    nb = s // bs + 3
+    table = torch.from_numpy(I.permuted_block_table(99, nb)[: s // bs]).cuda()
+    pool = torch.zeros(2, nb, bs, hkv, d, dtype=torch.float32, device="cuda")
+    H.paged_kv_scatter(pool, table, 0, 0, s, k.permute(1, 0, 2), v.permute(1, 0, 2))
+    o1, l1 = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
+                                     strategy=strategy)
+    o2, l2 = H.ring_attention_replay_paged(q.permute(1, 0, 2), pool, table, chunks, strategy=strategy)
+    assert H.last_path() == "mfma_f32"
+    torch.cuda.synchronize()
+    assert H.fetch_device_errors() == 0
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
 def test_ring_replay_paged_strategy_matches_unpaged(gpu):
     chunks = [256, 96, 160]
     s, hq, hkv, d, bs = sum(chunks), 8, 2, 128, 16
