@@ -423,7 +423,8 @@ static_assert(sizeof(RingPlan) <= 4096, "kernel arguments are limited to 4 KiB")
 // the workgroup moved past that source, two words each (0: never visited).
 constexpr int kTraceHeaderWords = 16;
 
-template <int DT, int G, bool POS, int BK, bool RING, class P, bool TRACE = false, bool PAIR = false>
+template <int DT, int G, bool POS, int BK, bool RING, class P, bool TRACE = false, bool PAIR = false,
+          int DWN = kD3>
 __device__ __forceinline__ void pingpong_body(const P& plan) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
@@ -431,9 +432,13 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   // adjacent KV heads, waves 0-3 fold query heads of the first from its left half and
   // waves 4-7 those of the second from its right half, each with the MFMA work and
   // fragment reads of a 64-dim head; tiles, DMA, swizzles and transposing reads are
-  // those of the 128-dim layout.
+  // those of the 128-dim layout.  DWN = 64 (head dims up to 64, one KV head per row):
+  // the row is the zero-padded 128-dim row of the DWN = 128 kernel, loaded the same way,
+  // and every wave folds its first 64 dims only -- the MFMAs and fragment reads of the
+  // zero half are not issued.
+  static_assert(DWN == kD3 || (DWN == kD3 / 2 && !PAIR), "dims folded: 128, or 64 without pairing");
   constexpr int D = kD3;
-  constexpr int DW = PAIR ? kD3 / 2 : kD3;       // head dims a wave folds
+  constexpr int DW = PAIR ? kD3 / 2 : DWN;       // head dims a wave folds
   constexpr int WPH = PAIR ? kWaves / 2 : kWaves;  // waves per KV head of a workgroup
   static_assert(WPH % G == 0, "heads per group must divide the waves per KV head");
   constexpr int TB = WPH / G;
@@ -647,7 +652,10 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   frag qf[KS];
   {
     const uint16_t* qbase = qv + head * q_hs + static_cast<int64_t>(wq0) * q_ss;
-    const auto qr = make_rsrc(qbase, static_cast<int64_t>(lq - wq0) * q_ss * 2);
+    // The range ends at the view's last element (row lq - 1, dim dn - 1): the fragment
+    // loads cover DW dims of every row, so with dn < DW a range of whole rows would let
+    // the last row of the last head read up to 2 (DW - dn) bytes past the end of Q.
+    const auto qr = make_rsrc(qbase, lq > wq0 ? (static_cast<int64_t>(lq - wq0 - 1) * q_ss + dn) * 2 : 0);
     const int32_t qoff = (lcol * static_cast<int32_t>(q_ss) + lhalf * 8) * 2;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -972,14 +980,14 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   }
 }
 
-template <int DT, int G, bool POS, int BK, bool PAIR>
+template <int DT, int G, bool POS, int BK, bool PAIR, int DWN>
 __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockGroup grp) {
-  pingpong_body<DT, G, POS, BK, false, BlockGroup, false, PAIR>(grp);
+  pingpong_body<DT, G, POS, BK, false, BlockGroup, false, PAIR, DWN>(grp);
 }
 
-template <int DT, int G, int BK, bool TRACE, bool PAIR>
+template <int DT, int G, int BK, bool TRACE, bool PAIR, int DWN>
 __global__ __launch_bounds__(kThreads, 1) void flash_ring_kernel(RingPlan plan) {
-  pingpong_body<DT, G, false, BK, true, RingPlan, TRACE, PAIR>(plan);
+  pingpong_body<DT, G, false, BK, true, RingPlan, TRACE, PAIR, DWN>(plan);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1463,12 +1471,16 @@ static bool block_pair_ok(const BlockLaunch& L) {
   return L.kv_sel == nullptr;
 }
 
+// Head dims up to 64 take the half-width instantiation (DWN = 64): same tiles and
+// zero padding, half the MFMA work of the 128-dim fold.
+static bool half_width_d(int d) { return d <= kD3 / 2; }
+
 // One launch of the head-dim-128 kernel over grp.a[0 .. grp.n) (same dtype, heads, and
 // positions mode; every pair has at least one query tile).
-template <int DT, int G, bool PAIR>
+template <int DT, int G, bool PAIR, int DWN = kD3>
 static void launch_pingpong_g(const BlockGroup& grp, bool pos, dim3 grid, hipStream_t stream) {
-  if (pos) flash_block_pingpong_kernel<DT, G, true, kBK3, PAIR><<<grid, kThreads, 0, stream>>>(grp);
-  else flash_block_pingpong_kernel<DT, G, false, kBK3, PAIR><<<grid, kThreads, 0, stream>>>(grp);
+  if (pos) flash_block_pingpong_kernel<DT, G, true, kBK3, PAIR, DWN><<<grid, kThreads, 0, stream>>>(grp);
+  else flash_block_pingpong_kernel<DT, G, false, kBK3, PAIR, DWN><<<grid, kThreads, 0, stream>>>(grp);
 }
 
 template <int DT>
@@ -1488,6 +1500,15 @@ static void launch_pingpong(BlockGroup& grp, hipStream_t stream, bool pair) {
       case 4: launch_pingpong_g<DT, 4, true>(grp, pos, grid, stream); break;
       case 2: launch_pingpong_g<DT, 2, true>(grp, pos, grid, stream); break;
       default: launch_pingpong_g<DT, 1, true>(grp, pos, grid, stream); break;
+    }
+    return;
+  }
+  if (half_width_d(a0.d)) {
+    switch (g) {
+      case 8: launch_pingpong_g<DT, 8, false, kD3 / 2>(grp, pos, grid, stream); break;
+      case 4: launch_pingpong_g<DT, 4, false, kD3 / 2>(grp, pos, grid, stream); break;
+      case 2: launch_pingpong_g<DT, 2, false, kD3 / 2>(grp, pos, grid, stream); break;
+      default: launch_pingpong_g<DT, 1, false, kD3 / 2>(grp, pos, grid, stream); break;
     }
     return;
   }
@@ -1636,22 +1657,28 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
   HCP_HIP(hipGetLastError());
 }
 
+template <int DT, bool TRACE, int DWN>
+static void launch_ring_kernel_w(int g, dim3 grid, const RingPlan& p, hipStream_t stream) {
+  switch (g) {
+    case 8: flash_ring_kernel<DT, 8, kBK3, TRACE, false, DWN><<<grid, kThreads, 0, stream>>>(p); break;
+    case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, false, DWN><<<grid, kThreads, 0, stream>>>(p); break;
+    case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, false, DWN><<<grid, kThreads, 0, stream>>>(p); break;
+    default: flash_ring_kernel<DT, 1, kBK3, TRACE, false, DWN><<<grid, kThreads, 0, stream>>>(p); break;
+  }
+}
+
 template <int DT, bool TRACE>
 static void launch_ring_kernel(int g, bool pair, dim3 grid, const RingPlan& p, hipStream_t stream) {
   if (pair) {
     switch (g) {
-      case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, true><<<grid, kThreads, 0, stream>>>(p); break;
-      case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, true><<<grid, kThreads, 0, stream>>>(p); break;
-      default: flash_ring_kernel<DT, 1, kBK3, TRACE, true><<<grid, kThreads, 0, stream>>>(p); break;
+      case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, true, kD3><<<grid, kThreads, 0, stream>>>(p); break;
+      case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, true, kD3><<<grid, kThreads, 0, stream>>>(p); break;
+      default: flash_ring_kernel<DT, 1, kBK3, TRACE, true, kD3><<<grid, kThreads, 0, stream>>>(p); break;
     }
     return;
   }
-  switch (g) {
-    case 8: flash_ring_kernel<DT, 8, kBK3, TRACE, false><<<grid, kThreads, 0, stream>>>(p); break;
-    case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, false><<<grid, kThreads, 0, stream>>>(p); break;
-    case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, false><<<grid, kThreads, 0, stream>>>(p); break;
-    default: flash_ring_kernel<DT, 1, kBK3, TRACE, false><<<grid, kThreads, 0, stream>>>(p); break;
-  }
+  if (half_width_d(p.d)) launch_ring_kernel_w<DT, TRACE, kD3 / 2>(g, grid, p, stream);
+  else launch_ring_kernel_w<DT, TRACE, kD3>(g, grid, p, stream);
 }
 
 bool ring_fused_applies(int dtype, int d) { return (dtype == kBF16 || dtype == kF16) && padded_d_ok(d); }

@@ -137,6 +137,34 @@ def test_c2_full_ring_prefill_both_schedules(gpu):
         assert np.abs(l[:, off:].cpu().numpy() - rl[0].numpy()).max() <= LSE_TOL
 
 
+def test_qwen2_0p5b_d64_ring_prefill_q_ending_at_a_segment(gpu):
+    # The reference's own model heads (Qwen2-0.5B: 14 q / 2 kv heads, D=64) on c2's chunks,
+    # token-major Q/K/V as the projection writes them, both schedules.  Q is 7 x 2 MiB,
+    # so it ends where the allocator's segment ends: the block kernel's Q loads must stop
+    # at the view's last element (a range of whole 128-dim rows once read 128 bytes past
+    # the end of Q for the last row of the last head).  Rows against the f64 closed form,
+    # the last row included.
+    chunks, hq, hkv, d = [4096, 2560, 1536], 14, 2, 64
+    s = sum(chunks)
+    q, k, v = synth(47, [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    assert (q.numel() * q.element_size()) % (2 << 20) == 0
+    qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+    out, lse = H.ring_attention_replay(qh, kh, vh, chunks)
+    assert H.last_path() == "ring_fused"
+    out_s, lse_s = H.ring_attention_replay(qh, kh, vh, chunks, schedule="per_step")
+    assert H.last_path() == "mfma"
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    rows = [0, 1, 127, 4095, 4096, 5000, 6655, 6656, 7000, 8190, 8191]
+    q32, k32, v32 = (x.float().cpu().numpy() for x in (q, k, v))
+    ref_o, ref_l = rows_closed_form(q32, k32, v32, rows, 1 / math.sqrt(d), lambda r: r + 1)
+    for o, l in ((out, lse), (out_s, lse_s)):
+        got_o = o.float().cpu().numpy()[:, rows].transpose(1, 0, 2)
+        got_l = l.cpu().numpy()[:, rows].T
+        assert np.abs(got_o - ref_o).max() <= OUT_TOL
+        assert np.abs(got_l - ref_l).max() <= LSE_TOL
+
+
 def test_c4_full_paged_decode_every_sequence(gpu):
     batch, hq, hkv, d, bs, ctx, nb = 64, 32, 8, 128, 16, 16384, 65536
     chunks = [8192, 5120, 3072]
