@@ -93,8 +93,6 @@ def test_static_decode_allocates_nothing(gpu):
     assert after[0] <= before[0] and after[1] == before[1] and after[2] == before[2], (before, after)
 
 
-@pytest.mark.skip(reason="first ran in the GPU call that ended with an unexplained GPU fault (in the next "
-                         "process, a head-dim-64 benchmark leg); kept off the GPU until that fault is explained")
 def test_static_decode_replays_in_a_graph(gpu):
     # Captured in a HIP graph (it records no memset nodes) and replayed three times with
     # eager work and synchronisations in between, each replay on new query values:
