@@ -45,9 +45,9 @@ C5 = dict(chunks=[21504, 13312, 18432, 23552, 24576, 9216, 8192, 12288], hq=32, 
 # The reference's own model (Qwen2-0.5B: 14 q / 2 kv heads, head dim 64,
 # docs/2domain_mps_hip_scale_matrix.md) on c3's 32k 4-domain split.
 # The reference's own model heads (Qwen2-0.5B: 14 q / 2 kv heads, head dim 64) on c2's
-# chunks.  The 32k size of this leg stays off: its one run (through the paired
-# head-dim-64 kernels, since switched off) ended with a GPU fault whose cause is unknown.
+# chunks and on c3's.
 QWEN64 = dict(name="qwen2_0p5b_d64", chunks=[4096, 2560, 1536], hq=14, hkv=2, d=64, seed=47)
+QWEN64_32K = dict(name="qwen2_0p5b_d64_32k", chunks=[12288, 8192, 8192, 4096], hq=14, hkv=2, d=64, seed=47)
 
 
 def log(msg: str) -> None:
@@ -234,14 +234,16 @@ def bench_c2(H, torch, steps: int, warmup: int):
     return res
 
 
-def bench_qwen_d64(H, torch, steps: int, warmup: int):
-    """Ring prefill with Qwen2-0.5B heads (14 q / 2 kv, D=64), S=8192 in [4096, 2560, 1536],
-    bf16, causal, fused schedule, K/V token-major as the projection writes them; head
-    dim 64 runs the half-width instantiation of the block kernel (the 128-dim tiles,
-    MFMAs on the first 64 dims only)."""
-    r = bench_prefill(H, torch, steps, warmup, QWEN64)
-    log(f"qwen d64 8k {r['tflops']:.1f} TFLOP/s ({r['path']})")
-    res = {"workload": "Qwen2-0.5B heads: S=8192 in [4096,2560,1536], 14q/2kv heads, D=64, bf16, causal",
+def bench_qwen_d64(H, torch, steps: int, warmup: int, c=None):
+    """Ring prefill with Qwen2-0.5B heads (14 q / 2 kv, D=64), bf16, causal, fused
+    schedule, K/V token-major as the projection writes them; head dim 64 runs the
+    half-width instantiation of the block kernel (the 128-dim tiles, MFMAs on the first
+    64 dims only).  Default: S=8192 in [4096, 2560, 1536]."""
+    c = c or QWEN64
+    r = bench_prefill(H, torch, steps, warmup, c)
+    log(f"{c['name']} {r['tflops']:.1f} TFLOP/s ({r['path']})")
+    chunks = ",".join(str(x) for x in c["chunks"])
+    res = {"workload": f"Qwen2-0.5B heads: S={sum(c['chunks'])} in [{chunks}], 14q/2kv heads, D=64, bf16, causal",
            **prefill_summary(r)}
     del r
     return res
@@ -695,7 +697,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
-    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "strategies", "fp32"], default=None,
+    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "qwen64_32k", "strategies", "fp32"], default=None,
                     help="run one prefill leg alone and print its JSON object (profiling)")
     ap.add_argument("--trace", action="store_true",
                     help="with --leg: also run traced launches (per-workgroup records) and summarise them")
@@ -717,8 +719,9 @@ def main():
     H = load_pkg()
     torch.cuda.set_device(0)
     log(f"device {torch.cuda.get_device_name(0)}")
-    if args.leg == "qwen64":
-        print(json.dumps({"leg": "qwen64", **bench_qwen_d64(H, torch, args.steps, args.warmup)}), flush=True)
+    if args.leg in ("qwen64", "qwen64_32k"):
+        c = QWEN64 if args.leg == "qwen64" else QWEN64_32K
+        print(json.dumps({"leg": args.leg, **bench_qwen_d64(H, torch, args.steps, args.warmup, c)}), flush=True)
         return
     if args.leg == "fp32":
         print(json.dumps({"leg": "fp32", **bench_fp32(H, torch, args.steps, args.warmup)}), flush=True)
@@ -750,6 +753,7 @@ def main():
         del per
         c2 = bench_c2(H, torch, args.steps, args.warmup)
         qwen = bench_qwen_d64(H, torch, args.steps, args.warmup)
+        qwen32 = bench_qwen_d64(H, torch, args.steps, args.warmup, QWEN64_32K)
         dec = bench_decode(H, torch, args.steps, args.warmup)
         log(f"c4 decode {dec['gbs']:.1f} GB/s")
         stg = bench_staged(H, torch, args.steps, args.warmup)
@@ -786,6 +790,7 @@ def main():
                                  "sampled_max_abs_err_lse": stg.get("sampled_err_lse")},
             c2_prefill=c2,
             qwen2_0p5b_d64_8k=qwen,
+            qwen2_0p5b_d64_32k=qwen32,
             c3_per_step=c3_per_step,
             lse_merge={"workload": "c3 ring partials of the 4 target domains (10 x [32, L, 128] fp32 + LSE) "
                                    "-> bf16 rows + fp32 LSE, one hcp_ring_lse_merge per domain",

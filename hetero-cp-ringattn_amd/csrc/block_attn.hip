@@ -423,25 +423,19 @@ static_assert(sizeof(RingPlan) <= 4096, "kernel arguments are limited to 4 KiB")
 // the workgroup moved past that source, two words each (0: never visited).
 constexpr int kTraceHeaderWords = 16;
 
-template <int DT, int G, bool POS, int BK, bool RING, class P, bool TRACE = false, bool PAIR = false,
-          int DWN = kD3>
+template <int DT, int G, bool POS, int BK, bool RING, class P, bool TRACE = false, int DWN = kD3>
 __device__ __forceinline__ void pingpong_body(const P& plan) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
-  // D: the LDS row of a K / V tile (128 dims).  PAIR (head dim 64): the row holds two
-  // adjacent KV heads, waves 0-3 fold query heads of the first from its left half and
-  // waves 4-7 those of the second from its right half, each with the MFMA work and
-  // fragment reads of a 64-dim head; tiles, DMA, swizzles and transposing reads are
-  // those of the 128-dim layout.  DWN = 64 (head dims up to 64, one KV head per row):
-  // the row is the zero-padded 128-dim row of the DWN = 128 kernel, loaded the same way,
-  // and every wave folds its first 64 dims only -- the MFMAs and fragment reads of the
-  // zero half are not issued.
-  static_assert(DWN == kD3 || (DWN == kD3 / 2 && !PAIR), "dims folded: 128, or 64 without pairing");
+  // D: the LDS row of a K / V tile (128 dims; head dims below it zero-padded by the DMA).
+  // DW = DWN: the head dims a wave folds.  DWN = 64 (head dims up to 64): the rows,
+  // tiles, DMA, swizzles and transposing reads of the 128-dim kernel, with the MFMAs and
+  // fragment reads of the zero half not issued.
+  static_assert(DWN == kD3 || DWN == kD3 / 2, "dims folded: 128 or 64");
   constexpr int D = kD3;
-  constexpr int DW = PAIR ? kD3 / 2 : DWN;       // head dims a wave folds
-  constexpr int WPH = PAIR ? kWaves / 2 : kWaves;  // waves per KV head of a workgroup
-  static_assert(WPH % G == 0, "heads per group must divide the waves per KV head");
-  constexpr int TB = WPH / G;
+  constexpr int DW = DWN;
+  static_assert(kWaves % G == 0, "heads per group must divide the waves");
+  constexpr int TB = kWaves / G;
   constexpr int TQ = 32 * TB;
   constexpr int KS = DW / 16;
   constexpr int DB = DW / 32;
@@ -520,20 +514,10 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     dn = ap->d;
   }
 
-  const int wave_h = PAIR ? wave % WPH : wave;  // wave index among its KV head's waves
-  const int half = PAIR ? wave / WPH : 0;         // which KV head of the pair (its LDS half)
-  int head, kvh;  // this wave's query head; the (first) KV head whose rows the tiles hold
-  if constexpr (PAIR) {
-    const int per_kv = rep / G;  // head groups per KV head
-    const int pair = hg / per_kv;
-    kvh = 2 * pair;
-    head = (kvh + half) * rep + (hg - pair * per_kv) * G + (wave_h % G);
-  } else {
-    head = hg * G + (wave % G);
-    kvh = (hg * G) / rep;
-  }
+  const int head = hg * G + (wave % G);  // this wave's query head
+  const int kvh = (hg * G) / rep;          // the KV head whose rows the tiles hold
   const int tq0 = qt * TQ;
-  const int wq0 = tq0 + (wave_h / G) * 32;
+  const int wq0 = tq0 + (wave / G) * 32;
   const int my_q = wq0 + lcol;
   const int q_end = min(lq, tq0 + TQ);
 
@@ -592,7 +576,6 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   const uint32_t k_lds0 = lds_offset(k_lds) + wave * (kDmaPerWave * 1024);
   const uint32_t v_lds0 = lds_offset(v_lds) + wave * (kDmaPerWave * 1024);
   uint32_t k_voff[kDmaPerWave], v_voff[kDmaPerWave];
-  const int dn_row = PAIR ? 2 * dn : dn;  // dims of a tile row read from the views
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
     const int r = (wave * kDmaPerWave + j) * 4 + (lane >> 4);
@@ -600,8 +583,8 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     // global chunk p ^ swz(r) of row r; chunks past the head dim get an offset beyond any
     // tile's records (tiles stay below 2^31 bytes), so the DMA writes zeros there
     const int kc = p ^ (r & 15), vc = p ^ (4 * (r & 3));
-    k_voff[j] = kc * 8 < dn_row ? static_cast<uint32_t>(r * k_ss * 2 + (kc << 4)) : 0x80000000u;
-    v_voff[j] = vc * 8 < dn_row ? static_cast<uint32_t>(r * v_ss * 2 + (vc << 4)) : 0x80000000u;
+    k_voff[j] = kc * 8 < dn ? static_cast<uint32_t>(r * k_ss * 2 + (kc << 4)) : 0x80000000u;
+    v_voff[j] = vc * 8 < dn ? static_cast<uint32_t>(r * v_ss * 2 + (vc << 4)) : 0x80000000u;
   }
   // Buffer descriptors of a tile's rows [kr, ke): a few scalar instructions per tile
   // (every wave of the CU shares one scalar unit, and the DMA issue sits on the
@@ -669,15 +652,12 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   // K fragment s of a lane sits at k_rd0 ^ (s << 5) in a tile: (lhalf + 2s) ^ (krow & 15)
   // changes only bits 1-3 of the 16-byte column index with s, and tile bases are
   // 1 KiB-aligned, so the XOR commutes with adding the base.
-  // (PAIR: k-steps 4 * half + s, the wave's half of the row: the XOR with 4 * half << 5
-  // sets bit 7 only, disjoint from the s << 5 of the loop)
-  const uint32_t k_rd0 = (krow * (D * 2) + ((lhalf ^ (krow & 15)) << 4)) ^ (PAIR ? (4u * half) << 5 : 0u);
+  const uint32_t k_rd0 = krow * (D * 2) + ((lhalf ^ (krow & 15)) << 4);
   const int g16 = lane >> 4, sl = lane & 15;
   uint32_t v_rd[DB];
 #pragma unroll
-  for (int bb = 0; bb < DB; ++bb) {
-    const int b = (PAIR ? 2 * half : 0) + bb;  // 32-dim block of the LDS row
-    v_rd[bb] = (8 * (g16 >> 1) + (sl >> 2)) * (D * 2) +
+  for (int b = 0; b < DB; ++b) {  // 32-dim block of the LDS row
+    v_rd[b] = (8 * (g16 >> 1) + (sl >> 2)) * (D * 2) +
                ((4 * (b ^ (sl >> 2)) + 2 * (g16 & 1) + ((sl & 3) >> 1)) << 4) + 8 * (sl & 1);
   }
   const uint32_t k_lds_off = lds_offset(k_lds);
@@ -980,14 +960,14 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   }
 }
 
-template <int DT, int G, bool POS, int BK, bool PAIR, int DWN>
+template <int DT, int G, bool POS, int BK, int DWN>
 __global__ __launch_bounds__(kThreads, 1) void flash_block_pingpong_kernel(BlockGroup grp) {
-  pingpong_body<DT, G, POS, BK, false, BlockGroup, false, PAIR, DWN>(grp);
+  pingpong_body<DT, G, POS, BK, false, BlockGroup, false, DWN>(grp);
 }
 
-template <int DT, int G, int BK, bool TRACE, bool PAIR, int DWN>
+template <int DT, int G, int BK, bool TRACE, int DWN>
 __global__ __launch_bounds__(kThreads, 1) void flash_ring_kernel(RingPlan plan) {
-  pingpong_body<DT, G, false, BK, true, RingPlan, TRACE, PAIR, DWN>(plan);
+  pingpong_body<DT, G, false, BK, true, RingPlan, TRACE, DWN>(plan);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1391,37 +1371,16 @@ static int heads_per_group(int rep) {
   return 1;
 }
 
-// Head dim 64 with adjacent KV heads (head stride = 64 elements, as in the token-major
-// [S, Hkv, 64] projection output) and an even KV head count: the paired
-// instantiations fold two KV heads per 128-dim tile row instead of zero-padding one
-// head to 128.  Switched off: a 32k run of the head-dim-64 benchmark leg (paired, then
-// zero-padded head-major) ended with a GPU fault whose cause is not identified (a host
-// model of every global access of both launches finds them in bounds), so head dim 64
-// takes the zero-padded kernels until that fault is explained.
-constexpr bool kPairedD64Enabled = false;
-static bool pair_ok(int dtype, int d, int hkv, int64_t k_hs, int64_t v_hs) {
-  return kPairedD64Enabled && (dtype == kBF16 || dtype == kF16) && d == kD3 / 2 && hkv % 2 == 0 &&
-         k_hs == kD3 / 2 && v_hs == kD3 / 2;
-}
-
 // Work decomposition of the matrix-core kernels: query heads per group (sharing a K/V
-// tile), query rows per workgroup and head groups per query tile.  Paired: up to 4
-// query heads of each of the two KV heads (4 waves per KV head).
+// tile), query rows per workgroup and head groups per query tile.
 struct Geometry {
   int g, tq, n_groups;
 };
-static Geometry geometry(int hq, int hkv, bool pair) {
-  const int rep = hq / hkv;
+static Geometry geometry(int hq, int hkv) {
   Geometry r;
-  if (pair) {
-    r.g = rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
-    r.tq = 32 * (kWaves / 2 / r.g);
-    r.n_groups = (hkv / 2) * (rep / r.g);
-  } else {
-    r.g = heads_per_group(rep);
-    r.tq = 32 * (kWaves / r.g);
-    r.n_groups = hq / r.g;
-  }
+  r.g = heads_per_group(hq / hkv);
+  r.tq = 32 * (kWaves / r.g);
+  r.n_groups = hq / r.g;
   return r;
 }
 
@@ -1432,7 +1391,7 @@ static void check_tile_bytes(int64_t k_ss, int64_t v_ss) {
           "k/v sequence strides too large for the matrix-core kernel");
 }
 
-static BlockArgs make_args(const BlockLaunch& L, bool pair) {
+static BlockArgs make_args(const BlockLaunch& L) {
   BlockArgs a;
   a.q = static_cast<const uint16_t*>(L.q);
   a.k = static_cast<const uint16_t*>(L.k);
@@ -1459,16 +1418,10 @@ static BlockArgs make_args(const BlockLaunch& L, bool pair) {
   a.alt_hs = L.alt_hs;
   a.alt_ss = L.alt_ss;
   a.d = static_cast<int32_t>(L.d);
-  const Geometry geo = geometry(L.hq, L.hkv, pair);
+  const Geometry geo = geometry(L.hq, L.hkv);
   a.n_qtiles = static_cast<int32_t>(ceil_div(L.lq, geo.tq));
   a.n_groups = geo.n_groups;
   return a;
-}
-
-static bool block_pair_ok(const BlockLaunch& L) {
-  if (!pair_ok(L.dtype, L.d, L.hkv, L.k_hs, L.v_hs)) return false;
-  // the sorted-row copies of a positioned call are head-major: not paired
-  return L.kv_sel == nullptr;
 }
 
 // Head dims up to 64 take the half-width instantiation (DWN = 64): same tiles and
@@ -1477,14 +1430,24 @@ static bool half_width_d(int d) { return d <= kD3 / 2; }
 
 // One launch of the head-dim-128 kernel over grp.a[0 .. grp.n) (same dtype, heads, and
 // positions mode; every pair has at least one query tile).
-template <int DT, int G, bool PAIR, int DWN = kD3>
+template <int DT, int G, int DWN>
 static void launch_pingpong_g(const BlockGroup& grp, bool pos, dim3 grid, hipStream_t stream) {
-  if (pos) flash_block_pingpong_kernel<DT, G, true, kBK3, PAIR, DWN><<<grid, kThreads, 0, stream>>>(grp);
-  else flash_block_pingpong_kernel<DT, G, false, kBK3, PAIR, DWN><<<grid, kThreads, 0, stream>>>(grp);
+  if (pos) flash_block_pingpong_kernel<DT, G, true, kBK3, DWN><<<grid, kThreads, 0, stream>>>(grp);
+  else flash_block_pingpong_kernel<DT, G, false, kBK3, DWN><<<grid, kThreads, 0, stream>>>(grp);
+}
+
+template <int DT, int DWN>
+static void launch_pingpong_w(const BlockGroup& grp, int g, bool pos, dim3 grid, hipStream_t stream) {
+  switch (g) {
+    case 8: launch_pingpong_g<DT, 8, DWN>(grp, pos, grid, stream); break;
+    case 4: launch_pingpong_g<DT, 4, DWN>(grp, pos, grid, stream); break;
+    case 2: launch_pingpong_g<DT, 2, DWN>(grp, pos, grid, stream); break;
+    default: launch_pingpong_g<DT, 1, DWN>(grp, pos, grid, stream); break;
+  }
 }
 
 template <int DT>
-static void launch_pingpong(BlockGroup& grp, hipStream_t stream, bool pair) {
+static void launch_pingpong(BlockGroup& grp, hipStream_t stream) {
   const BlockArgs& a0 = grp.a[0];
   for (int i = 0; i < grp.n; ++i) {
     check_tile_bytes(grp.a[i].k_ss, grp.a[i].v_ss);
@@ -1494,39 +1457,17 @@ static void launch_pingpong(BlockGroup& grp, hipStream_t stream, bool pair) {
   for (int i = 0; i < grp.n; ++i) grp.qt_begin[i + 1] = grp.qt_begin[i] + grp.a[i].n_qtiles;
   const dim3 grid(static_cast<unsigned>(grp.qt_begin[grp.n] * a0.n_groups));
   const bool pos = a0.q_lim != nullptr;
-  const int g = geometry(a0.hq, a0.hkv, pair).g;
-  if (pair) {
-    switch (g) {
-      case 4: launch_pingpong_g<DT, 4, true>(grp, pos, grid, stream); break;
-      case 2: launch_pingpong_g<DT, 2, true>(grp, pos, grid, stream); break;
-      default: launch_pingpong_g<DT, 1, true>(grp, pos, grid, stream); break;
-    }
-    return;
-  }
-  if (half_width_d(a0.d)) {
-    switch (g) {
-      case 8: launch_pingpong_g<DT, 8, false, kD3 / 2>(grp, pos, grid, stream); break;
-      case 4: launch_pingpong_g<DT, 4, false, kD3 / 2>(grp, pos, grid, stream); break;
-      case 2: launch_pingpong_g<DT, 2, false, kD3 / 2>(grp, pos, grid, stream); break;
-      default: launch_pingpong_g<DT, 1, false, kD3 / 2>(grp, pos, grid, stream); break;
-    }
-    return;
-  }
-  switch (g) {
-    case 8: launch_pingpong_g<DT, 8, false>(grp, pos, grid, stream); break;
-    case 4: launch_pingpong_g<DT, 4, false>(grp, pos, grid, stream); break;
-    case 2: launch_pingpong_g<DT, 2, false>(grp, pos, grid, stream); break;
-    default: launch_pingpong_g<DT, 1, false>(grp, pos, grid, stream); break;
-  }
+  const int g = geometry(a0.hq, a0.hkv).g;
+  if (half_width_d(a0.d)) launch_pingpong_w<DT, kD3 / 2>(grp, g, pos, grid, stream);
+  else launch_pingpong_w<DT, kD3>(grp, g, pos, grid, stream);
 }
 
 template <int DT>
 static void launch_mfma(const BlockLaunch& L, hipStream_t stream) {
   BlockGroup grp;
   grp.n = 1;
-  const bool pair = block_pair_ok(L);
-  grp.a[0] = make_args(L, pair);
-  launch_pingpong<DT>(grp, stream, pair);
+  grp.a[0] = make_args(L);
+  launch_pingpong<DT>(grp, stream);
 }
 
 static GenArgs make_gen_args(const BlockLaunch& L) {
@@ -1635,11 +1576,9 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
   if (live.empty()) return;
   const BlockLaunch& f = *live[0];
   bool grouped = !f.force_general && block_uses_mfma(f.dtype, f.d) && padded_d_ok(f.d);
-  const bool pair = block_pair_ok(f);
   for (const BlockLaunch* L : live)
     grouped = grouped && !L->force_general && L->dtype == f.dtype && L->d == f.d && L->hq == f.hq &&
-              L->hkv == f.hkv && (L->causal && L->q_lim != nullptr) == (f.causal && f.q_lim != nullptr) &&
-              block_pair_ok(*L) == pair;
+              L->hkv == f.hkv && (L->causal && L->q_lim != nullptr) == (f.causal && f.q_lim != nullptr);
   if (!grouped) {
     for (const BlockLaunch* L : live) launch_block_partial(*L, stream);
     return;
@@ -1650,9 +1589,9 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
   for (size_t base = 0; base < live.size(); base += kMaxGroup) {
     BlockGroup grp;
     grp.n = static_cast<int32_t>(std::min<size_t>(kMaxGroup, live.size() - base));
-    for (int i = 0; i < grp.n; ++i) grp.a[i] = make_args(*live[base + i], pair);
-    if (f.dtype == kBF16) launch_pingpong<kBF16>(grp, stream, pair);
-    else launch_pingpong<kF16>(grp, stream, pair);
+    for (int i = 0; i < grp.n; ++i) grp.a[i] = make_args(*live[base + i]);
+    if (f.dtype == kBF16) launch_pingpong<kBF16>(grp, stream);
+    else launch_pingpong<kF16>(grp, stream);
   }
   HCP_HIP(hipGetLastError());
 }
@@ -1660,23 +1599,15 @@ void launch_block_group(const BlockLaunch* Ls, int n, hipStream_t stream) {
 template <int DT, bool TRACE, int DWN>
 static void launch_ring_kernel_w(int g, dim3 grid, const RingPlan& p, hipStream_t stream) {
   switch (g) {
-    case 8: flash_ring_kernel<DT, 8, kBK3, TRACE, false, DWN><<<grid, kThreads, 0, stream>>>(p); break;
-    case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, false, DWN><<<grid, kThreads, 0, stream>>>(p); break;
-    case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, false, DWN><<<grid, kThreads, 0, stream>>>(p); break;
-    default: flash_ring_kernel<DT, 1, kBK3, TRACE, false, DWN><<<grid, kThreads, 0, stream>>>(p); break;
+    case 8: flash_ring_kernel<DT, 8, kBK3, TRACE, DWN><<<grid, kThreads, 0, stream>>>(p); break;
+    case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, DWN><<<grid, kThreads, 0, stream>>>(p); break;
+    case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, DWN><<<grid, kThreads, 0, stream>>>(p); break;
+    default: flash_ring_kernel<DT, 1, kBK3, TRACE, DWN><<<grid, kThreads, 0, stream>>>(p); break;
   }
 }
 
 template <int DT, bool TRACE>
-static void launch_ring_kernel(int g, bool pair, dim3 grid, const RingPlan& p, hipStream_t stream) {
-  if (pair) {
-    switch (g) {
-      case 4: flash_ring_kernel<DT, 4, kBK3, TRACE, true, kD3><<<grid, kThreads, 0, stream>>>(p); break;
-      case 2: flash_ring_kernel<DT, 2, kBK3, TRACE, true, kD3><<<grid, kThreads, 0, stream>>>(p); break;
-      default: flash_ring_kernel<DT, 1, kBK3, TRACE, true, kD3><<<grid, kThreads, 0, stream>>>(p); break;
-    }
-    return;
-  }
+static void launch_ring_kernel(int g, dim3 grid, const RingPlan& p, hipStream_t stream) {
   if (half_width_d(p.d)) launch_ring_kernel_w<DT, TRACE, kD3 / 2>(g, grid, p, stream);
   else launch_ring_kernel_w<DT, TRACE, kD3>(g, grid, p, stream);
 }
@@ -1698,8 +1629,7 @@ void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
   p.dtype = L.dtype;
   p.d = L.d;
   p.hq = L.hq; p.hkv = L.hkv; p.rep = L.hq / L.hkv;
-  const bool pair = ring_fused_paired(L);
-  const Geometry geo = geometry(L.hq, L.hkv, pair);
+  const Geometry geo = geometry(L.hq, L.hkv);
   const int g = geo.g, tq = geo.tq;
   p.n_groups = geo.n_groups;
   p.n = L.n;
@@ -1718,25 +1648,23 @@ void launch_ring_fused(const RingLaunch& L, hipStream_t stream) {
   for (int s = 0; s < L.n; ++s) p.qt_begin[s + 1] = p.qt_begin[s] + static_cast<int32_t>(ceil_div(p.len[L.n - 1 - s], tq));
   const int64_t blocks = static_cast<int64_t>(p.qt_begin[L.n]) * p.n_groups;
   require(blocks <= INT32_MAX, "fused ring: too many workgroups");
-  require(blocks == ring_fused_workgroups(L.hq, L.hkv, L.n, L.len, pair), "fused ring: workgroup count");
+  require(blocks == ring_fused_workgroups(L.hq, L.hkv, L.n, L.len), "fused ring: workgroup count");
   p.trace = L.trace;
   p.trace_stride = L.trace_stride;
   if (L.trace != nullptr) require(L.trace_stride >= kTraceHeaderWords + 2 * L.n, "fused ring: trace stride");
   const dim3 grid(static_cast<unsigned>(blocks));
   if (L.dtype == kBF16) {
-    if (L.trace != nullptr) launch_ring_kernel<kBF16, true>(g, pair, grid, p, stream);
-    else launch_ring_kernel<kBF16, false>(g, pair, grid, p, stream);
+    if (L.trace != nullptr) launch_ring_kernel<kBF16, true>(g, grid, p, stream);
+    else launch_ring_kernel<kBF16, false>(g, grid, p, stream);
   } else {
-    if (L.trace != nullptr) launch_ring_kernel<kF16, true>(g, pair, grid, p, stream);
-    else launch_ring_kernel<kF16, false>(g, pair, grid, p, stream);
+    if (L.trace != nullptr) launch_ring_kernel<kF16, true>(g, grid, p, stream);
+    else launch_ring_kernel<kF16, false>(g, grid, p, stream);
   }
   HCP_HIP(hipGetLastError());
 }
 
-bool ring_fused_paired(const RingLaunch& L) { return pair_ok(L.dtype, L.d, L.hkv, L.k_hs, L.v_hs); }
-
-int64_t ring_fused_workgroups(int hq, int hkv, int n, const int64_t* len, bool pair) {
-  const Geometry geo = geometry(hq, hkv, pair);
+int64_t ring_fused_workgroups(int hq, int hkv, int n, const int64_t* len) {
+  const Geometry geo = geometry(hq, hkv);
   int64_t tiles = 0;
   for (int i = 0; i < n; ++i) tiles += ceil_div(len[i], geo.tq);
   return tiles * geo.n_groups;

@@ -373,7 +373,7 @@ void run_replay_fused(const hcp_ring_replay_desc* d, const ReplayPlan& p, hcp_ri
   L.lse_hs = p.seq;
   L.len = p.len.data();
   if (g_trace.buf != nullptr) {
-    const int64_t blocks = ring_fused_workgroups(L.hq, L.hkv, p.n, p.len.data(), ring_fused_paired(L));
+    const int64_t blocks = ring_fused_workgroups(L.hq, L.hkv, p.n, p.len.data());
     const int stride = ring_trace_words(p.n);
     const size_t need = static_cast<size_t>(blocks) * stride * sizeof(uint32_t);
     require(g_trace.bytes >= need, "trace buffer too small: need " + std::to_string(need) + " bytes");
@@ -1710,10 +1710,7 @@ int hcp_ring_trace_attach(void* buffer, size_t bytes) {
 size_t hcp_ring_trace_record_bytes(const hcp_ring_replay_desc* desc) {
   try {
     const ReplayPlan p = plan_replay(desc, false);
-    // the larger of the two decompositions (head dim 64 may fold KV heads in pairs)
-    int64_t wg = 0;
-    for (bool pair : {false, true})
-      wg = std::max(wg, ring_fused_workgroups(desc->num_q_heads, desc->num_kv_heads, p.n, p.len.data(), pair));
+    const int64_t wg = ring_fused_workgroups(desc->num_q_heads, desc->num_kv_heads, p.n, p.len.data());
     return static_cast<size_t>(wg) * ring_trace_words(p.n) * sizeof(uint32_t);
   } catch (...) {
     return 0;

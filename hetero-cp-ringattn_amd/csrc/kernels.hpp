@@ -70,10 +70,8 @@ struct RingLaunch {
 };
 bool ring_fused_applies(int dtype, int d);
 void launch_ring_fused(const RingLaunch& L, hipStream_t stream);
-// Whether the fused launch of L folds KV heads in pairs (head dim 64, adjacent heads).
-bool ring_fused_paired(const RingLaunch& L);
 // Workgroups of the fused ring launch for this head layout and chunk list.
-int64_t ring_fused_workgroups(int hq, int hkv, int n, const int64_t* len, bool pair);
+int64_t ring_fused_workgroups(int hq, int hkv, int n, const int64_t* len);
 // 32-bit words of one trace record of an n-domain fused ring.
 int ring_trace_words(int n);
 

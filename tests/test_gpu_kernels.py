@@ -19,9 +19,6 @@ pytestmark = pytest.mark.gpu
 
 OUT_TOL = 2e-2
 LSE_TOL = 1e-3
-# The paired head-dim-64 kernels are switched off in the library (an unexplained GPU
-# fault in a 32k head-dim-64 run); their parity cases run the zero-padded kernels.
-PAIRED_D64 = False
 
 
 def dev_bits(bits: np.ndarray, dtype=torch.bfloat16):
@@ -75,13 +72,13 @@ BLOCK_CASES = [
     # head per workgroup) and 6 at D=128 (two per workgroup)
     ("qwen2_0p5b_rep7_d64", 150, 300, 14, 2, 64, 150, 0, True, torch.bfloat16),
     ("gqa6_d128", 120, 260, 12, 2, 128, 140, 0, True, torch.bfloat16),
-    # head dim 64 with adjacent KV heads: two KV heads per tile row (paired kernels), one
-    # to four query heads per KV head and workgroup half; an odd KV head count stays
-    # zero-padded
-    ("d64_pair_gqa4_causal_past", 300, 700, 16, 4, 64, 650, 0, True, torch.bfloat16),
-    ("d64_pair_rep8_two_groups", 96, 517, 16, 2, 64, 600, 100, True, torch.bfloat16),
-    ("d64_pair_rep2_noncausal_f16", 160, 1000, 8, 4, 64, 0, 0, False, torch.float16),
-    ("d64_odd_kv_heads_padded", 150, 260, 6, 3, 64, 140, 0, True, torch.bfloat16),
+    # head dim 64 (the half-width instantiation: MFMAs on the first 64 dims of the
+    # zero-padded 128-dim rows) across GQA ratios, causal offsets, fp16 without masking
+    # and an odd KV head count
+    ("d64_gqa4_causal_past", 300, 700, 16, 4, 64, 650, 0, True, torch.bfloat16),
+    ("d64_rep8_two_groups", 96, 517, 16, 2, 64, 600, 100, True, torch.bfloat16),
+    ("d64_rep2_noncausal_f16", 160, 1000, 8, 4, 64, 0, 0, False, torch.float16),
+    ("d64_odd_kv_heads", 150, 260, 6, 3, 64, 140, 0, True, torch.bfloat16),
 ]
 
 
@@ -392,7 +389,7 @@ RING_CASES = [
     # D=64 fp16 multi-head case
     ("qwen2_0p5b_d64", [320, 200, 136], 14, 2, 64, torch.bfloat16, 61),
     ("mha_d64_f16", [257, 190], 6, 6, 64, torch.float16, 62),
-    ("d64_pair_gqa4_uneven4", [300, 77, 500, 123], 16, 4, 64, torch.bfloat16, 63),
+    ("d64_gqa4_uneven4", [300, 77, 500, 123], 16, 4, 64, torch.bfloat16, 63),
     ("d64_odd_kv_padded", [200, 150], 3, 3, 64, torch.bfloat16, 64),
 ]
 
@@ -1352,11 +1349,12 @@ def test_traced_fused_replay_statistics_and_perf_log(gpu, causal, tmp_path):
 
 
 @pytest.mark.parametrize("schedule", ["auto", "per_step"])
-def test_d64_paired_and_zero_padded_layouts_agree(gpu, schedule):
+def test_d64_token_major_and_head_major_layouts_agree(gpu, schedule):
     # The same Qwen2-0.5B-shaped ring (14 q / 2 kv heads, D=64) with token-major K/V
-    # (adjacent heads: two KV heads per tile row) and with head-major K/V (zero-padded
-    # to 128): both within tolerance of the restatement of ring_attention and of each
-    # other, the paired one traced (its workgroup count is the paired decomposition's).
+    # (both KV heads in one row of the view) and with head-major K/V: both within
+    # tolerance of the restatement of ring_attention and of each other, the token-major
+    # one traced (its workgroup count is the decomposition's: one query head per group,
+    # 256 rows per workgroup).
     chunks, hq, hkv, d = [700, 300, 500], 14, 2, 64
     s = sum(chunks)
     (q, k, v), (q32, k32, v32) = draw(65, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
@@ -1370,7 +1368,7 @@ def test_d64_paired_and_zero_padded_layouts_agree(gpu, schedule):
         assert np.abs(o.float().cpu().numpy() - ro[0].numpy()).max() <= OUT_TOL
         assert np.abs(l.cpu().numpy() - rl[0].numpy()).max() <= LSE_TOL
     assert (o1.float() - o2.float()).abs().max().item() <= OUT_TOL
-    if schedule == "auto" and PAIRED_D64:
+    if schedule == "auto":
         buf = torch.zeros(H.trace_record_bytes(torch.bfloat16, hq, hkv, d, chunks), dtype=torch.uint8, device="cuda")
         H.trace_attach(buf)
         try:
@@ -1379,5 +1377,5 @@ def test_d64_paired_and_zero_padded_layouts_agree(gpu, schedule):
         finally:
             H.trace_attach(None)
         assert torch.equal(o3, o1)
-        # paired: one KV pair, 7 query heads per KV head (one per group), 128 rows per workgroup
-        assert launch["workgroups"] == sum(-(-c // 128) for c in chunks) * 7
+        # 14 head groups of one query head, 256 rows per workgroup
+        assert launch["workgroups"] == sum(-(-c // 256) for c in chunks) * 14
