@@ -635,10 +635,13 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   frag qf[KS];
   {
     const uint16_t* qbase = qv + head * q_hs + static_cast<int64_t>(wq0) * q_ss;
-    // The range ends at the view's last element (row lq - 1, dim dn - 1): the fragment
-    // loads cover DW dims of every row, so with dn < DW a range of whole rows would let
-    // the last row of the last head read up to 2 (DW - dn) bytes past the end of Q.
-    const auto qr = make_rsrc(qbase, lq > wq0 ? (static_cast<int64_t>(lq - wq0 - 1) * q_ss + dn) * 2 : 0);
+    // The range covers the wave's own rows (at most 32) and ends at the last one's
+    // element dn - 1: the fragment loads cover DW dims of every row, so with dn < DW a
+    // range of whole rows would let the last row of the last head read up to
+    // 2 (DW - dn) bytes past the end of Q; and a range from here to the chunk's end
+    // could pass the descriptor's 2 GiB limit on long chunks.
+    const int q_rows = min(lq - wq0, 32);
+    const auto qr = make_rsrc(qbase, q_rows > 0 ? (static_cast<int64_t>(q_rows - 1) * q_ss + dn) * 2 : 0);
     const int32_t qoff = (lcol * static_cast<int32_t>(q_ss) + lhalf * 8) * 2;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
