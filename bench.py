@@ -697,7 +697,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
-    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "qwen64_32k", "strategies", "fp32"], default=None,
+    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "qwen64_32k", "strategies", "fp32", "merge"], default=None,
                     help="run one prefill leg alone and print its JSON object (profiling)")
     ap.add_argument("--trace", action="store_true",
                     help="with --leg: also run traced launches (per-workgroup records) and summarise them")
@@ -722,6 +722,12 @@ def main():
     if args.leg in ("qwen64", "qwen64_32k"):
         c = QWEN64 if args.leg == "qwen64" else QWEN64_32K
         print(json.dumps({"leg": args.leg, **bench_qwen_d64(H, torch, args.steps, args.warmup, c)}), flush=True)
+        return
+    if args.leg == "merge":
+        m = bench_merge(H, torch, args.steps, args.warmup)
+        print(json.dumps({"leg": "merge", "value": round(m["merge_gbs"], 1), "unit": "GB/s",
+                          "ms_per_step": round(m["merge_ms"], 4), "frac_hbm": round(m["merge_gbs"] / PEAK_HBM_GBS, 4),
+                          "bytes": m["merge_bytes"]}), flush=True)
         return
     if args.leg == "fp32":
         print(json.dumps({"leg": "fp32", **bench_fp32(H, torch, args.steps, args.warmup)}), flush=True)
