@@ -1349,6 +1349,26 @@ def test_traced_fused_replay_statistics_and_perf_log(gpu, causal, tmp_path):
 
 
 @pytest.mark.parametrize("schedule", ["auto", "per_step"])
+@pytest.mark.parametrize("d", [8, 16, 24, 40, 56, 64, 72])
+def test_ring_replay_head_dims_around_the_half_width_kernel(gpu, d, schedule):
+    # Head dims up to 64 take the half-width instantiation (the MFMAs of the first 64 dims
+    # of the zero-padded 128-dim rows), 72 the full one: every multiple of 8 below 64 and
+    # the boundary, token-major Q/K/V, uneven causal chunks, GQA 2, fused and per step,
+    # against the f64 closed form.
+    chunks, hq, hkv = [150, 97, 70], 4, 2
+    s = sum(chunks)
+    (q, k, v), (q32, k32, v32) = draw(70 + d, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.bfloat16)
+    out, lse = H.ring_attention_replay(q.permute(1, 0, 2), k.permute(1, 0, 2), v.permute(1, 0, 2), chunks,
+                                       schedule=schedule)
+    assert H.last_path() == ("ring_fused" if schedule == "auto" else "mfma")
+    torch.cuda.synchronize()
+    pos = np.arange(s)
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, pos, pos, 1 / math.sqrt(d))
+    assert np.abs(out.float().cpu().numpy() - ref_o.transpose(1, 0, 2)).max() <= OUT_TOL
+    assert np.abs(lse.cpu().numpy() - ref_l.T).max() <= LSE_TOL
+
+
+@pytest.mark.parametrize("schedule", ["auto", "per_step"])
 def test_d64_token_major_and_head_major_layouts_agree(gpu, schedule):
     # The same Qwen2-0.5B-shaped ring (14 q / 2 kv heads, D=64) with token-major K/V
     # (both KV heads in one row of the view) and with head-major K/V: both within
