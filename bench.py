@@ -697,7 +697,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
-    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "qwen64_32k", "strategies", "fp32", "merge"], default=None,
+    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "qwen64_32k", "strategies", "fp32", "merge", "staging"],
+                    default=None,
                     help="run one prefill leg alone and print its JSON object (profiling)")
     ap.add_argument("--trace", action="store_true",
                     help="with --leg: also run traced launches (per-workgroup records) and summarise them")
@@ -722,6 +723,12 @@ def main():
     if args.leg in ("qwen64", "qwen64_32k"):
         c = QWEN64 if args.leg == "qwen64" else QWEN64_32K
         print(json.dumps({"leg": args.leg, **bench_qwen_d64(H, torch, args.steps, args.warmup, c)}), flush=True)
+        return
+    if args.leg == "staging":
+        g = bench_staged(H, torch, args.steps, args.warmup, full_prefill=False)
+        print(json.dumps({"leg": "staging", "value": round(g["scatter_gbs"], 1), "unit": "GB/s",
+                          "ms_per_step": round(g["scatter_ms"], 4), "gather_gbs": round(g["gather_gbs"], 1),
+                          "bit_exact": g["bit_exact"]}), flush=True)
         return
     if args.leg == "merge":
         m = bench_merge(H, torch, args.steps, args.warmup)
