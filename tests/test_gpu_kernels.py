@@ -839,6 +839,32 @@ def test_ring_replay_strategy_matches_full_attention(gpu, case, strategy, schedu
         assert np.abs(out - ro[0].numpy()).max() <= 1e-4
 
 
+def test_reference_uneven_3to1_every_strategy(gpu):
+    # The reference's own strategy check at its own size (ring.rs:3168-3224 through
+    # run_uneven_ring_attention, ring.rs:3226-3364): S=4096 split 3:1, 8 heads, head dim
+    # 128, fp32, vanilla / striped / zigzag, each against full attention after the
+    # inverse permutation -- mean |delta| < 1e-4 there, and no NaN; here also the max.
+    chunks, hq, hkv, d = [3072, 1024], 8, 8, 128
+    s = sum(chunks)
+    (q, k, v), (q32, k32, v32) = draw(66, [(s, hq, d), (s, hkv, d), (s, hkv, d)], torch.float32)
+    p = np.arange(s)
+    ref_o, ref_l = C.attention_f64(q32, k32, v32, p, p, 1 / math.sqrt(d))
+    ref_o = ref_o.transpose(1, 0, 2)
+    for strategy in ("vanilla", "striped", "zigzag"):
+        pos, inv = _strategy_rows(chunks, strategy)
+        rows = torch.tensor(sum(pos, []), device="cuda")
+        qd, kd, vd = (x.index_select(0, rows).permute(1, 0, 2) for x in (q, k, v))
+        out, lse = H.ring_attention_replay(qd, kd, vd, chunks, strategy=strategy)
+        torch.cuda.synchronize()
+        assert H.fetch_device_errors() == 0
+        out = out.cpu().numpy()[:, inv]
+        lse = lse.cpu().numpy()[:, inv]
+        assert np.isfinite(out).all() and np.isfinite(lse).all(), strategy
+        err = np.abs(out - ref_o)
+        assert err.mean() < 1e-4 and err.max() <= 1e-4, (strategy, err.mean(), err.max())
+        assert np.abs(lse - ref_l.T).max() <= 1e-4, strategy
+
+
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
 def test_fp32_replay_one_launch(gpu, causal):
     # fp32 (the reference's CPU dtype): AUTO runs the whole replay as one block on the
