@@ -755,37 +755,39 @@ def main():
     pre = bench_prefill(H, torch, args.steps, args.warmup)
     log(f"c3 prefill {pre['tflops']:.1f} TFLOP/s ({pre['ms_step']:.3f} ms/step, {pre['path']})")
     extra = {}
-    if not args.no_extra:
+
+    def guarded(keys, fn):
+        # One extra leg: a failure is reported inside the JSON line under the leg's keys
+        # (and logged), so it cannot take the headline figure with it.
+        try:
+            extra.update(fn())
+        except Exception as e:  # noqa: BLE001
+            msg = f"{type(e).__name__}: {e}"
+            log(f"extra leg {'/'.join(keys)} failed: {msg}")
+            extra.update({k: {"error": msg} for k in keys})
+
+    def leg_per_step():
         # the same c3 replay under the per-step schedule (one grouped launch per ring step)
         per = bench_prefill(H, torch, args.steps, args.warmup, schedule="per_step", tensors=pre["tensors"])
         log(f"c3 prefill per step {per['tflops']:.1f} TFLOP/s")
-        c3_per_step = dict(workload="c3 with schedule per_step (one grouped launch per ring step, fp32 state "
-                                    "in HBM between steps)", **prefill_summary(per),
-                           max_abs_diff_vs_fused=round((per["out"].float() - pre["out"].float()).abs().max().item(),
-                                                       5))
-        del per
-        c2 = bench_c2(H, torch, args.steps, args.warmup)
-        qwen = bench_qwen_d64(H, torch, args.steps, args.warmup)
-        qwen32 = bench_qwen_d64(H, torch, args.steps, args.warmup, QWEN64_32K)
+        diff = (per["out"].float() - pre["out"].float()).abs().max().item()
+        return dict(c3_per_step=dict(workload="c3 with schedule per_step (one grouped launch per ring step, fp32 "
+                                              "state in HBM between steps)", **prefill_summary(per),
+                                     max_abs_diff_vs_fused=round(diff, 5)))
+
+    def leg_decode():
         dec = bench_decode(H, torch, args.steps, args.warmup)
         log(f"c4 decode {dec['gbs']:.1f} GB/s")
+        return dict(paged_decode={"workload": "c4: B=64, ctx 16384 in [8192,5120,3072], 32q/8kv, D=128, bf16, bs=16",
+                                  "value": round(dec["gbs"], 1), "unit": "GB/s",
+                                  "ms_per_step": round(dec["ms_step"], 4),
+                                  "frac_hbm": round(dec["gbs"] / PEAK_HBM_GBS, 4), "bytes": dec["bytes"],
+                                  "chunk0_kernel_gbs": round(dec["chunk0_gbs"], 1), "finite": dec["finite"]})
+
+    def leg_staging():
         stg = bench_staged(H, torch, args.steps, args.warmup)
-        mrg = bench_merge(H, torch, args.steps, args.warmup)
-        strat = bench_strategies(H, torch, pre["tensors"], args.steps, args.warmup)
-        wire = bench_wire(H, torch, pre["tensors"], args.steps, args.warmup)
-        log(f"wire {wire}")
-        qkv = bench_qkv(H, torch, args.steps, args.warmup)
-        log(f"qkv {qkv}")
-        f32 = bench_fp32(H, torch, args.steps, args.warmup)
-        log(f"fp32 {f32}")
-        log(f"c3 strategies {strat}")
-        log(f"c3 lse merge {mrg['merge_gbs']:.1f} GB/s")
         log(f"c5 gather {stg['gather_gbs']:.1f} GB/s, prefill {stg.get('prefill_tflops', 0):.1f} TFLOP/s")
-        extra = dict(
-            paged_decode={"workload": "c4: B=64, ctx 16384 in [8192,5120,3072], 32q/8kv, D=128, bf16, bs=16",
-                          "value": round(dec["gbs"], 1), "unit": "GB/s", "ms_per_step": round(dec["ms_step"], 4),
-                          "frac_hbm": round(dec["gbs"] / PEAK_HBM_GBS, 4), "bytes": dec["bytes"],
-                          "chunk0_kernel_gbs": round(dec["chunk0_gbs"], 1), "finite": dec["finite"]},
+        return dict(
             kv_staging={"workload": "c5: gather of all 8 chunks (131072 tokens, 8 kv heads, D=128, bf16) from a "
                                     "permuted bs=16 block pool",
                         "value": round(stg["gather_gbs"], 1), "unit": "GB/s", "ms": round(stg["gather_ms"], 4),
@@ -800,24 +802,54 @@ def main():
                                  "kernel_path": stg.get("prefill_path"), "finite": stg.get("prefill_finite"),
                                  "sampled_rows": stg.get("sampled_rows"),
                                  "sampled_max_abs_err_out": stg.get("sampled_err_out"),
-                                 "sampled_max_abs_err_lse": stg.get("sampled_err_lse")},
-            c2_prefill=c2,
-            qwen2_0p5b_d64_8k=qwen,
-            qwen2_0p5b_d64_32k=qwen32,
-            c3_per_step=c3_per_step,
-            lse_merge={"workload": "c3 ring partials of the 4 target domains (10 x [32, L, 128] fp32 + LSE) "
-                                   "-> bf16 rows + fp32 LSE, one hcp_ring_lse_merge per domain",
-                       "value": round(mrg["merge_gbs"], 1), "unit": "GB/s", "ms_per_step": round(mrg["merge_ms"], 4),
-                       "frac_hbm": round(mrg["merge_gbs"] / PEAK_HBM_GBS, 4), "bytes": mrg["merge_bytes"]},
-            strategies=dict(workload="c3 ring prefill with Striped / ZigZag positions (same causal FLOPs)", **strat),
-            kv_frame=wire,
-            qkv_rope=qkv,
-            fp32=f32,
-        )
+                                 "sampled_max_abs_err_lse": stg.get("sampled_err_lse")})
+
+    def leg_merge():
+        mrg = bench_merge(H, torch, args.steps, args.warmup)
+        log(f"c3 lse merge {mrg['merge_gbs']:.1f} GB/s")
+        return dict(lse_merge={"workload": "c3 ring partials of the 4 target domains (10 x [32, L, 128] fp32 + LSE) "
+                                           "-> bf16 rows + fp32 LSE, one hcp_ring_lse_merge per domain",
+                               "value": round(mrg["merge_gbs"], 1), "unit": "GB/s",
+                               "ms_per_step": round(mrg["merge_ms"], 4),
+                               "frac_hbm": round(mrg["merge_gbs"] / PEAK_HBM_GBS, 4), "bytes": mrg["merge_bytes"]})
+
+    def leg_strategies():
+        strat = bench_strategies(H, torch, pre["tensors"], args.steps, args.warmup)
+        log(f"c3 strategies {strat}")
+        return dict(strategies=dict(workload="c3 ring prefill with Striped / ZigZag positions (same causal FLOPs)",
+                                    **strat))
+
+    def leg_logged(key, fn):
+        def run():
+            r = fn()
+            log(f"{key} {r}")
+            return {key: r}
+        return run
+
+    if not args.no_extra:
+        guarded(["c3_per_step"], leg_per_step)
+        guarded(["c2_prefill"], leg_logged("c2_prefill", lambda: bench_c2(H, torch, args.steps, args.warmup)))
+        guarded(["qwen2_0p5b_d64_8k"], leg_logged("qwen2_0p5b_d64_8k",
+                                                  lambda: bench_qwen_d64(H, torch, args.steps, args.warmup)))
+        guarded(["qwen2_0p5b_d64_32k"], leg_logged("qwen2_0p5b_d64_32k",
+                                                   lambda: bench_qwen_d64(H, torch, args.steps, args.warmup,
+                                                                          QWEN64_32K)))
+        guarded(["paged_decode"], leg_decode)
+        guarded(["kv_staging", "staged_prefill_128k"], leg_staging)
+        guarded(["lse_merge"], leg_merge)
+        guarded(["strategies"], leg_strategies)
+        guarded(["kv_frame"], leg_logged("kv_frame", lambda: bench_wire(H, torch, pre["tensors"], args.steps,
+                                                                        args.warmup)))
+        guarded(["qkv_rope"], leg_logged("qkv_rope", lambda: bench_qkv(H, torch, args.steps, args.warmup)))
+        guarded(["fp32"], leg_logged("fp32", lambda: bench_fp32(H, torch, args.steps, args.warmup)))
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(torch, pre["tensors"])
-        log(f"cpu baseline {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads")
+        try:
+            cpu = cpu_baseline(torch, pre["tensors"])
+            log(f"cpu baseline {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads")
+        except Exception as e:  # noqa: BLE001 -- reported in the line, like a failed extra leg
+            cpu = {"error": f"{type(e).__name__}: {e}"}
+            log(f"cpu baseline failed: {cpu['error']}")
     line = {
         "metric": METRIC,
         "value": round(pre["tflops"], 2),
