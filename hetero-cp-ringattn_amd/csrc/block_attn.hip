@@ -1503,10 +1503,10 @@ static void launch_general(const BlockLaunch& L, hipStream_t stream) {
   else general_block_kernel<DT, 256><<<grid, kGenRows, 0, stream>>>(a);
 }
 
-// Head dims the head-dim-128 kernel takes: up to 128 in 16-byte columns, zero-padded.
-// Head dim 64 goes this way too: at half the MFMA work wasted it measured 7-29% faster
-// (Llama-3-8B / Qwen2-0.5B heads, 32k ring) than a dedicated head-dim-64 kernel with
-// register-staged 64-key tiles.
+// Head dims the head-dim-128 kernel takes: up to 128 in 16-byte columns, zero-padded in
+// LDS.  Head dims up to 64 run its half-width instantiation (the MFMAs and fragment reads
+// of dims 64-127 not issued); a dedicated head-dim-64 kernel with register-staged 64-key
+// tiles measured 7-29% slower than even the zero-padded full-width form.
 static bool padded_d_ok(int d) { return d > 0 && d <= kD3 && d % 8 == 0; }
 
 // True when the matrix-core kernels handle this shape.
