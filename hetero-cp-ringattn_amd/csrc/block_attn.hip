@@ -344,6 +344,10 @@ __device__ __forceinline__ void write_final_row(void* out, int dtype, int64_t of
 // three (160 KiB of LDS, all of it; V's third buffer gives its loads a super-step more
 // slack).  The kernel also compiles for 64-key tiles with rings of three; 128 keys
 // halve the per-tile barriers, DMA issue and softmax bookkeeping and measured 5% faster.
+// The half-width instantiation (head dims up to 64) keeps 64 dims per LDS row: 8 rows
+// per DMA instruction, swizzles K (r >> 1) & 7 and V 4 ((r >> 1) & 1), 16 KiB tiles
+// (80 KiB of LDS; against 128-dim rows with a zero half, +2.6% on a 32k Qwen2-0.5B
+// ring and +4-6% at 8k; a third K buffer measured 2% slower).
 //
 // Ping-pong.  The work of a tile is split in two phases per wave -- M: the MFMA phase
 // (O^T += V^T P^T of the previous tile, then S^T = K Q^T of this tile: 64 MFMAs fed by
@@ -427,31 +431,34 @@ template <int DT, int G, bool POS, int BK, bool RING, class P, bool TRACE = fals
 __device__ __forceinline__ void pingpong_body(const P& plan) {
   using Ops = MfmaOps<DT>;
   using frag = typename Ops::frag;
-  // D: the LDS row of a K / V tile (128 dims; head dims below it zero-padded by the DMA).
-  // DW = DWN: the head dims a wave folds.  DWN = 64 (head dims up to 64): the rows,
-  // tiles, DMA, swizzles and transposing reads of the 128-dim kernel, with the MFMAs and
-  // fragment reads of the zero half not issued.
+  // DW = DWN: the head dims a wave folds and the width of a K / V row in LDS (head dims
+  // below it zero-padded by the DMA).  DWN = 64 (head dims up to 64) runs the same loop
+  // on 128-byte LDS rows: half the LDS, half the DMA instructions, its own swizzles.
   static_assert(DWN == kD3 || DWN == kD3 / 2, "dims folded: 128 or 64");
-  constexpr int D = kD3;
   constexpr int DW = DWN;
   static_assert(kWaves % G == 0, "heads per group must divide the waves");
   constexpr int TB = kWaves / G;
   constexpr int TQ = 32 * TB;
   constexpr int KS = DW / 16;
   constexpr int DB = DW / 32;
-  constexpr int kDmaPerWave = BK / 4 / kWaves;  // 1 KiB DMA instructions per wave per tile (K or V)
-  constexpr int kTile = BK * D * 2;              // bytes of one K or V tile
+  // PW: bytes of a K / V row in LDS, the dims a wave folds (256 for 128 dims, 128 for
+  // the half-width kernel); CPR 16-byte chunks per row, RPI rows per 1 KiB DMA.
+  constexpr int PW = DW * 2;
+  constexpr int CPR = PW / 16;
+  constexpr int RPI = 1024 / PW;
+  constexpr int kDmaPerWave = BK / RPI / kWaves;  // 1 KiB DMA instructions per wave per tile (K or V)
+  constexpr int kTile = BK * PW;                 // bytes of one K or V tile
   constexpr int NKB = BK / 32;                   // 32-key blocks of S^T per tile
   constexpr int NPS = BK / 16;                   // 16-key steps of the PV product per tile
   // LDS buffers per ring: 3 + 3 tiles of 64 keys (96 KiB); 2 K + 3 V tiles of 128 keys
-  // (160 KiB; two V buffers measured 0.4% slower).
+  // (160 KiB at 128 dims, 80 KiB at 64; two V buffers measured 0.4% slower).
   constexpr int NBK = BK == 64 ? 3 : 2;
   constexpr int NBV = 3;
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[NBK * BK * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[NBV * BK * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[NBK * BK * PW / 2];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[NBV * BK * PW / 2];
   // Two small reduction arrays live at the start of the last V buffer, which the DMA
   // first writes in super-step 1, after every read of them.
-  int* const lim_red = reinterpret_cast<int*>(v_lds + (NBV - 1) * BK * D);
+  int* const lim_red = reinterpret_cast<int*>(v_lds + (NBV - 1) * BK * PW / 2);
   int* const simd_of = lim_red + kWaves;
 
   [[maybe_unused]] uint64_t trace_t0 = 0, trace_c0 = 0;
@@ -570,7 +577,12 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     }
   };
 
-  // ---- DMA set-up: wave w fills rows 8w .. 8w+7 of every K and V tile ----
+  // Swizzles (16-byte chunk index XOR, per row) that make the fragment reads bank-
+  // conflict free: 256-byte rows K r & 15, V 4 (r & 3); 128-byte rows K (r >> 1) & 7,
+  // V 4 ((r >> 1) & 1) (the row's parity already spreads rows over the two bank halves).
+  auto swz_k = [](int r) __attribute__((always_inline)) { return PW == 256 ? (r & 15) : ((r >> 1) & 7); };
+  auto swz_v = [](int r) __attribute__((always_inline)) { return PW == 256 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); };
+  // ---- DMA set-up: wave w fills rows BK/8 w .. BK/8 w + BK/8 - 1 of every K and V tile ----
   const uint16_t* kbase = kv + kvh * k_hs;
   const uint16_t* vbase = vv + kvh * v_hs;
   const uint32_t k_lds0 = lds_offset(k_lds) + wave * (kDmaPerWave * 1024);
@@ -578,11 +590,11 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   uint32_t k_voff[kDmaPerWave], v_voff[kDmaPerWave];
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
-    const int r = (wave * kDmaPerWave + j) * 4 + (lane >> 4);
-    const int p = lane & 15;
+    const int r = (wave * kDmaPerWave + j) * RPI + lane / CPR;
+    const int p = lane % CPR;
     // global chunk p ^ swz(r) of row r; chunks past the head dim get an offset beyond any
     // tile's records (tiles stay below 2^31 bytes), so the DMA writes zeros there
-    const int kc = p ^ (r & 15), vc = p ^ (4 * (r & 3));
+    const int kc = p ^ swz_k(r), vc = p ^ swz_v(r);
     k_voff[j] = kc * 8 < dn ? static_cast<uint32_t>(r * k_ss * 2 + (kc << 4)) : 0x80000000u;
     v_voff[j] = vc * 8 < dn ? static_cast<uint32_t>(r * v_ss * 2 + (vc << 4)) : 0x80000000u;
   }
@@ -655,13 +667,15 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
   // K fragment s of a lane sits at k_rd0 ^ (s << 5) in a tile: (lhalf + 2s) ^ (krow & 15)
   // changes only bits 1-3 of the 16-byte column index with s, and tile bases are
   // 1 KiB-aligned, so the XOR commutes with adding the base.
-  const uint32_t k_rd0 = krow * (D * 2) + ((lhalf ^ (krow & 15)) << 4);
+  const uint32_t k_rd0 = krow * PW + ((lhalf ^ swz_k(krow)) << 4);
   const int g16 = lane >> 4, sl = lane & 15;
   uint32_t v_rd[DB];
 #pragma unroll
   for (int b = 0; b < DB; ++b) {  // 32-dim block of the LDS row
-    v_rd[b] = (8 * (g16 >> 1) + (sl >> 2)) * (D * 2) +
-               ((4 * (b ^ (sl >> 2)) + 2 * (g16 & 1) + ((sl & 3) >> 1)) << 4) + 8 * (sl & 1);
+    // row 8 (g16 >> 1) + (sl >> 2) of a 16-key step (and 4 rows on), so swz_v of that
+    // row is 4 (sl >> 2) for 256-byte rows and 4 ((sl >> 3) & 1) for 128-byte ones
+    const int vs = PW == 256 ? (sl >> 2) : ((sl >> 3) & 1);
+    v_rd[b] = (8 * (g16 >> 1) + (sl >> 2)) * PW + ((4 * (b ^ vs) + 2 * (g16 & 1) + ((sl & 3) >> 1)) << 4) + 8 * (sl & 1);
   }
   const uint32_t k_lds_off = lds_offset(k_lds);
   const char* v_lds_c = reinterpret_cast<const char*>(v_lds);
@@ -706,9 +720,9 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
     for (int s = 0; s < NPS; ++s) {
 #pragma unroll
       for (int b = 0; b < DB; ++b) {
-        const char* p0 = vl + v_rd[b] + s * 16 * D * 2;
+        const char* p0 = vl + v_rd[b] + s * 16 * PW;
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0 + 4 * D * 2));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p0 + 4 * PW));
         const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
         oacc[b] = Ops::mma(as_frag<frag>(u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}), pf[s], oacc[b]);
       }
@@ -726,7 +740,7 @@ __device__ __forceinline__ void pingpong_body(const P& plan) {
 #pragma unroll
       for (int b = 0; b < NKB; ++b) {
         const frag kf = as_frag<frag>(*reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
-            static_cast<uintptr_t>(ks + b * 32 * D * 2)));
+            static_cast<uintptr_t>(ks + b * 32 * PW)));
         sacc[b] = Ops::mma(kf, qf[s], sacc[b]);
       }
     }

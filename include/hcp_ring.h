@@ -128,8 +128,8 @@ int hcp_ring_fetch_device_errors(void* stream, int* flags);
  * With accumulate=1, o/lse hold a running partial on entry and are replaced by the
  * merge of it with this block (the rm=lse, rs=1, obh=o re-entry of ring.rs:585-587).
  * dtype: BF16 or F16 (matrix-core path: head_dim any multiple of 8 up to 128, run by
- * the head-dim-128 kernel with the columns past head_dim zero-padded, up to 64 with
- * the MFMAs of the first 64 dims only) or
+ * the head-dim-128 kernel with the columns past head_dim zero-padded, up to 64 by its
+ * half-width form, 64 dims per LDS row) or
  * F32 (any head_dim <= 256; F16/BF16 with other head dims take the same general
  * kernel).
  * ------------------------------------------------------------------------------- */
