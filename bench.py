@@ -8,7 +8,8 @@ pair, each folding its source into the domain's running state, the last one writ
 the output rows) through ``hcp_ring_prefill_replay``, inputs resident in HBM.  ``value`` counts
 algorithmic FLOPs of causal pairs only: 2 GEMMs x 2 x D x Hq x S(S+1)/2.
 
-Also reported on the same line: paged decode GB/s (config c4), KV staging gather GB/s
+Also reported on the same line: paged decode GB/s (config c4) and the growth-sharded
+decode Q-ring at c4's shape, KV staging gather GB/s
 and the staged 128k prefill (config c5), the LSE merge GB/s, the c3 prefill with Striped
 and ZigZag positions, the KV wire-frame pack, the fused QKV + RoPE + KV append, fp32 on
 the matrix cores (c1 and an 8k block), a roofline object for the
@@ -524,6 +525,59 @@ def bench_decode(H, torch, steps: int, warmup: int):
     return res
 
 
+def bench_decode_ring(H, torch, steps: int, warmup: int):
+    """One decode step of the Q-ring with growth sharding (hcp_decode_ring_replay,
+    ring.rs:665-818, owner rule ring.rs:1930-1936) at c4's shape: 64 sequences of 16384
+    tokens, the first 16288 prefilled over c4's three domains (the last domain's chunk
+    96 shorter), the last 96 decode tokens each in its owner's shard (p mod 3).  Each
+    domain's shard is its own permuted bs=16 block table; one replay runs the paged
+    decode over every shard and the journey-order merge.  Synthetic K/V: the timing and
+    the bytes, not the values, are what this leg measures (parity: the GPU tests)."""
+    c = C4
+    b, hq, hkv, d, bs = c["batch"], c["hq"], c["hkv"], c["d"], c["bs"]
+    n = len(c["chunks"])
+    dec = 96
+    prefill = c["ctx"] - dec
+    chunks = list(c["chunks"])
+    chunks[-1] -= dec
+    lens = [chunks[dom] + sum(1 for p in range(prefill, c["ctx"]) if p % n == dom) for dom in range(n)]
+    nblk = [-(-L // bs) for L in lens]
+    nb = b * sum(nblk) + 1
+    q = torch.empty(b, hq, d, dtype=torch.bfloat16, device="cuda")
+    pool = torch.empty(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.synth_normals(c["seed"] + 7, 0, q.numel(), q)
+    H.synth_normals(c["seed"] + 7, q.numel(), pool.numel(), pool)
+    perm = lcg_permutation(c["seed"] + 7, nb)
+    shards, cur = [], 0
+    for dom in range(n):
+        tab = torch.tensor(perm[cur: cur + b * nblk[dom]], dtype=torch.int32, device="cuda").view(b, nblk[dom])
+        cur += b * nblk[dom]
+        shards.append((tab, torch.full((b,), lens[dom], dtype=torch.int32, device="cuda"), lens[dom]))
+    out = torch.empty(b, hq, d, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(b, hq, dtype=torch.float32, device="cuda")
+    # the replay's workspace (split partials and the N domain partials), allocated once
+    ws = torch.empty(max(H.decode_ring_workspace_size(q, pool, shards), 1), dtype=torch.uint8, device="cuda")
+
+    def step():
+        H.decode_ring_replay(q, pool, shards, 0, out=out, lse_out=lse, workspace=ws)
+
+    log(f"decode ring warmup x{warmup}")
+    for _ in range(warmup):
+        step()
+    log(f"decode ring timed x{steps}")
+    ms = time_cuda(torch, step, steps)
+    kv_bytes = 2 * b * sum(lens) * hkv * d * 2
+    alg = kv_bytes + q.numel() * 2 + 2 * n * b * hq * (d + 1) * 4 + b * sum(nblk) * 4 + out.numel() * 2 + lse.numel() * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+    res = dict(workload=f"f1 decode Q-ring: B={b}, ctx {c['ctx']} growth-sharded over {n} domains "
+                        f"(prefill {chunks}, {dec} decode tokens by owner p mod {n}), {hq}q/{hkv}kv, D={d}, bf16, "
+                        f"bs={bs}; one hcp_decode_ring_replay (paged decode per shard + journey-order merge)",
+               value=round(gbs, 1), unit="GB/s", ms_per_step=round(ms, 4), frac_hbm=round(gbs / PEAK_HBM_GBS, 4),
+               bytes=alg, finite=bool(torch.isfinite(out.float()).all().item()))
+    del pool
+    return res
+
+
 # ------------------------------------------------------------------ c5 staging ----
 def bench_staged(H, torch, steps: int, warmup: int, full_prefill: bool = True):
     c = C5
@@ -697,7 +751,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
-    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "qwen64_32k", "strategies", "fp32", "merge", "staging"],
+    ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "qwen64_32k", "strategies", "fp32", "merge", "staging",
+                                      "decode_ring"],
                     default=None,
                     help="run one prefill leg alone and print its JSON object (profiling)")
     ap.add_argument("--trace", action="store_true",
@@ -735,6 +790,9 @@ def main():
         print(json.dumps({"leg": "merge", "value": round(m["merge_gbs"], 1), "unit": "GB/s",
                           "ms_per_step": round(m["merge_ms"], 4), "frac_hbm": round(m["merge_gbs"] / PEAK_HBM_GBS, 4),
                           "bytes": m["merge_bytes"]}), flush=True)
+        return
+    if args.leg == "decode_ring":
+        print(json.dumps({"leg": "decode_ring", **bench_decode_ring(H, torch, args.steps, args.warmup)}), flush=True)
         return
     if args.leg == "fp32":
         print(json.dumps({"leg": "fp32", **bench_fp32(H, torch, args.steps, args.warmup)}), flush=True)
@@ -835,6 +893,8 @@ def main():
                                                    lambda: bench_qwen_d64(H, torch, args.steps, args.warmup,
                                                                           QWEN64_32K)))
         guarded(["paged_decode"], leg_decode)
+        guarded(["decode_ring"], leg_logged("decode_ring", lambda: bench_decode_ring(H, torch, args.steps,
+                                                                                   args.warmup)))
         guarded(["kv_staging", "staged_prefill_128k"], leg_staging)
         guarded(["lse_merge"], leg_merge)
         guarded(["strategies"], leg_strategies)

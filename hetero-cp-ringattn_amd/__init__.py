@@ -559,6 +559,18 @@ def _shards(shards):
     return arr
 
 
+def _ring_desc(q, pool, scale=None):
+    b, hq, d = q.shape
+    return DecodeDesc(dtype_code(q.dtype), b, hq, pool.shape[3], d, 0, 0, 0, 0, 0,
+                      scale if scale is not None else 1.0 / math.sqrt(d))
+
+
+def decode_ring_workspace_size(q, pool, shards) -> int:
+    """Workspace bytes hcp_decode_ring_replay needs for these shards."""
+    desc, pp, arr = _ring_desc(q, pool), paged_pool(pool), _shards(shards)
+    return lib().hcp_decode_ring_workspace_size(ctypes.byref(desc), ctypes.byref(pp), len(shards), arr)
+
+
 def decode_ring_replay(q, pool, shards, seed_domain, scale=None, out=None, lse_out=None, workspace=None,
                        stream=None):
     """ring_decode_attention (ring.rs:665-818) for a batch on one GPU.
@@ -568,8 +580,7 @@ def decode_ring_replay(q, pool, shards, seed_domain, scale=None, out=None, lse_o
     Returns (out [B, Hq, D] in q's dtype, lse [B, Hq] fp32)."""
     torch = _torch()
     b, hq, d = q.shape
-    desc = DecodeDesc(dtype_code(q.dtype), b, hq, pool.shape[3], d, 0, 0, 0, 0, 0,
-                      scale if scale is not None else 1.0 / math.sqrt(d))
+    desc = _ring_desc(q, pool, scale)
     pp = paged_pool(pool)
     arr = _shards(shards)
     n = len(shards)
