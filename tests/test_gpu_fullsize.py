@@ -1,5 +1,5 @@
-"""Parity at the full benchmark sizes (c2 8k and c3 32k ring prefill, c4 paged decode,
-c5 128k staging and prefill), through properties that do not need the whole closed form: sampled query rows
+"""Parity at the full benchmark sizes (c2 8k and c3 32k ring prefill, c4 paged decode and
+the growth-sharded decode Q-ring at its shape, c5 128k staging and prefill), through properties that do not need the whole closed form: sampled query rows
 against the f64 closed form, order invariance between strategies, bit-exactness against
 an independent GPU gather (torch advanced indexing) and scatter/gather round trips.
 Inputs come from the device LCG generator with the bench's seeds."""
@@ -199,6 +199,55 @@ def test_c4_full_paged_decode_every_sequence(gpu):
         ro = torch.matmul(torch.exp(sc - rl.unsqueeze(2)), v)                                  # [hkv, rep, d]
         err_o = max(err_o, (out[b] - ro.reshape(hq, d)).abs().max().item())
         err_l = max(err_l, (lse[b] - rl.reshape(hq)).abs().max().item())
+    assert err_o <= OUT_TOL and err_l <= LSE_TOL, (err_o, err_l)
+
+
+def test_decode_ring_growth_sharded_at_c4_shape(gpu):
+    # The decode Q-ring (ring.rs:665-818) at c4's shape with growth sharding
+    # (ring.rs:1930-1936): 64 sequences of 16384 tokens, the last 96 decode tokens each
+    # in its owner's shard (p mod 3), every domain shard with its own permuted block
+    # table.  From two seeds, every sequence's output equals the f64 closed form over the
+    # union of its shards (the whole context).
+    batch, hq, hkv, d, bs, ctx, dec, n = 64, 32, 8, 128, 16, 16384, 96, 3
+    chunks = [8192, 5120, 3072 - dec]
+    prefill = ctx - dec
+    lens = [chunks[dom] + sum(1 for p in range(prefill, ctx) if p % n == dom) for dom in range(n)]
+    nblk = [-(-L // bs) for L in lens]
+    nb = batch * sum(nblk) + 1
+    q = torch.empty(batch, hq, d, dtype=torch.bfloat16, device="cuda")
+    pool = torch.empty(2, nb, bs, hkv, d, dtype=torch.bfloat16, device="cuda")
+    H.synth_normals(48, 0, q.numel(), q)
+    H.synth_normals(48, q.numel(), pool.numel(), pool)
+    perm = I.permuted_block_table(48, nb)
+    shards, tabs, cur = [], [], 0
+    for dom in range(n):
+        tab = perm[cur:cur + batch * nblk[dom]].reshape(batch, nblk[dom])
+        cur += batch * nblk[dom]
+        tabs.append(torch.from_numpy(tab.astype(np.int64)))
+        shards.append((torch.from_numpy(np.ascontiguousarray(tab)).cuda(),
+                       torch.full((batch,), lens[dom], dtype=torch.int32, device="cuda"), lens[dom]))
+    results = []
+    for seed in (0, 2):
+        out, lse = H.decode_ring_replay(q, pool, shards, seed)
+        torch.cuda.synchronize()
+        assert H.fetch_device_errors() == 0
+        results.append((out.float().cpu(), lse.cpu()))
+    pool_h, q_h = pool.cpu(), q.cpu().double()
+    rep, scale = hq // hkv, 1 / math.sqrt(d)
+    err_o = err_l = 0.0
+    for b in range(batch):
+        ks, vs = [], []
+        for dom in range(n):
+            ks.append(pool_h[0].index_select(0, tabs[dom][b]).reshape(-1, hkv, d)[:lens[dom]])
+            vs.append(pool_h[1].index_select(0, tabs[dom][b]).reshape(-1, hkv, d)[:lens[dom]])
+        k = torch.cat(ks).double().permute(1, 2, 0)                                            # [hkv, d, ctx]
+        v = torch.cat(vs).double().permute(1, 0, 2)                                            # [hkv, ctx, d]
+        sc = torch.matmul(q_h[b].view(hkv, rep, d), k) * scale                                 # [hkv, rep, ctx]
+        rl = torch.logsumexp(sc, dim=2)
+        ro = torch.matmul(torch.exp(sc - rl.unsqueeze(2)), v).reshape(hq, d)
+        for out, lse in results:
+            err_o = max(err_o, (out[b] - ro).abs().max().item())
+            err_l = max(err_l, (lse[b] - rl.reshape(hq)).abs().max().item())
     assert err_o <= OUT_TOL and err_l <= LSE_TOL, (err_o, err_l)
 
 
