@@ -9,10 +9,10 @@ the output rows) through ``hcp_ring_prefill_replay``, inputs resident in HBM.  `
 algorithmic FLOPs of causal pairs only: 2 GEMMs x 2 x D x Hq x S(S+1)/2.
 
 Also reported on the same line: paged decode GB/s (config c4) and the growth-sharded
-decode Q-ring at c4's shape, KV staging gather GB/s
-and the staged 128k prefill (config c5), the LSE merge GB/s, the c3 prefill with Striped
-and ZigZag positions, the KV wire-frame pack, the fused QKV + RoPE + KV append, fp32 on
-the matrix cores (c1 and an 8k block), a roofline object for the
+decode Q-ring at c4's shape, KV staging gather GB/s and the staged 128k prefill (config
+c5), the LSE merge GB/s, the c3 prefill with Striped and ZigZag positions, the KV
+wire-frame pack, the block-direct transport of a KV chunk, the fused QKV + RoPE + KV
+append, fp32 on the matrix cores (c1 and an 8k block), a roofline object for the
 dominant kernel (the flash block kernel, from HIP events recorded by the replay
 driver on its launch stream over the timed region) and the CPU baseline (the oracle's
 op-for-op libtorch restatement of ring.rs timed on this host on a bounded sample).
@@ -578,6 +578,47 @@ def bench_decode_ring(H, torch, steps: int, warmup: int):
     return res
 
 
+def bench_block_transport(H, torch, steps: int, warmup: int):
+    """The block-direct transport (block_transport.rs:36-126) moving one c3 domain-1 K/V
+    chunk (8192 tokens, 8 KV heads, D=128, bf16: K and V in one [2, 8, 8192, 128]
+    block, 32 MiB) between a linked agent pair on this GPU: per step one
+    submit_transfer (an async device copy) and host polls until the receiver reports
+    the completion.  GB/s counts the block's bytes once (the bytes on the wire)."""
+    src = torch.empty(2, 8, 8192, 128, dtype=torch.bfloat16, device="cuda")
+    H.synth_normals(C3["seed"] + 3, 0, src.numel(), src)
+    dst = torch.zeros_like(src)
+    sender, receiver = H.BlockAgent.pair("domain-0", "domain-1")
+    try:
+        dst_id, _ = receiver.register_block(dst)
+        src_id, _ = sender.register_block(src)
+        receiver.load_remote_metadata(sender.local_metadata())
+        sender.load_remote_metadata(receiver.local_metadata())
+        remote = sender.remote_desc("domain-1", dst_id)
+
+        def step():
+            sender.submit_transfer(src_id, remote)
+            while not receiver.poll_transfers():
+                pass
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        exact = bool(torch.equal(dst.view(torch.int16), src.view(torch.int16)))
+        sent, _ = sender.wire_bytes()
+    finally:
+        sender.destroy()
+        receiver.destroy()
+    nbytes = src.numel() * 2
+    return dict(workload="f3 block-direct transport: one c3 domain-1 K/V chunk (8192 tokens, 8 kv heads, D=128, "
+                         "bf16, 32 MiB) per step, submit_transfer + receiver polls until completion",
+                value=round(nbytes / (ms * 1e-3) / 1e9, 1), unit="GB/s", ms_per_step=round(ms, 4), bytes=nbytes,
+                bit_exact=exact, wire_bytes_sent=int(sent))
+
+
 # ------------------------------------------------------------------ c5 staging ----
 def bench_staged(H, torch, steps: int, warmup: int, full_prefill: bool = True):
     c = C5
@@ -752,7 +793,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="headline prefill only")
     ap.add_argument("--only-prefill", action="store_true", help="c3 prefill only, no CPU leg (profiling)")
     ap.add_argument("--leg", choices=["c2", "c3", "qwen64", "qwen64_32k", "strategies", "fp32", "merge", "staging",
-                                      "decode_ring"],
+                                      "decode_ring", "block_transport"],
                     default=None,
                     help="run one prefill leg alone and print its JSON object (profiling)")
     ap.add_argument("--trace", action="store_true",
@@ -790,6 +831,10 @@ def main():
         print(json.dumps({"leg": "merge", "value": round(m["merge_gbs"], 1), "unit": "GB/s",
                           "ms_per_step": round(m["merge_ms"], 4), "frac_hbm": round(m["merge_gbs"] / PEAK_HBM_GBS, 4),
                           "bytes": m["merge_bytes"]}), flush=True)
+        return
+    if args.leg == "block_transport":
+        print(json.dumps({"leg": "block_transport", **bench_block_transport(H, torch, args.steps, args.warmup)}),
+              flush=True)
         return
     if args.leg == "decode_ring":
         print(json.dumps({"leg": "decode_ring", **bench_decode_ring(H, torch, args.steps, args.warmup)}), flush=True)
@@ -900,6 +945,8 @@ def main():
         guarded(["strategies"], leg_strategies)
         guarded(["kv_frame"], leg_logged("kv_frame", lambda: bench_wire(H, torch, pre["tensors"], args.steps,
                                                                         args.warmup)))
+        guarded(["block_transport"], leg_logged("block_transport", lambda: bench_block_transport(H, torch, args.steps,
+                                                                                              args.warmup)))
         guarded(["qkv_rope"], leg_logged("qkv_rope", lambda: bench_qkv(H, torch, args.steps, args.warmup)))
         guarded(["fp32"], leg_logged("fp32", lambda: bench_fp32(H, torch, args.steps, args.warmup)))
     cpu = None
