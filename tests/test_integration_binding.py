@@ -1,8 +1,9 @@
-"""The reference-side Rust binding published in INTEGRATION.md stays locked to the C ABI.
+"""The reference-side Rust binding published with this library (the ``hip_ring.rs`` block
+of its integration notes, read from the repository root) stays locked to the C ABI.
 
 The reference binds native code through an ``extern "C"`` block
-(rust/src/smoke/bridges/cxx.rs:8-70).  INTEGRATION.md gives the block a maintainer adds
-for this library; it cannot be compiled here (no cargo), so this test parses it and
+(rust/src/smoke/bridges/cxx.rs:8-70).  The integration notes give the block a maintainer
+adds for this library; it cannot be compiled here (no cargo), so this test parses it and
 checks it against ``include/hcp_ring.h`` -- every ``#[repr(C)]`` struct field and every
 ``extern "C"`` function parameter, by name, order and type -- and checks the ctypes
 mirrors of the Python package against the header's struct layouts.  A field dropped,
