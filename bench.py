@@ -43,10 +43,8 @@ C4 = dict(batch=64, hq=32, hkv=8, d=128, bs=16, ctx=16384, chunks=[8192, 5120, 3
           pool_blocks=65536, seed=45)
 C5 = dict(chunks=[21504, 13312, 18432, 23552, 24576, 9216, 8192, 12288], hq=32, hkv=8, d=128,
           bs=16, seed=46)
-# The reference's own model (Qwen2-0.5B: 14 q / 2 kv heads, head dim 64,
-# docs/2domain_mps_hip_scale_matrix.md) on c3's 32k 4-domain split.
-# The reference's own model heads (Qwen2-0.5B: 14 q / 2 kv heads, head dim 64) on c2's
-# chunks and on c3's.
+# The reference's own model heads (Qwen2-0.5B: 14 q / 2 kv heads, head dim 64,
+# docs/2domain_mps_hip_scale_matrix.md) on c2's chunks and on c3's 32k 4-domain split.
 QWEN64 = dict(name="qwen2_0p5b_d64", chunks=[4096, 2560, 1536], hq=14, hkv=2, d=64, seed=47)
 QWEN64_32K = dict(name="qwen2_0p5b_d64_32k", chunks=[12288, 8192, 8192, 4096], hq=14, hkv=2, d=64, seed=47)
 
